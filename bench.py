@@ -1,0 +1,244 @@
+"""Benchmark of the MI355X PTQ hot path (BASELINE.json metric).
+
+Workload: every GPT-2-124M linear, INT8 W8A8, batch 8 x seq
+1024 (M = 8192), 12 layers; per layer qkv [768->2304], attn-out [768->768],
+MLP up [768->3072], MLP down [3072->768].  Weights ~N(0, 0.02) are
+calibrated per output channel and quantized once (offline PTQ); each step
+runs, for all 48 linears, the per-call path of the reference's quantized
+linear: per-tensor absmax calibration of the activation, int8 quantize,
+INT8 GEMM with INT32 accumulate and the fused dequant + bias epilogue to
+f32.  Activations ~N(0, 1), bias ~N(0, 0.01), synthetic (LCG31 +
+Box-Muller, tv/training/gpt2_ref.tkv:1977-1991); every linear has its own
+input and output buffer in HBM (5 GB working set, far beyond the 256 MB
+Infinity Cache), all resident before timing.
+
+`value` = GEMM ops of the step (2*M*N*K summed, 1.3916e12) / step time.
+The JSON line also carries the INT8 GEMM kernel's roofline (achieved from
+HIP events around every GEMM launch in the timed region), the config-2
+quantize / calibrate bandwidths, and the CPU baseline (the oracle's scalar
+restatement of the reference loops, on a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+M = 8192
+LAYERS = 12
+SHAPES = [("qkv", 2304, 768), ("attn_out", 768, 768), ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)]
+PEAK_INT8_TOPS = 5000.0      # MI355X dense INT8 MFMA
+PEAK_HBM_GBPS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemm_bytes(m, n, k):
+    return m * k + n * k + 8 * n + 4 * m * n
+
+
+def run_gpu(steps, warmup):
+    import oracle as O
+    from tokenvector.inference_amd import _lib
+    from tokenvector.inference_amd import device as D
+
+    if _lib.lib().tkv_hip_device_count() < 1:
+        raise SystemExit("bench.py: no gfx950 device visible")
+    ctx = D.Context(0)
+
+    # ---- inputs (generated on the host once, resident in HBM) ----
+    t0 = time.time()
+    x_host = {768: O.gi_noise(M * 768, 0, 1.0), 3072: O.gi_noise(M * 3072, 7, 1.0)}
+    layers = []
+    for l in range(LAYERS):
+        lin = []
+        for j, (name, n, k) in enumerate(SHAPES):
+            w = O.gi_noise(n * k, 10 + 100 * l + j + 1, 0.02)
+            b = O.gi_noise(n, 10 + 100 * l + j + 51, 0.01)
+            dw = D.DeviceBuffer.from_host(ctx, w)
+            db = D.DeviceBuffer.from_host(ctx, b)
+            q = D.QuantizedLinear.from_float(ctx, dw, n, k, db, D.WEIGHT_INT8)
+            dw.close()
+            dx = D.DeviceBuffer.from_host(ctx, x_host[k])
+            dy = D.DeviceBuffer.empty(ctx, (M, n), np.float32)
+            qa = D.DeviceBuffer.empty(ctx, (M, k), np.int8)
+            lin.append((name, n, k, q, dx, dy, qa, db))
+        layers.append(lin)
+    params = [D.params_buffer(ctx) for _ in range(4)]
+    ctx.synchronize()
+    log(f"inputs ready in {time.time() - t0:.1f}s")
+
+    ops_step = sum(2.0 * M * n * k for (_, n, k) in SHAPES) * LAYERS
+    n_gemm = LAYERS * len(SHAPES)
+    ev_pairs = [(D.Event(), D.Event()) for _ in range(n_gemm * steps)]
+
+    def step(record=None):
+        i = 0
+        for lin in layers:
+            for j, (name, n, k, q, dx, dy, qa, db) in enumerate(lin):
+                p = params[j]
+                # calibrate_minmax + quantize_int8_symmetric (device, no sync)
+                D.quantize_int8_dynamic_tensor(ctx, dx, M * k, qa, p)
+                if record is not None:
+                    record[i][0].record(ctx)
+                # INT8 GEMM + dequant (scale_a from the calibration) + bias
+                D.matmul_int8(ctx, qa, q.codes, M, n, k, p.ptr, 0, 0.0, q.scales, q.bias, dy)
+                if record is not None:
+                    record[i][1].record(ctx)
+                i += 1
+
+    for _ in range(warmup):
+        step()
+    ctx.synchronize()
+    t_start = time.perf_counter()
+    for s in range(steps):
+        step(ev_pairs[s * n_gemm:(s + 1) * n_gemm])
+    ctx.synchronize()
+    t_end = time.perf_counter()
+    ms_per_step = (t_end - t_start) * 1000.0 / steps
+    gemm_ms = [a.elapsed_ms(b) for (a, b) in ev_pairs]
+    avg_gemm_ms = float(np.mean(gemm_ms))
+    ops_per_launch = ops_step / n_gemm
+    achieved_tops = ops_per_launch / (avg_gemm_ms * 1e-3) / 1e12
+    per_shape = {}
+    for j, (name, n, k) in enumerate(SHAPES):
+        t = [gemm_ms[s * n_gemm + l * 4 + j] for s in range(steps) for l in range(LAYERS)]
+        tm = float(np.mean(t))
+        ops = 2.0 * M * n * k
+        ceil = min(PEAK_INT8_TOPS, ops / gemm_bytes(M, n, k) * PEAK_HBM_GBPS * 1e9 / 1e12)
+        per_shape[name] = {"us": round(tm * 1e3, 2), "tops": round(ops / (tm * 1e-3) / 1e12, 1),
+                           "ceiling_tops": round(ceil, 1),
+                           "frac_of_ceiling": round(ops / (tm * 1e-3) / 1e12 / ceil, 3)}
+
+    # ---- config 2: quantize / calibrate bandwidth at M = 65536 x 768 ----
+    quant = bench_quant(ctx, D, O)
+    ctx.close()
+    return {
+        "ms_per_step": ms_per_step,
+        "value": ops_step / (ms_per_step * 1e-3) / 1e12,
+        "gemm": {"avg_launch_us": avg_gemm_ms * 1e3, "achieved_tops": achieved_tops,
+                 "launches_timed": len(gemm_ms), "per_shape": per_shape},
+        "quant": quant,
+        "ops_per_step": ops_step,
+    }
+
+
+def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
+    n = m * cols
+    x = O.add_outliers(O.gi_noise(n, 0, 1.0), 0.001, 3, 4, 20.0)
+    # distinct buffers per repetition keep the Infinity Cache cold
+    nbuf = 4
+    xs = [D.DeviceBuffer.from_host(ctx, x) for _ in range(nbuf)]
+    q8 = D.DeviceBuffer.empty(ctx, n, np.int8)
+    p = D.params_buffer(ctx)
+    sc = D.DeviceBuffer.empty(ctx, m, np.float32)
+    out = {}
+
+    def timeit(fn, nbytes):
+        for i in range(3):
+            fn(xs[i % nbuf])
+        e0, e1 = D.Event(), D.Event()
+        ctx.synchronize()
+        e0.record(ctx)
+        for i in range(reps):
+            fn(xs[i % nbuf])
+        e1.record(ctx)
+        ms = e0.elapsed_ms(e1) / reps
+        return {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac_of_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 3)}
+
+    out["calibrate_absmax"] = timeit(lambda xb: D.calibrate_minmax(ctx, xb, n, 1, p), 4 * n)
+    D.calibrate_minmax(ctx, xs[0], n, 1, p)
+    out["quantize_int8"] = timeit(lambda xb: D.quantize_int8_tensor(ctx, xb, n, p, q8), 5 * n)
+    out["calibrate_quantize_int8"] = timeit(
+        lambda xb: D.quantize_int8_dynamic_tensor(ctx, xb, n, q8, p), 9 * n)
+    out["quantize_rowwise_int8"] = timeit(
+        lambda xb: D.quantize_dynamic_int8_rowwise(ctx, xb, m, cols, q8, sc), 5 * n + 4 * m)
+    out["quantize_fp8"] = timeit(lambda xb: D.quantize_fp8_e4m3(ctx, xb, n, q8), 5 * n)
+    out["config"] = f"M={m} x {cols} f32 (config 2, largest)"
+    for b in xs:
+        b.close()
+    return out
+
+
+def cpu_baseline(rows=2048):
+    """The oracle's scalar restatement of the reference loops (one thread),
+    on a bounded sample of the same workload: `rows` activation rows of each
+    of the four linear shapes (calibrate + quantize + INT8 GEMM + epilogue)."""
+    import oracle as O
+    t_total, ops = 0.0, 0.0
+    for j, (name, n, k) in enumerate(SHAPES):
+        x = O.gi_noise(rows * k, 0, 1.0)
+        w = O.gi_noise(n * k, 11 + j, 0.02)
+        b = O.gi_noise(n, 61 + j, 0.01)
+        sw = np.array([p.scale for p in O.calibrate_per_channel_minmax(w, n, k)], np.float32)
+        wq = O.quantize_int8_per_channel(w, n, k, sw)
+        t0 = time.perf_counter()
+        p = O.calibrate_minmax(x, 1)
+        xq = O.quantize_int8_symmetric(x, p.scale)
+        O.matmul_int8_per_channel(xq, wq, b, rows, n, k, p.scale, sw)
+        t_total += time.perf_counter() - t0
+        ops += 2.0 * rows * n * k
+    return {"value": round(ops / t_total / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"{rows} of 8192 activation rows of each GPT-2 linear shape "
+                      f"(one layer: calibrate + quantize + INT8 GEMM + dequant), "
+                      f"{ops / 1e9:.1f} GOP in {t_total:.1f} s; oracle/tkv_oracle.c -O2, 1 thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=2048)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        sys.exit(2)
+
+    r = run_gpu(args.steps, args.warmup)
+    gemm = r["gemm"]
+    line = {
+        "metric": "INT8/FP8 GEMM TOPS + quantize GB/s (% of roofline) on GPT-2-124M linears",
+        "value": round(r["value"], 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (LCG31 + Box-Muller, seeds per SURVEY 8d; random-init GPT-2 shapes)",
+        "config": {"workload": "configs[2]: all GPT-2-124M linears W8A8, M=8192, 12 layers "
+                               "(per step: 48 x [absmax calibrate + int8 quantize + INT8 GEMM + "
+                               "dequant/bias epilogue])",
+                   "M": M, "layers": LAYERS, "shapes_NK": [[n, k] for (_, n, k) in SHAPES],
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(gemm["achieved_tops"], 1),
+                     "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm["achieved_tops"] / PEAK_INT8_TOPS, 4),
+                     "traffic": None,
+                     "kernel": "k_gemm_i8 (INT8 MFMA GEMM + fused dequant epilogue)",
+                     "avg_launch_us": round(gemm["avg_launch_us"], 2),
+                     "per_shape": gemm["per_shape"]},
+        "quantize": r["quant"],
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

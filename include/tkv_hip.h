@@ -1,0 +1,282 @@
+/*
+ * tkv_hip.h -- C ABI of libtkv_hip, the MI355X (gfx950) implementation of
+ * TokenVector.Inference's post-training-quantization hot path.
+ *
+ * The reference (.tkv compiled to .NET IL) reaches native code only through
+ * compiler builtins that P/Invoke a C export taking the backing arrays of
+ * List<T> plus int64 sizes and returning an int32 rc
+ * (docs/HANDOFF.md:1616,1643,2009,2563; the simd_gemm_* family).  This
+ * library follows that convention:
+ *
+ *   - every entry point is extern "C", takes plain pointers and int64 sizes,
+ *     and returns an int32 rc (TKV_HIP_OK or a negative code below);
+ *   - on rc < 0 the caller runs its original .tkv loop (docs/HANDOFF.md:3649);
+ *   - the caller owns every buffer; nothing is retained after return except
+ *     through an explicit handle (context, weight) with create/destroy, as
+ *     simd_gemm_packed_create/free do (docs/HANDOFF.md:1675);
+ *   - entry points are re-entrant: state lives in contexts, never in
+ *     process-wide mutable globals (the shared g_job of simd_gemm hung two
+ *     callers, docs/COMPILER_TEAM_REQUEST2.md:46,91).
+ *
+ * Two families:
+ *   tkv_hip_<fn>       host-pointer mirrors of the .tkv functions, with the
+ *                      same argument order and meaning; codes are int32 per
+ *                      element (List<int>), as the reference stores them.
+ *   tkv_hip_dev_<fn>   device-pointer variants on packed codes (int8 for INT8,
+ *                      raw e4m3 bytes for FP8) that run asynchronously on the
+ *                      context's stream.
+ *
+ * Citations are path:line inside the reference checkout.
+ */
+#ifndef TKV_HIP_H
+#define TKV_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- return codes ----------------------------------------------------- */
+#define TKV_HIP_OK 0
+#define TKV_HIP_UNSUPPORTED (-1) /* shape / layout not handled: fall back      */
+#define TKV_HIP_NO_DEVICE (-2)   /* no usable gfx950 device                      */
+#define TKV_HIP_OOM (-3)         /* device or pinned allocation failed           */
+#define TKV_HIP_BAD_ARG (-4)     /* the cases where the .tkv raises ValueError   */
+#define TKV_HIP_DEVICE_ERROR (-5)/* HIP runtime error (message in last_error)    */
+
+/* Numeric recipe switches: typing the reference compiler leaves unpinned
+ * (f32 vs f64 reciprocal in quantize_int8_symmetric, f64 vs f32 epilogue
+ * chain in the INT8 GEMMs).  PRIMARY follows the IL typing rules of
+ * docs/HANDOFF.md:1994-1999,3645,3663,3994-3997. */
+#define TKV_HIP_RECIPE_PRIMARY 0
+#define TKV_HIP_RECIPE_ALTERNATE 1
+
+/* Per-tensor quantization parameters as kept in device memory, so that a
+ * calibration can feed a quantize / GEMM without a host round trip.
+ * scale/zero_point/min_val/max_val are the QuantParams fields
+ * (tv/quantization/types.tkv:17-27); inv is the reciprocal the reference's
+ * quantize loop multiplies by (f64). */
+typedef struct {
+    float scale;
+    float min_val;
+    float max_val;
+    int32_t zero_point;
+    double inv;
+    double reserved;
+} tkv_hip_qparams_dev;
+
+/* ---- library / context -------------------------------------------------- */
+/* No reference counterpart: library plumbing. */
+int32_t tkv_hip_version(void);
+/* Number of visible gfx950 devices (0 if none). */
+int32_t tkv_hip_device_count(void);
+/* Copies the calling thread's last error message; returns its length. */
+int32_t tkv_hip_last_error(char* buf, int32_t len);
+/* A context owns a HIP stream (or borrows the caller's) and a grow-only
+ * device workspace.  Handles are int64 as the .tkv builtins pass them. */
+int32_t tkv_hip_ctx_create(int32_t device, int64_t* ctx_out);
+int32_t tkv_hip_ctx_destroy(int64_t ctx);
+/* Use an external hipStream_t (e.g. torch's) for subsequent dev calls;
+ * NULL restores the context's own stream. */
+int32_t tkv_hip_ctx_set_stream(int64_t ctx, void* stream);
+int32_t tkv_hip_ctx_get_stream(int64_t ctx, void** stream_out);
+int32_t tkv_hip_ctx_synchronize(int64_t ctx);
+/* Device memory and copies for callers without their own allocator (tests,
+ * the .NET side).  Copies are ordered on the context's stream. */
+int32_t tkv_hip_malloc(int64_t ctx, int64_t bytes, void** ptr_out);
+int32_t tkv_hip_free(int64_t ctx, void* ptr);
+int32_t tkv_hip_memcpy_h2d(int64_t ctx, void* dst, const void* src, int64_t bytes);
+int32_t tkv_hip_memcpy_d2h(int64_t ctx, void* dst, const void* src, int64_t bytes);
+int32_t tkv_hip_memset(int64_t ctx, void* dst, int32_t value, int64_t bytes);
+/* Stream-ordered event timing (bench harness). */
+int32_t tkv_hip_event_create(int64_t* ev_out);
+int32_t tkv_hip_event_destroy(int64_t ev);
+int32_t tkv_hip_event_record(int64_t ctx, int64_t ev);
+int32_t tkv_hip_event_elapsed_ms(int64_t ev_start, int64_t ev_end, float* ms_out);
+
+/* ======================================================================== */
+/* Host-pointer mirrors (one per .tkv function).  ctx-free: each calling    */
+/* thread uses its own default context on device 0.                         */
+/* ======================================================================== */
+
+/* calibrate_minmax(data, symmetric) -> QuantParams   engine.tkv:13-36 */
+int32_t tkv_hip_calibrate_minmax(const float* data, int64_t n, int32_t symmetric,
+                                 float* scale, int64_t* zero_point, float* min_val,
+                                 float* max_val);
+/* calibrate_per_channel_minmax(data, rows, cols, symmetric) engine.tkv:202-213;
+ * outputs one QuantParams per row as four arrays (zero_points/min/max may be
+ * NULL).  BAD_ARG where the .tkv raises (rows/cols <= 0, short data). */
+int32_t tkv_hip_calibrate_per_channel_minmax(const float* data, int64_t n_data,
+                                             int64_t rows, int64_t cols, int32_t symmetric,
+                                             float* scales, int64_t* zero_points,
+                                             float* min_vals, float* max_vals);
+/* quantize_int8_symmetric(src, dst, scale)            engine.tkv:216-226 */
+int32_t tkv_hip_quantize_int8_symmetric(const float* src, int64_t n_src, int32_t* dst,
+                                        int64_t n_dst, float scale);
+int32_t tkv_hip_quantize_int8_symmetric_recipe(const float* src, int64_t n_src,
+                                               int32_t* dst, int64_t n_dst, float scale,
+                                               int32_t recipe);
+/* dequantize_int8_symmetric(src, dst, scale)          engine.tkv:229-234 */
+int32_t tkv_hip_dequantize_int8_symmetric(const int32_t* src, int64_t n_src, float* dst,
+                                          int64_t n_dst, float scale);
+/* quantize_int8_per_channel(src, dst, rows, cols, scales) engine.tkv:237-250 */
+int32_t tkv_hip_quantize_int8_per_channel(const float* src, int64_t n_src, int32_t* dst,
+                                          int64_t n_dst, int64_t rows, int64_t cols,
+                                          const float* scales, int64_t n_scales);
+/* dequantize_int8_per_channel(...)                    engine.tkv:253-262 */
+int32_t tkv_hip_dequantize_int8_per_channel(const int32_t* src, int64_t n_src, float* dst,
+                                            int64_t n_dst, int64_t rows, int64_t cols,
+                                            const float* scales, int64_t n_scales);
+/* quantize_dynamic_int8_rowwise(src, dst, rows, cols, scales_out) engine.tkv:266-285 */
+int32_t tkv_hip_quantize_dynamic_int8_rowwise(const float* src, int64_t n_src, int32_t* dst,
+                                              int64_t n_dst, int64_t rows, int64_t cols,
+                                              float* scales_out, int64_t n_scales_out);
+/* quantize_fp8_e4m3(src, dst): dst = e4m3 byte - 128    matmul.tkv:60-66 */
+int32_t tkv_hip_quantize_fp8_e4m3(const float* src, int64_t n_src, int32_t* dst,
+                                  int64_t n_dst);
+/* dequantize_fp8_e4m3(src, dst)                         matmul.tkv:68-73 */
+int32_t tkv_hip_dequantize_fp8_e4m3(const int32_t* src, int64_t n_src, float* dst,
+                                    int64_t n_dst);
+/* matmul_int8_symmetric(pa, pw, pbias, py, m, n, k, scale_a, scale_w) matmul.tkv:4-15.
+ * n_bias == 0 means no bias (len(pbias) == 0). */
+int32_t tkv_hip_matmul_int8_symmetric(const int32_t* pa, const int32_t* pw,
+                                      const float* pbias, int64_t n_bias, float* py,
+                                      int64_t m, int64_t n, int64_t k, float scale_a,
+                                      float scale_w);
+/* matmul_int8_per_channel(pa, pw, pbias, py, m, n, k, scale_a, scales_w) matmul.tkv:17-29;
+ * BAD_ARG when n_scales < n (matmul.tkv:18-19). */
+int32_t tkv_hip_matmul_int8_per_channel(const int32_t* pa, const int32_t* pw,
+                                        const float* pbias, int64_t n_bias, float* py,
+                                        int64_t m, int64_t n, int64_t k, float scale_a,
+                                        const float* scales_w, int64_t n_scales);
+/* Same two GEMMs with the epilogue recipe selectable. */
+int32_t tkv_hip_matmul_int8_recipe(const int32_t* pa, const int32_t* pw, const float* pbias,
+                                   int64_t n_bias, float* py, int64_t m, int64_t n,
+                                   int64_t k, float scale_a, float scale_w,
+                                   const float* scales_w, int64_t n_scales, int32_t recipe);
+/* The INT32 accumulators of the INT8 GEMM (matmul.tkv:116-127 per output). */
+int32_t tkv_hip_matmul_int8_accum(const int32_t* pa, const int32_t* pw, int32_t* acc,
+                                  int64_t m, int64_t n, int64_t k);
+/* matmul_fp8_e4m3(pa, pw, pbias, py, m, n, k)           matmul.tkv:46-58 */
+int32_t tkv_hip_matmul_fp8_e4m3(const int32_t* pa, const int32_t* pw, const float* pbias,
+                                int64_t n_bias, float* py, int64_t m, int64_t n,
+                                int64_t k);
+/* QuantizedGemm node (session.tkv:678-697): per-channel iff n_scales > 0,
+ * else symmetric with (scale_a, scale_b); M, K from A's shape, N from W's. */
+int32_t tkv_hip_quantized_gemm(const int32_t* aq, const int32_t* wq, const float* bias,
+                               int64_t n_bias, float* y, int64_t m, int64_t n, int64_t k,
+                               float scale_a, float scale_b, const float* scales_w,
+                               int64_t n_scales);
+/* MatMulInteger node (session.tkv:2789-2851): Y[M,N] int64 = A[M,K] . B[K,N]
+ * with B row-major [K,N]; reads past na/nb are 0, writes past ny dropped. */
+int32_t tkv_hip_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, int64_t nb,
+                               int64_t* y, int64_t ny, int64_t m, int64_t n, int64_t k);
+/* QuantizeLinear node (session.tkv:1896-1953): n_scales == 1 per-tensor, else
+ * per-axis over the [outer, dim, inner] view of x. */
+int32_t tkv_hip_quantize_linear(const float* x, int64_t nx, const float* scales,
+                                int64_t n_scales, int64_t zero_point, int64_t outer,
+                                int64_t dim, int64_t inner, int32_t* y);
+/* DequantizeLinear node (session.tkv:1955-1990) */
+int32_t tkv_hip_dequantize_linear(const int32_t* x, int64_t nx, const float* scales,
+                                  int64_t n_scales, int64_t zero_point, int64_t outer,
+                                  int64_t dim, int64_t inner, float* y);
+/* DynamicQuantizeLinear node (session.tkv:2853-2901) */
+int32_t tkv_hip_dynamic_quantize_linear(const float* x, int64_t nx, int32_t* y,
+                                        float* y_scale, float* y_zero_point);
+
+/* ======================================================================== */
+/* Device-pointer variants (asynchronous on the context's stream).          */
+/* ctx == 0 selects the calling thread's default context.                   */
+/* ======================================================================== */
+
+/* calibrate_minmax on device data; writes one tkv_hip_qparams_dev.
+ * engine.tkv:13-36 */
+int32_t tkv_hip_dev_calibrate_minmax(int64_t ctx, const float* x, int64_t n,
+                                     int32_t symmetric, tkv_hip_qparams_dev* params);
+/* Per-row absmax scales (symmetric calibrate_per_channel_minmax, engine.tkv:202-213):
+ * scales[r] = fl32(max(|x[r,:]|, 1e-8) / 127). */
+int32_t tkv_hip_dev_calibrate_rows(int64_t ctx, const float* x, int64_t rows, int64_t cols,
+                                   float* scales);
+/* quantize_int8_symmetric with the scale read from params (device), so it
+ * can follow tkv_hip_dev_calibrate_minmax without a sync.  engine.tkv:216-226 */
+int32_t tkv_hip_dev_quantize_int8_tensor(int64_t ctx, const float* x, int64_t n,
+                                         const tkv_hip_qparams_dev* params, int8_t* q);
+/* calibrate_minmax(x, 1) + quantize_int8_symmetric(x, q, p.scale) fused:
+ * the activation path of a W8A8 linear (two kernels, no host sync). */
+int32_t tkv_hip_dev_quantize_int8_dynamic_tensor(int64_t ctx, const float* x, int64_t n,
+                                                 int8_t* q, tkv_hip_qparams_dev* params);
+/* quantize_int8_per_channel with device scales.  engine.tkv:237-250 */
+int32_t tkv_hip_dev_quantize_int8_per_channel(int64_t ctx, const float* x, int64_t rows,
+                                              int64_t cols, const float* scales, int8_t* q);
+/* quantize_dynamic_int8_rowwise, one pass per row.  engine.tkv:266-285 */
+int32_t tkv_hip_dev_quantize_dynamic_int8_rowwise(int64_t ctx, const float* x,
+                                                  int64_t rows, int64_t cols, int8_t* q,
+                                                  float* scales_out);
+/* dequantize_int8_symmetric / _per_channel (scales == NULL -> per-tensor
+ * `scale`).  engine.tkv:229-234,253-262 */
+int32_t tkv_hip_dev_dequantize_int8(int64_t ctx, const int8_t* q, int64_t rows, int64_t cols,
+                                    float scale, const float* scales, float* y);
+/* quantize_fp8_e4m3: raw e4m3 bytes (the reference's code + 128).
+ * matmul.tkv:60-66 */
+int32_t tkv_hip_dev_quantize_fp8_e4m3(int64_t ctx, const float* x, int64_t n, uint8_t* q);
+/* Extension for per-tensor-scaled FP8 (not in the reference): bytes of
+ * encode(fl32(x * fl32(1 / scale))), scale read from params. */
+int32_t tkv_hip_dev_quantize_fp8_e4m3_scaled(int64_t ctx, const float* x, int64_t n,
+                                             const tkv_hip_qparams_dev* params, uint8_t* q);
+/* dequantize_fp8_e4m3 (reference decoder).  matmul.tkv:68-73 */
+int32_t tkv_hip_dev_dequantize_fp8_e4m3(int64_t ctx, const uint8_t* q, int64_t n, float* y);
+
+/* INT8 GEMM: A int8 [M,K] row-major, W int8 [N,K] row-major (both K-major,
+ * matmul.tkv:22), INT32 accumulate, fused dequant epilogue, f32 Y [M,N].
+ * Epilogue (matmul.tkv:14,28):
+ *   scales_w != NULL: y = acc * sa * scales_w[n] + bias[n]   (per-channel)
+ *   scales_w == NULL: y = acc * fl32(sa * scale_w) + bias[n] (symmetric)
+ * sa = scale_a[m * scale_a_stride]: stride 0 per-tensor, 1 per-token (the
+ * per-token form is an extension).  bias may be NULL. */
+int32_t tkv_hip_dev_matmul_int8(int64_t ctx, const int8_t* a, const int8_t* w, int64_t m,
+                                int64_t n, int64_t k, const float* scale_a,
+                                int64_t scale_a_stride, float scale_w,
+                                const float* scales_w, const float* bias, float* y,
+                                int32_t recipe);
+/* INT32 accumulators only (MatMulInteger core; exactness checks). */
+int32_t tkv_hip_dev_matmul_int8_accum(int64_t ctx, const int8_t* a, const int8_t* w,
+                                      int64_t m, int64_t n, int64_t k, int32_t* acc);
+/* FP8 e4m3 GEMM: raw e4m3 bytes A [M,K], W [N,K]; f32 accumulate;
+ * y = fl32(acc + bias[n]) (matmul.tkv:46-58).  With scale_a / scales_w
+ * non-NULL the extension epilogue y = acc * sa * scales_w[n] + bias[n]. */
+int32_t tkv_hip_dev_matmul_fp8_e4m3(int64_t ctx, const uint8_t* a, const uint8_t* w,
+                                    int64_t m, int64_t n, int64_t k, const float* scale_a,
+                                    int64_t scale_a_stride, const float* scales_w,
+                                    const float* bias, float* y);
+
+/* ---- device-resident quantized weight (pack once, run many) ------------ */
+/* Calibrates W f32 [N,K] (device pointer) per output channel and quantizes
+ * it to int8 (format 0) or per-tensor-scaled e4m3 (format 1), keeping codes,
+ * scales and an optional bias on the device.  Mirrors the offline
+ * calibrate_per_channel_minmax + quantize_int8_per_channel steps of CS1. */
+#define TKV_HIP_WEIGHT_INT8 0
+#define TKV_HIP_WEIGHT_FP8 1
+int32_t tkv_hip_weight_create(int64_t ctx, const float* w, int64_t n, int64_t k,
+                              const float* bias, int32_t format, int64_t* handle_out);
+/* Pre-quantized int8 weight codes [N,K] + per-channel scales (device). */
+int32_t tkv_hip_weight_create_int8(int64_t ctx, const int8_t* codes, const float* scales,
+                                   int64_t n, int64_t k, const float* bias,
+                                   int64_t* handle_out);
+int32_t tkv_hip_weight_free(int64_t handle);
+/* Read back the weight's codes / scales (device pointers owned by the handle). */
+int32_t tkv_hip_weight_info(int64_t handle, void** codes, float** scales, float** bias,
+                            int64_t* n, int64_t* k, int32_t* format);
+/* Quantized linear: y[M,N] = dequant(quant(x) . W^T) + bias.
+ * act_mode 0: dynamic per-tensor activation scale (calibrate_minmax + R3);
+ * act_mode 1: dynamic per-token scale (quantize_dynamic_int8_rowwise).
+ * x, y are device pointers; the activation codes live in ctx workspace. */
+#define TKV_HIP_ACT_PER_TENSOR 0
+#define TKV_HIP_ACT_PER_TOKEN 1
+int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int64_t m,
+                               int32_t act_mode, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,377 @@
+"""CPU oracle for the PTQ path -- TEST INFRASTRUCTURE ONLY.
+
+numpy wrappers over ``libtkv_oracle.so`` (the C restatement in
+``tkv_oracle.c``).  Only tests, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker or the timed CPU baseline -- never as the product path.
+
+Each wrapper restates the reference function named in its docstring
+(paths relative to the reference checkout).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from typing import NamedTuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libtkv_oracle.so")
+
+PRIMARY = 0
+ALTERNATE = 1
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class _QP(C.Structure):
+    _fields_ = [("scale", C.c_float), ("zero_point", C.c_int64),
+                ("min_val", C.c_float), ("max_val", C.c_float)]
+
+
+class QuantParams(NamedTuple):
+    """QuantParams record (tv/quantization/types.tkv:17-27)."""
+    scale: float
+    zero_point: int
+    min_val: float
+    max_val: float
+
+    @staticmethod
+    def _from(qp: _QP) -> "QuantParams":
+        return QuantParams(np.float32(qp.scale), int(qp.zero_point),
+                           np.float32(qp.min_val), np.float32(qp.max_val))
+
+
+P = C.c_void_p
+I64 = C.c_int64
+I32 = C.c_int32
+F32 = C.c_float
+F64 = C.c_double
+
+
+def _declare(L: C.CDLL) -> None:
+    sig = {
+        "tkvo_f64_to_f32_bits": (I64, [F64]),
+        "tkvo_f32_bits_to_f64": (F64, [I64]),
+        "tkvo_rne_rshift": (I64, [I64, I64]),
+        "tkvo_fp8_e4m3_encode": (I64, [F32]),
+        "tkvo_fp8_e4m3_decode": (F32, [I64]),
+        "tkvo_fp8_e5m2_encode": (I64, [F32]),
+        "tkvo_fp8_e5m2_decode": (F32, [I64]),
+        "tkvo_quant_identity": (_QP, []),
+        "tkvo_calibrate_minmax": (_QP, [P, I64, I32]),
+        "tkvo_calibrate_per_channel_minmax": (I32, [P, I64, I64, I64, I32, P]),
+        "tkvo_quantize_int8_symmetric": (I32, [P, I64, P, F32, I32]),
+        "tkvo_dequantize_int8_symmetric": (I32, [P, I64, P, F32]),
+        "tkvo_quantize_int8_per_channel": (I32, [P, P, I64, I64, P]),
+        "tkvo_dequantize_int8_per_channel": (I32, [P, P, I64, I64, P]),
+        "tkvo_quantize_dynamic_int8_rowwise": (I32, [P, P, I64, I64, P]),
+        "tkvo_dot_int8": (I64, [P, I64, P, I64, I64]),
+        "tkvo_matmul_int8_symmetric": (I32, [P, P, P, I64, P, I64, I64, I64, F32, F32, I32]),
+        "tkvo_matmul_int8_per_channel": (I32, [P, P, P, I64, P, I64, I64, I64, F32, P, I64, I32]),
+        "tkvo_matmul_int8_per_channel_mt": (I32, [P, P, P, I64, P, I64, I64, I64, F32, P, I64, I32]),
+        "tkvo_matmul_int8_accum": (I32, [P, P, P, I64, I64, I64]),
+        "tkvo_quantize_fp8_e4m3": (I32, [P, I64, P]),
+        "tkvo_dequantize_fp8_e4m3": (I32, [P, I64, P]),
+        "tkvo_matmul_fp8_e4m3": (I32, [P, P, P, I64, P, I64, I64, I64]),
+        "tkvo_matmul_fp8_e4m3_exact": (I32, [P, P, P, P, I64, I64, I64]),
+        "tkvo_matmul_integer": (I32, [P, I64, P, I64, P, I64, I64, I64, I64]),
+        "tkvo_quantize_linear": (I32, [P, I64, P, I64, I64, I64, I64, I64, P]),
+        "tkvo_dequantize_linear": (I32, [P, I64, P, I64, I64, I64, I64, I64, P]),
+        "tkvo_dynamic_quantize_linear": (I32, [P, I64, P, P, P]),
+        "tkvo_quantized_gemm_node": (I32, [P, P, P, I64, P, I64, I64, I64, F32, F32, P, I64, I32]),
+        "tkvo_lcg31": (I64, [I64]),
+        "tkvo_gi_noise": (None, [P, I64, I64, F64]),
+        "tkvo_add_outliers": (None, [P, I64, I64, I64, I64, F64]),
+        "tkvo_pin_e4m3_spec_encode": (I64, [F32]),
+        "tkvo_fp8_e4m3_encode_bits": (I32, [P, I64, P, I32]),
+        "tkvo_pin_e4m3_exhaustive": (I64, [I32, I32, I32, C.POINTER(C.c_uint32)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def _i32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.int32)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---- generator (tv/training/gpt2_ref.tkv:1977-1991) ----------------------
+
+def gi_noise(n: int, seed: int, sigma: float) -> np.ndarray:
+    out = np.empty(int(n), dtype=np.float32)
+    lib().tkvo_gi_noise(_p(out), int(n), int(seed), float(sigma))
+    return out
+
+
+def add_outliers(x: np.ndarray, frac: float, seed: int, seed2: int, sigma: float) -> np.ndarray:
+    x = _f32(x).copy()
+    n_out = int(round(x.size * frac))
+    lib().tkvo_add_outliers(_p(x), x.size, n_out, int(seed), int(seed2), float(sigma))
+    return x
+
+
+# ---- f32_bits.tkv / types.tkv ---------------------------------------------
+
+def f64_to_f32_bits(x: float) -> int:
+    return int(lib().tkvo_f64_to_f32_bits(float(x)))
+
+
+def f32_bits_to_f64(b: int) -> float:
+    return float(lib().tkvo_f32_bits_to_f64(int(b)))
+
+
+def rne_rshift(v: int, s: int) -> int:
+    return int(lib().tkvo_rne_rshift(int(v), int(s)))
+
+
+def fp8_e4m3_encode(x: float) -> int:
+    return int(lib().tkvo_fp8_e4m3_encode(float(np.float32(x))))
+
+
+def fp8_e4m3_decode(v: int) -> np.float32:
+    return np.float32(lib().tkvo_fp8_e4m3_decode(int(v)))
+
+
+def fp8_e5m2_encode(x: float) -> int:
+    return int(lib().tkvo_fp8_e5m2_encode(float(np.float32(x))))
+
+
+def fp8_e5m2_decode(v: int) -> np.float32:
+    return np.float32(lib().tkvo_fp8_e5m2_decode(int(v)))
+
+
+def host_threads() -> int:
+    """Worker count for threaded oracle helpers: the host's cores, at most 16
+    (the CPU share of one GPU on the MI355X boxes)."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def fp8_encode_bits(bits: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """fp8_e4m3_encode of every f32 bit pattern in `bits` (uint32)."""
+    b = np.ascontiguousarray(bits, dtype=np.uint32)
+    out = np.empty(b.size, np.uint8)
+    lib().tkvo_fp8_e4m3_encode_bits(_p(b), b.size, _p(out), int(nthreads or host_threads()))
+    return out
+
+
+def spec_e4m3_encode(x: float) -> int:
+    return int(lib().tkvo_pin_e4m3_spec_encode(float(np.float32(x))))
+
+
+def e4m3_exhaustive(elo: int, ehi: int, nthreads: int = 0):
+    bad = C.c_uint32(0)
+    n = lib().tkvo_pin_e4m3_exhaustive(int(elo), int(ehi), int(nthreads), C.byref(bad))
+    return int(n), int(bad.value)
+
+
+# ---- engine.tkv ------------------------------------------------------------
+
+def quant_identity() -> QuantParams:
+    return QuantParams._from(lib().tkvo_quant_identity())
+
+
+def calibrate_minmax(data, symmetric: int = 1) -> QuantParams:
+    x = _f32(data)
+    return QuantParams._from(lib().tkvo_calibrate_minmax(_p(x), x.size, int(symmetric)))
+
+
+def calibrate_per_channel_minmax(data, rows: int, cols: int, symmetric: int = 1):
+    x = _f32(data)
+    out = (_QP * max(int(rows), 1))()
+    rc = lib().tkvo_calibrate_per_channel_minmax(_p(x), x.size, int(rows), int(cols),
+                                                  int(symmetric), C.cast(out, C.c_void_p))
+    if rc != 0:
+        raise ValueError("rows/cols must be > 0 and data must hold rows*cols")
+    return [QuantParams._from(out[i]) for i in range(int(rows))]
+
+
+def quantize_int8_symmetric(src, scale: float, recipe: int = PRIMARY) -> np.ndarray:
+    x = _f32(src)
+    dst = np.zeros(x.size, dtype=np.int32)
+    lib().tkvo_quantize_int8_symmetric(_p(x), x.size, _p(dst), float(np.float32(scale)), int(recipe))
+    return dst
+
+
+def dequantize_int8_symmetric(src, scale: float) -> np.ndarray:
+    q = _i32(src)
+    dst = np.zeros(q.size, dtype=np.float32)
+    lib().tkvo_dequantize_int8_symmetric(_p(q), q.size, _p(dst), float(np.float32(scale)))
+    return dst
+
+
+def quantize_int8_per_channel(src, rows: int, cols: int, scales) -> np.ndarray:
+    x = _f32(src)
+    s = _f32(scales)
+    dst = np.zeros(int(rows) * int(cols), dtype=np.int32)
+    lib().tkvo_quantize_int8_per_channel(_p(x), _p(dst), int(rows), int(cols), _p(s))
+    return dst
+
+
+def dequantize_int8_per_channel(src, rows: int, cols: int, scales) -> np.ndarray:
+    q = _i32(src)
+    s = _f32(scales)
+    dst = np.zeros(int(rows) * int(cols), dtype=np.float32)
+    lib().tkvo_dequantize_int8_per_channel(_p(q), _p(dst), int(rows), int(cols), _p(s))
+    return dst
+
+
+def quantize_dynamic_int8_rowwise(src, rows: int, cols: int):
+    x = _f32(src)
+    dst = np.zeros(int(rows) * int(cols), dtype=np.int32)
+    sc = np.zeros(int(rows), dtype=np.float32)
+    lib().tkvo_quantize_dynamic_int8_rowwise(_p(x), _p(dst), int(rows), int(cols), _p(sc))
+    return dst, sc
+
+
+# ---- matmul.tkv ------------------------------------------------------------
+
+def _bias(bias):
+    if bias is None:
+        return np.zeros(1, dtype=np.float32), 0
+    b = _f32(bias)
+    return (b if b.size else np.zeros(1, dtype=np.float32)), b.size
+
+
+def matmul_int8_accum(a, w, m: int, n: int, k: int) -> np.ndarray:
+    A, W = _i32(a), _i32(w)
+    acc = np.zeros(int(m) * int(n), dtype=np.int32)
+    lib().tkvo_matmul_int8_accum(_p(A), _p(W), _p(acc), int(m), int(n), int(k))
+    return acc
+
+
+def matmul_int8_symmetric(a, w, bias, m, n, k, scale_a, scale_w, recipe=PRIMARY) -> np.ndarray:
+    A, W = _i32(a), _i32(w)
+    b, nb = _bias(bias)
+    y = np.zeros(int(m) * int(n), dtype=np.float32)
+    lib().tkvo_matmul_int8_symmetric(_p(A), _p(W), _p(b), nb, _p(y), int(m), int(n), int(k),
+                                     float(np.float32(scale_a)), float(np.float32(scale_w)),
+                                     int(recipe))
+    return y
+
+
+def matmul_int8_per_channel(a, w, bias, m, n, k, scale_a, scales_w, recipe=PRIMARY,
+                            threads: int = 1) -> np.ndarray:
+    A, W = _i32(a), _i32(w)
+    b, nb = _bias(bias)
+    s = _f32(scales_w)
+    if s.size < int(n):
+        raise ValueError("scales_w smaller than N")
+    y = np.zeros(int(m) * int(n), dtype=np.float32)
+    if threads == 1:
+        lib().tkvo_matmul_int8_per_channel(_p(A), _p(W), _p(b), nb, _p(y), int(m), int(n), int(k),
+                                           float(np.float32(scale_a)), _p(s), s.size, int(recipe))
+    else:
+        lib().tkvo_matmul_int8_per_channel_mt(_p(A), _p(W), _p(b), nb, _p(y), int(m), int(n),
+                                              int(k), float(np.float32(scale_a)), _p(s), s.size,
+                                              int(threads))
+    return y
+
+
+def quantize_fp8_e4m3(src) -> np.ndarray:
+    x = _f32(src)
+    dst = np.zeros(x.size, dtype=np.int32)
+    lib().tkvo_quantize_fp8_e4m3(_p(x), x.size, _p(dst))
+    return dst
+
+
+def dequantize_fp8_e4m3(src) -> np.ndarray:
+    q = _i32(src)
+    dst = np.zeros(q.size, dtype=np.float32)
+    lib().tkvo_dequantize_fp8_e4m3(_p(q), q.size, _p(dst))
+    return dst
+
+
+def matmul_fp8_e4m3(a, w, bias, m, n, k) -> np.ndarray:
+    A, W = _i32(a), _i32(w)
+    b, nb = _bias(bias)
+    y = np.zeros(int(m) * int(n), dtype=np.float32)
+    lib().tkvo_matmul_fp8_e4m3(_p(A), _p(W), _p(b), nb, _p(y), int(m), int(n), int(k))
+    return y
+
+
+def matmul_fp8_e4m3_exact(a, w, m, n, k):
+    """Exact dot sums (units of 2^-20, int64) and sum |a_k w_k| per output."""
+    A, W = _i32(a), _i32(w)
+    acc = np.zeros(int(m) * int(n), dtype=np.int64)
+    asum = np.zeros(int(m) * int(n), dtype=np.float64)
+    lib().tkvo_matmul_fp8_e4m3_exact(_p(A), _p(W), _p(acc), _p(asum), int(m), int(n), int(k))
+    return acc, asum
+
+
+# ---- session.tkv nodes -----------------------------------------------------
+
+def matmul_integer(a, b, y_len, m, n, k) -> np.ndarray:
+    A, B = _i32(a), _i32(b)
+    y = np.zeros(max(int(y_len), 1), dtype=np.int64)
+    lib().tkvo_matmul_integer(_p(A), A.size, _p(B), B.size, _p(y), int(y_len),
+                              int(m), int(n), int(k))
+    return y[: int(y_len)]
+
+
+def quantize_linear(x, scales, zero_point=0, outer=1, dim=1, inner=1) -> np.ndarray:
+    X, S = _f32(x), _f32(scales)
+    y = np.zeros(X.size, dtype=np.int32)
+    lib().tkvo_quantize_linear(_p(X), X.size, _p(S), S.size, int(zero_point), int(outer),
+                               int(dim), int(inner), _p(y))
+    return y
+
+
+def dequantize_linear(x, scales, zero_point=0, outer=1, dim=1, inner=1) -> np.ndarray:
+    X, S = _i32(x), _f32(scales)
+    y = np.zeros(X.size, dtype=np.float32)
+    lib().tkvo_dequantize_linear(_p(X), X.size, _p(S), S.size, int(zero_point), int(outer),
+                                 int(dim), int(inner), _p(y))
+    return y
+
+
+def dynamic_quantize_linear(x):
+    X = _f32(x)
+    y = np.zeros(X.size, dtype=np.int32)
+    ys = np.zeros(1, dtype=np.float32)
+    yz = np.zeros(1, dtype=np.float32)
+    rc = lib().tkvo_dynamic_quantize_linear(_p(X), X.size, _p(y), _p(ys), _p(yz))
+    if rc != 0:
+        raise ValueError("DynamicQuantizeLinear needs a non-empty input")
+    return y, ys[0], yz[0]
+
+
+def quantized_gemm_node(aq, wq, bias, m, n, k, scale_a, scale_b, scales_w, recipe=PRIMARY):
+    A, W = _i32(aq), _i32(wq)
+    b, nb = _bias(bias)
+    s = _f32(scales_w if scales_w is not None else [])
+    sp = s if s.size else np.zeros(1, dtype=np.float32)
+    y = np.zeros(int(m) * int(n), dtype=np.float32)
+    rc = lib().tkvo_quantized_gemm_node(_p(A), _p(W), _p(b), nb, _p(y), int(m), int(n), int(k),
+                                        float(np.float32(scale_a)), float(np.float32(scale_b)),
+                                        _p(sp), s.size, int(recipe))
+    if rc != 0:
+        raise ValueError("scales_w smaller than N")
+    return y

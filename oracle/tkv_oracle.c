@@ -1,0 +1,827 @@
+/*
+ * tkv_oracle.c -- CPU restatement of TokenVector.Inference's PTQ path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and CPU baseline for
+ * libtkv_hip.  Built with -O2 -ffp-contract=off (no FMA contraction, no
+ * fast-math) so every f64 / f32 operation rounds exactly once, as the
+ * reference's .NET JIT does.
+ *
+ * Conventions restated from the reference runtime:
+ *  - round(x) is .NET Math.Round(double): round half to even  -> rint().
+ *  - int(x) of a double is .NET's conversion, saturating since .NET 9
+ *    (the reference targets .NET 10): NaN -> 0, out of range -> INT64_MIN/MAX.
+ *  - unannotated float locals are f64; f32 (+) f32 and literal (+) f32 are
+ *    computed in f32; values round to f32 when stored to list[f32] / f32
+ *    fields / f32 returns.
+ *
+ * Parity pinning (what fixes each function independently of this file) is
+ * listed in tests/test_oracle_*.py.  Functions whose result depends on
+ * compiler typing that no reference test pins carry a "parity unpinned"
+ * note below; they keep the alternate reading behind a recipe switch.
+ */
+#include "tkv_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#define TKVO_ERR_ARG (-4)
+
+/* .NET (>= 9) double -> long conversion: saturating, NaN -> 0. */
+static int64_t net_to_i64(double v) {
+    if (v != v) return 0;
+    if (v >= 9223372036854775808.0) return INT64_MAX;
+    if (v <= -9223372036854775808.0) return INT64_MIN;
+    return (int64_t)v;
+}
+
+/* .NET Math.Round(double) with MidpointRounding.ToEven. */
+static double net_round(double v) { return rint(v); }
+
+static int64_t clamp_i64(int64_t v, int64_t lo, int64_t hi) {
+    if (v < lo) return lo;
+    if (v > hi) return hi;
+    return v;
+}
+
+/* ===================================================================== */
+/* tv/runtime/f32_bits.tkv                                               */
+/* ===================================================================== */
+
+/* f32_bits.tkv:6-57.  Bit pattern of fl32(x) found by halving/doubling.
+ * x == 0.0 (either sign) returns 0, so -0.0 maps to +0.0's bits (:19-20).
+ * The reference's exponent loop never ends for +-inf (:27-29); this
+ * restatement returns the f32 infinity pattern there instead. */
+int64_t tkvo_f64_to_f32_bits(double x) {
+    if (x == 0.0) return 0;
+    int64_t s = 0;
+    double a = x;
+    if (x < 0.0) {
+        s = 2147483648LL;
+        a = 0.0 - x;
+    }
+    if (isinf(a)) return s + 255LL * 8388608LL;
+    int64_t e = 0;
+    while (a >= 2.0) {
+        a = a / 2.0;
+        e = e + 1;
+    }
+    while (a < 1.0) {
+        a = a * 2.0;
+        e = e - 1;
+    }
+    int64_t ex = e + 127;
+    if (ex >= 255) return s + 255LL * 8388608LL;
+    if (ex <= 0) {
+        int64_t sh = e + 149;
+        if (sh <= 0) return s;
+        return s + net_to_i64(a * pow(2.0, (double)sh) + 0.5);
+    }
+    double t = (a - 1.0) * 8388608.0;
+    int64_t f = net_to_i64(t);
+    double r = t - (double)f;
+    int64_t m;
+    if (r > 0.5) {
+        m = f + 1;
+    } else if (r < 0.5) {
+        m = f;
+    } else {
+        m = f;
+        if (f % 2 != 0) m = f + 1;
+    }
+    if (m > 8388607) {
+        m = 0;
+        ex = ex + 1;
+        if (ex >= 255) return s + 255LL * 8388608LL;
+    }
+    return s + ex * 8388608LL + m;
+}
+
+/* f32_bits.tkv:60-74.  Note the exponent-255 branch yields 2^129 (finite in
+ * f64, +-inf once rounded to f32) whatever the mantissa, and a set sign bit
+ * on zero gives 0.0 - 0.0 = +0.0. */
+double tkvo_f32_bits_to_f64(int64_t b) {
+    int64_t s = b & 2147483648LL;
+    int64_t ex = (b >> 23) & 255;
+    int64_t mant = b & 8388607;
+    double v;
+    if (ex == 0) {
+        v = (double)mant * pow(2.0, 0.0 - 149.0);
+    } else if (ex == 255) {
+        v = pow(2.0, 128.0) * 2.0;
+    } else {
+        v = (1.0 + (double)mant / 8388608.0) * pow(2.0, (double)(ex - 127));
+    }
+    if (s != 0) v = 0.0 - v;
+    return v;
+}
+
+/* ===================================================================== */
+/* tv/quantization/types.tkv                                             */
+/* ===================================================================== */
+
+/* types.tkv:71-93: round v >= 0 right by s bits, ties to even. */
+int64_t tkvo_rne_rshift(int64_t v, int64_t s) {
+    if (s > 40) return 0;
+    if (s <= 0) return v;
+    int64_t half = 1;
+    for (int64_t i = 0; i < s - 1; i++) half = half * 2;
+    int64_t q = v >> s;
+    int64_t rem = v - (q << s);
+    if (rem > half) return q + 1;
+    if (rem < half) return q;
+    if ((q & 1) == 1) return q + 1;
+    return q;
+}
+
+/* types.tkv:154-191: generic FP8 encode on the binary32 bit pattern.
+ * e4m3 arguments (7, 3, 15, 0, 126): the saturation test is e8 >= 15, so
+ * |x| >= 248 gives 0x7E; subnormal round-up is clamped to mantissa 7. */
+int64_t tkvo_fp8_encode(float x, int64_t bias, int64_t w, int64_t emax_field,
+                        int64_t has_inf, int64_t sat_bits) {
+    int64_t b = tkvo_f64_to_f32_bits((double)x);
+    int64_t sign = (b >> 31) & 1;
+    int64_t ex = (b >> 23) & 255;
+    int64_t man = b & 8388607;
+    if (ex == 255) {
+        if (man != 0) {
+            if (has_inf == 1) return (sign << 7) | sat_bits;
+            return (sign << 7) | 127;
+        }
+        if (has_inf == 1) return (sign << 7) | emax_field;
+        return (sign << 7) | 127;
+    }
+    int64_t e, full;
+    if (ex == 0) {
+        e = -126;
+        full = man;
+    } else {
+        e = ex - 127;
+        full = man | 8388608;
+    }
+    int64_t e8 = e + bias;
+    if (e8 >= emax_field) return (sign << 7) | sat_bits;
+    if (e8 <= 0) {
+        int64_t m = tkvo_rne_rshift(full, 24 - w - e8);
+        int64_t lim = (1LL << w) - 1;
+        if (m > lim) m = lim;
+        return (sign << 7) | m;
+    }
+    int64_t r = tkvo_rne_rshift(full, 23 - w);
+    int64_t base = 1LL << w;
+    if (r >= base * 2) {
+        r = base;
+        e8 = e8 + 1;
+        if (e8 >= emax_field) return (sign << 7) | sat_bits;
+    }
+    return (sign << 7) | (e8 << w) | (r - base);
+}
+
+/* types.tkv:193-226: generic FP8 decode; result typed f32. */
+float tkvo_fp8_decode(int64_t v, int64_t bias, int64_t w, int64_t emax_field,
+                      int64_t has_inf) {
+    int64_t sign = (v >> 7) & 1;
+    int64_t ebits = 5;
+    if (emax_field == 15) ebits = 4;
+    int64_t emask = (1LL << ebits) - 1;
+    int64_t e8 = (v >> w) & emask;
+    int64_t m8 = v & ((1LL << w) - 1);
+    int64_t base = 1LL << w;
+    if (e8 == emax_field) {
+        if (has_inf == 0) {
+            if (m8 == 7)
+                return (float)tkvo_f32_bits_to_f64((sign << 31) | 2139095040LL | 4194304LL);
+        } else {
+            if (m8 != 0)
+                return (float)tkvo_f32_bits_to_f64((sign << 31) | 2139095040LL | 4194304LL);
+            return (float)tkvo_f32_bits_to_f64((sign << 31) | 2139095040LL);
+        }
+    }
+    int64_t e32, man32;
+    if (e8 == 0) {
+        if (m8 == 0) return (float)tkvo_f32_bits_to_f64(sign << 31);
+        int64_t t = m8;
+        int64_t n = 0;
+        while (t < base) {
+            t = t * 2;
+            n = n + 1;
+        }
+        e32 = 127 - bias - n;
+        man32 = (t - base) << (23 - w);
+    } else {
+        e32 = e8 - bias + 127;
+        man32 = m8 << (23 - w);
+    }
+    return (float)tkvo_f32_bits_to_f64((sign << 31) | (e32 << 23) | man32);
+}
+
+/* types.tkv:228-233 */
+int64_t tkvo_fp8_e4m3_encode(float x) { return tkvo_fp8_encode(x, 7, 3, 15, 0, 126); }
+float tkvo_fp8_e4m3_decode(int64_t v) { return tkvo_fp8_decode(v, 7, 3, 15, 0); }
+/* types.tkv:235-240 */
+int64_t tkvo_fp8_e5m2_encode(float x) { return tkvo_fp8_encode(x, 15, 2, 31, 1, 252); }
+float tkvo_fp8_e5m2_decode(int64_t v) { return tkvo_fp8_decode(v, 15, 2, 31, 1); }
+
+/* ===================================================================== */
+/* tv/quantization/engine.tkv                                            */
+/* ===================================================================== */
+
+/* engine.tkv:9-10 */
+tkvo_qparams tkvo_quant_identity(void) {
+    tkvo_qparams p;
+    p.scale = 1.0f;
+    p.zero_point = 0;
+    p.min_val = (float)-340282346638528859811704183484516925440.0;
+    p.max_val = (float)340282346638528859811704183484516925440.0;
+    return p;
+}
+
+/* engine.tkv:13-36.  mn / mx are f64 locals holding f32 values; the
+ * QuantParams fields round to f32.  Symmetric: scale = fl32(am / 127.0). */
+tkvo_qparams tkvo_calibrate_minmax(const float* data, int64_t n, int32_t symmetric) {
+    if (n == 0) return tkvo_quant_identity();
+    double mn = data[0];
+    double mx = data[0];
+    for (int64_t i = 1; i < n; i++) {
+        double v = data[i];
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+    }
+    tkvo_qparams p;
+    if (symmetric) {
+        double am = fabs(mx);
+        if (fabs(mn) > am) am = fabs(mn);
+        if (am < 0.00000001) am = 0.00000001;
+        p.scale = (float)(am / 127.0);
+        p.zero_point = 0;
+        p.min_val = (float)(-am);
+        p.max_val = (float)am;
+        return p;
+    }
+    if (fabs(mx - mn) < 0.00000001) mx = mn + 0.00000001;
+    double scale = (mx - mn) / 255.0;
+    /* int(...) - 128 runs in the runtime's overflow-free integer (TkvInt),
+     * so the clamp sees the mathematical value: clamp in f64. */
+    double z = net_round(-mn / scale);
+    if (z != z) z = 0.0;
+    z = z - 128.0;
+    int64_t zp = z < -128.0 ? -128 : (z > 127.0 ? 127 : (int64_t)z);
+    p.scale = (float)scale;
+    p.zero_point = zp;
+    p.min_val = (float)mn;
+    p.max_val = (float)mx;
+    return p;
+}
+
+/* engine.tkv:202-213: A1 on a copy of each row. */
+int32_t tkvo_calibrate_per_channel_minmax(const float* data, int64_t len, int64_t rows,
+                                          int64_t cols, int32_t symmetric,
+                                          tkvo_qparams* out) {
+    if (rows <= 0 || cols <= 0) return TKVO_ERR_ARG;
+    if (len < rows * cols) return TKVO_ERR_ARG;
+    for (int64_t r = 0; r < rows; r++)
+        out[r] = tkvo_calibrate_minmax(data + r * cols, cols, symmetric);
+    return 0;
+}
+
+/* engine.tkv:216-226.  `inv = 1.0 / scale` with scale an f32 parameter is a
+ * literal (+) f32 operation, i.e. an f32 division (primary); the product
+ * src[i] * inv is taken in f64 (inv is an f64 local) and is exact.
+ * Parity unpinned at the compiler boundary: the alternate recipe divides in
+ * f64.  The two differ only where x*inv lands on a rounding tie. */
+int32_t tkvo_quantize_int8_symmetric(const float* src, int64_t n, int32_t* dst,
+                                     float scale, int32_t recipe) {
+    double inv;
+    if ((double)scale > 0.00000001) {
+        if (recipe == TKVO_RECIPE_PRIMARY)
+            inv = (double)(1.0f / scale);
+        else
+            inv = 1.0 / (double)scale;
+    } else {
+        inv = 1.0 / 0.00000001;
+    }
+    for (int64_t i = 0; i < n; i++) {
+        int64_t q = net_to_i64(net_round((double)src[i] * inv));
+        dst[i] = (int32_t)clamp_i64(q, -127, 127);
+    }
+    return 0;
+}
+
+/* engine.tkv:229-234: fl32(q * scale); the product is exact in f64. */
+int32_t tkvo_dequantize_int8_symmetric(const int32_t* src, int64_t n, float* dst,
+                                       float scale) {
+    for (int64_t i = 0; i < n; i++) dst[i] = (float)((double)src[i] * (double)scale);
+    return 0;
+}
+
+/* engine.tkv:237-250: sc is an f64 local, inv = 1.0 / sc in f64. */
+int32_t tkvo_quantize_int8_per_channel(const float* src, int32_t* dst, int64_t rows,
+                                       int64_t cols, const float* scales) {
+    for (int64_t r = 0; r < rows; r++) {
+        double sc = scales[r];
+        if (sc <= 0.00000001) sc = 0.00000001;
+        double inv = 1.0 / sc;
+        for (int64_t c = 0; c < cols; c++) {
+            int64_t i = r * cols + c;
+            dst[i] = (int32_t)clamp_i64(net_to_i64(net_round((double)src[i] * inv)), -127, 127);
+        }
+    }
+    return 0;
+}
+
+/* engine.tkv:253-262 */
+int32_t tkvo_dequantize_int8_per_channel(const int32_t* src, float* dst, int64_t rows,
+                                         int64_t cols, const float* scales) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c++) {
+            int64_t i = r * cols + c;
+            dst[i] = (float)((double)src[i] * (double)scales[r]);
+        }
+    return 0;
+}
+
+/* engine.tkv:266-285: per-row absmax; sc = am / 127.0 stays f64 (unrounded)
+ * for the reciprocal, and is rounded to f32 only in scales_out. */
+int32_t tkvo_quantize_dynamic_int8_rowwise(const float* src, int32_t* dst, int64_t rows,
+                                           int64_t cols, float* scales_out) {
+    for (int64_t r = 0; r < rows; r++) {
+        double am = 0.0;
+        for (int64_t c = 0; c < cols; c++) {
+            double a = fabs((double)src[r * cols + c]);
+            if (a > am) am = a;
+        }
+        if (am < 0.00000001) am = 0.00000001;
+        double sc = am / 127.0;
+        scales_out[r] = (float)sc;
+        double inv = 1.0 / sc;
+        for (int64_t c = 0; c < cols; c++) {
+            int64_t i = r * cols + c;
+            dst[i] = (int32_t)clamp_i64(net_to_i64(net_round((double)src[i] * inv)), -127, 127);
+        }
+    }
+    return 0;
+}
+
+/* ===================================================================== */
+/* tv/quantization/matmul.tkv                                            */
+/* ===================================================================== */
+
+/* matmul.tkv:116-127: exact integer dot product, 32-way unrolled. */
+int64_t tkvo_dot_int8(const int32_t* a, int64_t ao, const int32_t* b, int64_t bo,
+                      int64_t k) {
+    int64_t acc = 0;
+    int64_t kk = 0;
+    int64_t limit = k - 31;
+    while (kk < limit) {
+        for (int64_t l = 0; l < 32; l++)
+            acc = acc + (int64_t)a[ao + kk + l] * (int64_t)b[bo + kk + l];
+        kk = kk + 32;
+    }
+    while (kk < k) {
+        acc = acc + (int64_t)a[ao + kk] * (int64_t)b[bo + kk];
+        kk = kk + 1;
+    }
+    return acc;
+}
+
+int32_t tkvo_matmul_int8_accum(const int32_t* a, const int32_t* w, int32_t* acc,
+                               int64_t m, int64_t n, int64_t k) {
+    for (int64_t mm = 0; mm < m; mm++)
+        for (int64_t nn = 0; nn < n; nn++)
+            acc[mm * n + nn] = (int32_t)tkvo_dot_int8(a, mm * k, w, nn * k, k);
+    return 0;
+}
+
+/* matmul.tkv:4-15.  s = scale_a * scale_w is an f32 multiply (f32 (+) f32);
+ * y = acc * s + bias runs in f64 and rounds once to f32.
+ * Parity unpinned at the compiler boundary: alternate forms s in f64. */
+int32_t tkvo_matmul_int8_symmetric(const int32_t* a, const int32_t* w,
+                                   const float* bias, int64_t nbias, float* y,
+                                   int64_t m, int64_t n, int64_t k,
+                                   float scale_a, float scale_w, int32_t recipe) {
+    double s;
+    if (recipe == TKVO_RECIPE_PRIMARY)
+        s = (double)(scale_a * scale_w);
+    else
+        s = (double)scale_a * (double)scale_w;
+    for (int64_t mm = 0; mm < m; mm++)
+        for (int64_t nn = 0; nn < n; nn++) {
+            int64_t acc = tkvo_dot_int8(a, mm * k, w, nn * k, k);
+            double b = nbias > 0 ? (double)bias[nn] : 0.0;
+            y[mm * n + nn] = (float)((double)acc * s + b);
+        }
+    return 0;
+}
+
+/* matmul.tkv:17-29.  Primary: the i64 accumulator widens to f64 and the
+ * chain acc * scale_a * scales_w[n] + bias runs left to right in f64 (the
+ * first product is exact), rounding once to f32.
+ * Parity unpinned at the compiler boundary: alternate is an all-f32 chain. */
+int32_t tkvo_matmul_int8_per_channel(const int32_t* a, const int32_t* w,
+                                     const float* bias, int64_t nbias, float* y,
+                                     int64_t m, int64_t n, int64_t k, float scale_a,
+                                     const float* scales_w, int64_t nscales,
+                                     int32_t recipe) {
+    if (nscales < n) return TKVO_ERR_ARG;
+    for (int64_t mm = 0; mm < m; mm++)
+        for (int64_t nn = 0; nn < n; nn++) {
+            int64_t acc = tkvo_dot_int8(a, mm * k, w, nn * k, k);
+            if (recipe == TKVO_RECIPE_PRIMARY) {
+                double b = nbias > 0 ? (double)bias[nn] : 0.0;
+                y[mm * n + nn] = (float)((double)acc * (double)scale_a * (double)scales_w[nn] + b);
+            } else {
+                float b = nbias > 0 ? bias[nn] : 0.0f;
+                float t = (float)acc * scale_a;
+                t = t * scales_w[nn];
+                y[mm * n + nn] = t + b;
+            }
+        }
+    return 0;
+}
+
+/* matmul.tkv:75-77: FP8E4M3(1, v + 128).to_float() -- the positional
+ * record skips __init__, so value = v + 128 unmasked; the decoder's shifts
+ * and masks only look at the low 8 bits. */
+static float fp8_code_decode(int64_t v) { return tkvo_fp8_e4m3_decode(v + 128); }
+
+/* matmul.tkv:60-66: dst = encode(x) - 128 (offset code, not two's complement). */
+int32_t tkvo_quantize_fp8_e4m3(const float* src, int64_t n, int32_t* dst) {
+    for (int64_t i = 0; i < n; i++) dst[i] = (int32_t)(tkvo_fp8_e4m3_encode(src[i]) - 128);
+    return 0;
+}
+
+/* matmul.tkv:68-73 */
+int32_t tkvo_dequantize_fp8_e4m3(const int32_t* src, int64_t n, float* dst) {
+    for (int64_t i = 0; i < n; i++) dst[i] = fp8_code_decode(src[i]);
+    return 0;
+}
+
+/* matmul.tkv:46-58.  acc is an f64 local; each product is an f32 multiply of
+ * two f32 decodes (exact: <= 8 significant bits).  y = fl32(acc + bias). */
+int32_t tkvo_matmul_fp8_e4m3(const int32_t* a, const int32_t* w, const float* bias,
+                             int64_t nbias, float* y, int64_t m, int64_t n, int64_t k) {
+    for (int64_t mm = 0; mm < m; mm++)
+        for (int64_t nn = 0; nn < n; nn++) {
+            double acc = 0.0;
+            for (int64_t kk = 0; kk < k; kk++) {
+                float p = fp8_code_decode(a[mm * k + kk]) * fp8_code_decode(w[nn * k + kk]);
+                acc = acc + (double)p;
+            }
+            double b = nbias > 0 ? (double)bias[nn] : 0.0;
+            y[mm * n + nn] = (float)(acc + b);
+        }
+    return 0;
+}
+
+/* Every finite value of the reference decoder is an integer multiple of
+ * 2^-10 (its subnormals decode to m * 2^-10), so each product is a multiple
+ * of 2^-20 below 2^18 in magnitude: the sum is exact in int64 units of 2^-20.
+ * (The reference's own f64 running sum is exact while K * 2^38 < 2^53.) */
+int32_t tkvo_matmul_fp8_e4m3_exact(const int32_t* a, const int32_t* w, int64_t* acc_q20,
+                                   double* abs_sum, int64_t m, int64_t n, int64_t k) {
+    for (int64_t mm = 0; mm < m; mm++)
+        for (int64_t nn = 0; nn < n; nn++) {
+            int64_t acc = 0;
+            double as = 0.0;
+            for (int64_t kk = 0; kk < k; kk++) {
+                double p = (double)fp8_code_decode(a[mm * k + kk]) *
+                           (double)fp8_code_decode(w[nn * k + kk]);
+                acc += (int64_t)ldexp(p, 20);
+                as += fabs(p);
+            }
+            acc_q20[mm * n + nn] = acc;
+            if (abs_sum) abs_sum[mm * n + nn] = as;
+        }
+    return 0;
+}
+
+/* ===================================================================== */
+/* tv/runtime/session.tkv nodes                                          */
+/* ===================================================================== */
+
+/* session.tkv:2789-2851: Y[M,N] = A[M,K] . B[K,N] (B row-major K x N). */
+int32_t tkvo_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, int64_t nb,
+                            int64_t* y, int64_t ny, int64_t m, int64_t n, int64_t k) {
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t j = 0; j < n; j++) {
+            int64_t acc = 0;
+            for (int64_t p = 0; p < k; p++) {
+                int64_t ai = i * k + p;
+                int64_t bi = p * n + j;
+                int64_t av = (ai >= 0 && ai < na) ? a[ai] : 0;
+                int64_t bv = (bi >= 0 && bi < nb) ? b[bi] : 0;
+                acc = acc + av * bv;
+            }
+            int64_t yi = i * n + j;
+            if (yi >= 0 && yi < ny) y[yi] = acc;
+        }
+    return 0;
+}
+
+/* session.tkv:1896-1953: q = clamp(round(x / s) + zp, -128, 127) with
+ * s = max(sc, 1e-12) as an f64 local: a true f64 division, not a reciprocal
+ * multiply.  Integer arithmetic is the runtime's overflow-free integer, so
+ * the clamp sees the mathematical value. */
+static int32_t qlinear_one(float x, double s, int64_t zp) {
+    double r = net_round((double)x / s);
+    if (r != r) r = 0.0;
+    if (r > 0x1p62) r = 0x1p62;
+    if (r < -0x1p62) r = -0x1p62;
+    int64_t q = (int64_t)r + zp;
+    return (int32_t)clamp_i64(q, -128, 127);
+}
+
+int32_t tkvo_quantize_linear(const float* x, int64_t nx, const float* scales,
+                             int64_t nscale, int64_t zero_point, int64_t outer,
+                             int64_t dim, int64_t inner, int32_t* y) {
+    if (nscale == 1) {
+        double s = (scales[0] > 0.000000000001) ? (double)scales[0] : 0.000000000001;
+        for (int64_t i = 0; i < nx; i++) y[i] = qlinear_one(x[i], s, zero_point);
+        return 0;
+    }
+    for (int64_t o = 0; o < outer; o++)
+        for (int64_t j = 0; j < dim; j++) {
+            double s = (scales[j] > 0.000000000001) ? (double)scales[j] : 0.000000000001;
+            for (int64_t t = 0; t < inner; t++) {
+                int64_t i = (o * dim + j) * inner + t;
+                y[i] = qlinear_one(x[i], s, zero_point);
+            }
+        }
+    return 0;
+}
+
+/* session.tkv:1955-1990: y = fl32((q - zp) * sc). */
+int32_t tkvo_dequantize_linear(const int32_t* x, int64_t nx, const float* scales,
+                               int64_t nscale, int64_t zero_point, int64_t outer,
+                               int64_t dim, int64_t inner, float* y) {
+    if (nscale == 1) {
+        for (int64_t i = 0; i < nx; i++)
+            y[i] = (float)((double)((int64_t)x[i] - zero_point) * (double)scales[0]);
+        return 0;
+    }
+    for (int64_t o = 0; o < outer; o++)
+        for (int64_t j = 0; j < dim; j++)
+            for (int64_t t = 0; t < inner; t++) {
+                int64_t i = (o * dim + j) * inner + t;
+                y[i] = (float)((double)((int64_t)x[i] - zero_point) * (double)scales[j]);
+            }
+    return 0;
+}
+
+/* session.tkv:2853-2901: uint8-asymmetric dynamic quantization shifted to
+ * int8.  sc stays f64 (unrounded) for the division; y_scale rounds to f32. */
+int32_t tkvo_dynamic_quantize_linear(const float* x, int64_t nx, int32_t* y,
+                                     float* y_scale, float* y_zero_point) {
+    if (nx <= 0) return TKVO_ERR_ARG;
+    double mn = x[0];
+    double mx = x[0];
+    for (int64_t i = 1; i < nx; i++) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mx) mx = x[i];
+    }
+    if (mn > 0.0) mn = 0.0;
+    if (mx < 0.0) mx = 0.0;
+    if (mx - mn < 0.00000001) mx = mn + 0.00000001;
+    double sc = (mx - mn) / 255.0;
+    double zpf = net_round(-mn / sc);
+    int64_t zp = clamp_i64(net_to_i64(zpf), 0, 255);
+    *y_scale = (float)sc;
+    *y_zero_point = (float)zp;
+    for (int64_t i = 0; i < nx; i++) {
+        double r = net_round((double)x[i] / sc);
+        if (r != r) r = 0.0;
+        if (r > 0x1p62) r = 0x1p62;
+        if (r < -0x1p62) r = -0x1p62;
+        int64_t q = clamp_i64((int64_t)r + zp, 0, 255);
+        y[i] = (int32_t)clamp_i64(q - 128, -128, 127);
+    }
+    return 0;
+}
+
+/* session.tkv:678-697: per-channel iff scales_w is non-empty, else the
+ * symmetric GEMM with (scale_a, scale_b). */
+int32_t tkvo_quantized_gemm_node(const int32_t* aq, const int32_t* wq,
+                                 const float* bias, int64_t nbias, float* y,
+                                 int64_t m, int64_t n, int64_t k, float scale_a,
+                                 float scale_b, const float* scales_w,
+                                 int64_t nscales, int32_t recipe) {
+    if (nscales > 0)
+        return tkvo_matmul_int8_per_channel(aq, wq, bias, nbias, y, m, n, k, scale_a,
+                                            scales_w, nscales, recipe);
+    return tkvo_matmul_int8_symmetric(aq, wq, bias, nbias, y, m, n, k, scale_a, scale_b,
+                                      recipe);
+}
+
+/* ===================================================================== */
+/* tv/training/gpt2_ref.tkv:1977-1991 input generator                    */
+/* ===================================================================== */
+
+int64_t tkvo_lcg31(int64_t state) { return (state * 1103515245LL + 12345LL) % 2147483648LL; }
+
+/* _gi_noise with the hard-coded 0.02 replaced by sigma. */
+void tkvo_gi_noise(float* out, int64_t n, int64_t seed, double sigma) {
+    int64_t s = seed % 2147483648LL;
+    for (int64_t i = 0; i < n; i++) {
+        s = tkvo_lcg31(s);
+        double u1 = ((double)s + 0.5) / 2147483648.0;
+        s = tkvo_lcg31(s);
+        double u2 = (double)s / 2147483648.0;
+        out[i] = (float)(sqrt(0.0 - 2.0 * log(u1)) * cos(6.283185307179586 * u2) * sigma);
+    }
+}
+
+void tkvo_add_outliers(float* x, int64_t n, int64_t n_out, int64_t seed, int64_t seed2,
+                       double sigma_out) {
+    if (n <= 0 || n_out <= 0) return;
+    if (n_out > n) n_out = n;
+    unsigned char* taken = (unsigned char*)calloc((size_t)n, 1);
+    float* vals = (float*)malloc(sizeof(float) * (size_t)n_out);
+    tkvo_gi_noise(vals, n_out, seed2, sigma_out);
+    int64_t s = seed % 2147483648LL;
+    int64_t placed = 0;
+    while (placed < n_out) {
+        s = tkvo_lcg31(s);
+        int64_t pos = (int64_t)(((unsigned __int128)s * (unsigned __int128)n) >> 31);
+        if (taken[pos]) continue;
+        taken[pos] = 1;
+        x[pos] = vals[placed++];
+    }
+    free(vals);
+    free(taken);
+}
+
+/* ===================================================================== */
+/* Pinning: independent e4m3 encoder                                     */
+/* ===================================================================== */
+
+/* Value of positive e4m3fn code c (0..0x7E) from the OCP definition:
+ * exponent field e = c >> 3, mantissa m = c & 7, bias 7. */
+static double e4m3_spec_value(int c) {
+    int e = c >> 3, m = c & 7;
+    if (e == 0) return ldexp((double)m, -9);
+    return ldexp(1.0 + m / 8.0, e - 7);
+}
+
+int64_t tkvo_pin_e4m3_spec_encode(float x) {
+    uint32_t bits;
+    memcpy(&bits, &x, 4);
+    int64_t sign = bits >> 31;
+    if (x == 0.0f) return 0;                         /* deviation 3: -0.0 -> 0x00 */
+    if (isnan(x) || isinf(x)) return (sign << 7) | 0x7F;
+    double a = fabs((double)x);
+    if (a >= 248.0) return (sign << 7) | 0x7E;       /* deviation 1 */
+    /* largest code lo in [0, 0x77] with value(lo) <= a; 0x78 (256) is the
+     * virtual upper neighbour of 0x77 */
+    int lo = 0, hi = 0x77;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) / 2;
+        if (e4m3_spec_value(mid) <= a) lo = mid; else hi = mid - 1;
+    }
+    int code = lo;
+    double vlo = e4m3_spec_value(lo);
+    if (vlo != a) {
+        double vhi = e4m3_spec_value(lo + 1);
+        double dlo = a - vlo, dhi = vhi - a;        /* exact: all are dyadic */
+        if (dhi < dlo || (dhi == dlo && ((lo + 1) & 1) == 0)) code = lo + 1;
+    }
+    if (code == 0x08 && a < ldexp(1.0, -6)) code = 0x07; /* deviation 2 */
+    return (sign << 7) | code;
+}
+
+typedef struct {
+    int32_t elo, ehi;
+    uint64_t begin, end;    /* index range over (sign, exp, mant) */
+    int64_t bad;
+    uint32_t first_bad;
+} pin_job;
+
+static void* pin_worker(void* p) {
+    pin_job* j = (pin_job*)p;
+    uint64_t nexp = (uint64_t)(j->ehi - j->elo + 1);
+    for (uint64_t idx = j->begin; idx < j->end; idx++) {
+        uint64_t mant = idx & 0x7FFFFF;
+        uint64_t rest = idx >> 23;
+        uint64_t e = (uint64_t)j->elo + rest % nexp;
+        uint64_t sign = rest / nexp;
+        uint32_t bits = (uint32_t)((sign << 31) | (e << 23) | mant);
+        float x;
+        memcpy(&x, &bits, 4);
+        if (tkvo_fp8_e4m3_encode(x) != tkvo_pin_e4m3_spec_encode(x)) {
+            if (j->bad == 0) j->first_bad = bits;
+            j->bad++;
+        }
+    }
+    return NULL;
+}
+
+int64_t tkvo_pin_e4m3_exhaustive(int32_t elo, int32_t ehi, int32_t nthreads,
+                                 uint32_t* first_bad) {
+    if (elo < 0 || ehi > 254 || elo > ehi) return -1;
+    if (nthreads <= 0) nthreads = (int32_t)sysconf(_SC_NPROCESSORS_ONLN);
+    if (nthreads > 64) nthreads = 64;
+    uint64_t total = (uint64_t)(ehi - elo + 1) * 2ULL << 23;
+    pthread_t th[64];
+    pin_job jobs[64];
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t].elo = elo;
+        jobs[t].ehi = ehi;
+        jobs[t].begin = total * (uint64_t)t / (uint64_t)nthreads;
+        jobs[t].end = total * (uint64_t)(t + 1) / (uint64_t)nthreads;
+        jobs[t].bad = 0;
+        jobs[t].first_bad = 0;
+        pthread_create(&th[t], NULL, pin_worker, &jobs[t]);
+    }
+    int64_t bad = 0;
+    int have = 0;
+    for (int t = 0; t < nthreads; t++) {
+        pthread_join(th[t], NULL);
+        if (jobs[t].bad && !have) {
+            have = 1;
+            if (first_bad) *first_bad = jobs[t].first_bad;
+        }
+        bad += jobs[t].bad;
+    }
+    return bad;
+}
+
+typedef struct {
+    const uint32_t* bits;
+    uint8_t* out;
+    int64_t begin, end;
+} enc_job;
+
+static void* enc_worker(void* p) {
+    enc_job* j = (enc_job*)p;
+    for (int64_t i = j->begin; i < j->end; i++) {
+        float x;
+        memcpy(&x, &j->bits[i], 4);
+        j->out[i] = (uint8_t)tkvo_fp8_e4m3_encode(x);
+    }
+    return NULL;
+}
+
+int32_t tkvo_fp8_e4m3_encode_bits(const uint32_t* bits, int64_t n, uint8_t* out,
+                                  int32_t nthreads) {
+    if (nthreads <= 0) nthreads = (int32_t)sysconf(_SC_NPROCESSORS_ONLN);
+    if (nthreads > 64) nthreads = 64;
+    pthread_t th[64];
+    enc_job jobs[64];
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t].bits = bits;
+        jobs[t].out = out;
+        jobs[t].begin = n * t / nthreads;
+        jobs[t].end = n * (t + 1) / nthreads;
+        pthread_create(&th[t], NULL, enc_worker, &jobs[t]);
+    }
+    for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+    return 0;
+}
+
+/* ===================================================================== */
+/* Threaded baseline (timing only; same arithmetic as the scalar path)   */
+/* ===================================================================== */
+
+typedef struct {
+    const int32_t *a, *w;
+    const float* bias;
+    int64_t nbias;
+    float* y;
+    int64_t m0, m1, n, k;
+    float scale_a;
+    const float* scales_w;
+    int64_t nscales;
+} mm_job;
+
+static void* mm_worker(void* p) {
+    mm_job* j = (mm_job*)p;
+    if (j->m1 > j->m0)
+        tkvo_matmul_int8_per_channel(j->a + j->m0 * j->k, j->w, j->bias, j->nbias,
+                                     j->y + j->m0 * j->n, j->m1 - j->m0, j->n, j->k,
+                                     j->scale_a, j->scales_w, j->nscales,
+                                     TKVO_RECIPE_PRIMARY);
+    return NULL;
+}
+
+int32_t tkvo_matmul_int8_per_channel_mt(const int32_t* a, const int32_t* w,
+                                        const float* bias, int64_t nbias, float* y,
+                                        int64_t m, int64_t n, int64_t k, float scale_a,
+                                        const float* scales_w, int64_t nscales,
+                                        int32_t nthreads) {
+    if (nscales < n) return TKVO_ERR_ARG;
+    if (nthreads <= 0) nthreads = (int32_t)sysconf(_SC_NPROCESSORS_ONLN);
+    if (nthreads > 256) nthreads = 256;
+    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    mm_job* jobs = (mm_job*)malloc(sizeof(mm_job) * (size_t)nthreads);
+    for (int t = 0; t < nthreads; t++) {
+        mm_job j = {a, w, bias, nbias, y, m * t / nthreads, m * (t + 1) / nthreads,
+                    n, k, scale_a, scales_w, nscales};
+        jobs[t] = j;
+        pthread_create(&th[t], NULL, mm_worker, &jobs[t]);
+    }
+    for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+    free(th);
+    free(jobs);
+    return 0;
+}

@@ -1,0 +1,580 @@
+// capi.hip -- extern "C" entry points of libtkv_hip (declared in
+// include/tkv_hip.h).  Host-pointer mirrors validate exactly where the .tkv
+// functions raise ValueError (returning TKV_HIP_BAD_ARG), move the
+// reference's int32-per-code lists to and from packed device codes, and run
+// the same kernels as the device-pointer variants.
+#include <cstring>
+#include <vector>
+
+#include "tkv_internal.h"
+
+using namespace tkv;
+
+namespace {
+
+// Host-mirror workspace slots (slots 2 and 3 belong to the GEMM launchers).
+enum { WS_IN = 0, WS_OUT = 1, WS_A = 4, WS_W = 5, WS_SMALL = 6, WS_Y = 7 };
+
+int begin_host(Ctx** c) {
+    if (!hip_path_enabled())
+        return set_error(TKV_HIP_UNSUPPORTED, "TKV_QUANT_HIP=0: HIP path disabled");
+    return ctx_get(0, c);
+}
+
+int upload(Ctx* c, int slot, const void* h, size_t bytes, void** d) {
+    TKV_RC_TRY(ctx_workspace(c, slot, bytes, d));
+    if (bytes) TKV_HIP_TRY(hipMemcpyAsync(*d, h, bytes, hipMemcpyHostToDevice, c->stream));
+    return TKV_HIP_OK;
+}
+
+int download(Ctx* c, void* h, const void* d, size_t bytes) {
+    if (bytes) TKV_HIP_TRY(hipMemcpyAsync(h, d, bytes, hipMemcpyDeviceToHost, c->stream));
+    TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    return TKV_HIP_OK;
+}
+
+// int32 codes (List<int>) -> int8 rows padded to ldk (multiple of 16).
+// Codes outside [lo, hi] cannot ride the int8 datapath: UNSUPPORTED, so the
+// caller keeps its own loop.
+int pack_codes(const int32_t* src, int64_t rows, int64_t k, int64_t ldk, int bias, int lo, int hi,
+               std::vector<int8_t>& out) {
+    out.assign((size_t)(rows * ldk), 0);
+    for (int64_t r = 0; r < rows; r++) {
+        const int32_t* s = src + r * k;
+        int8_t* d = out.data() + r * ldk;
+        for (int64_t i = 0; i < k; i++) {
+            int v = s[i];
+            if (v < lo || v > hi)
+                return set_error(TKV_HIP_UNSUPPORTED, "code outside the int8 datapath range");
+            d[i] = (int8_t)(v + bias);
+        }
+    }
+    return TKV_HIP_OK;
+}
+
+int check_recipe(int32_t recipe) {
+    if (recipe != TKV_HIP_RECIPE_PRIMARY && recipe != TKV_HIP_RECIPE_ALTERNATE)
+        return set_error(TKV_HIP_BAD_ARG, "unknown recipe");
+    return TKV_HIP_OK;
+}
+
+// Shared body of the INT8 GEMM host mirrors.
+int host_gemm_i8(const int32_t* pa, const int32_t* pw, const float* pbias, int64_t n_bias,
+                 void* py, bool accum, int64_t m, int64_t n, int64_t k, float scale_a,
+                 float scale_w, const float* scales_w, int64_t n_scales, int32_t recipe) {
+    if (m < 0 || n < 0 || k < 0) return set_error(TKV_HIP_BAD_ARG, "negative GEMM size");
+    TKV_RC_TRY(check_recipe(recipe));
+    if (!accum && n_bias > 0 && n_bias < n)
+        return set_error(TKV_HIP_BAD_ARG, "bias shorter than N");
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    if (m == 0 || n == 0) return TKV_HIP_OK;
+    if (k == 0) {  // empty dot products (acc = 0): one zero term gives the same sums
+        std::vector<int32_t> za((size_t)m, 0), zw((size_t)n, 0);
+        return host_gemm_i8(za.data(), zw.data(), pbias, n_bias, py, accum, m, n, 1, scale_a,
+                            scale_w, scales_w, n_scales, recipe);
+    }
+    int64_t ldk = (k + 15) & ~int64_t(15);
+    std::vector<int8_t> ha, hw;
+    TKV_RC_TRY(pack_codes(pa, m, k, ldk, 0, -128, 127, ha));
+    TKV_RC_TRY(pack_codes(pw, n, k, ldk, 0, -128, 127, hw));
+    void *da, *dw, *dsmall, *dy;
+    TKV_RC_TRY(upload(c, WS_A, ha.data(), ha.size(), &da));
+    TKV_RC_TRY(upload(c, WS_W, hw.data(), hw.size(), &dw));
+    // small arrays: [scale_a][scales_w (n)][bias (n)]
+    std::vector<float> small(1 + 2 * (size_t)n, 0.0f);
+    small[0] = scale_a;
+    if (scales_w) memcpy(&small[1], scales_w, sizeof(float) * (size_t)n);
+    bool has_bias = !accum && n_bias > 0;
+    if (has_bias) memcpy(&small[1 + n], pbias, sizeof(float) * (size_t)n);
+    TKV_RC_TRY(upload(c, WS_SMALL, small.data(), small.size() * sizeof(float), &dsmall));
+    size_t ybytes = (size_t)(m * n) * 4;
+    TKV_RC_TRY(ctx_workspace(c, WS_Y, ybytes, &dy));
+    const float* fs = static_cast<const float*>(dsmall);
+    I8Epilogue ep;
+    ep.mode = accum ? EPI_ACCUM_I32 : (scales_w ? EPI_PER_CHANNEL : EPI_SYMMETRIC);
+    ep.recipe = recipe;
+    ep.scale_a = fs;
+    ep.scale_a_stride = 0;
+    ep.scale_w = scale_w;
+    ep.scales_w = scales_w ? fs + 1 : nullptr;
+    ep.bias = has_bias ? fs + 1 + n : nullptr;
+    TKV_RC_TRY(launch_gemm_i8(c, static_cast<int8_t*>(da), static_cast<int8_t*>(dw), m, n, ldk,
+                              ep, dy));
+    return download(c, py, dy, ybytes);
+}
+
+}  // namespace
+
+extern "C" {
+
+// ===========================================================================
+// Host-pointer mirrors
+// ===========================================================================
+
+int32_t tkv_hip_calibrate_minmax(const float* data, int64_t n, int32_t symmetric, float* scale,
+                                 int64_t* zero_point, float* min_val, float* max_val) {
+    if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative length");
+    tkv_hip_qparams_dev p;
+    if (n == 0) {  // _quant_identity(), engine.tkv:9-10
+        p.scale = 1.0f;
+        p.zero_point = 0;
+        p.min_val = -3.4028234663852886e38f;
+        p.max_val = 3.4028234663852886e38f;
+    } else {
+        void* dx;
+        Ctx* c;
+        TKV_RC_TRY(begin_host(&c));
+        TKV_RC_TRY(upload(c, WS_IN, data, (size_t)n * 4, &dx));
+        TKV_RC_TRY(launch_minmax_tensor(c, static_cast<float*>(dx), n,
+                                        symmetric ? MM_SYMMETRIC : MM_ASYMMETRIC,
+                                        TKV_HIP_RECIPE_PRIMARY, c->params));
+        TKV_RC_TRY(download(c, &p, c->params, sizeof(p)));
+    }
+    if (scale) *scale = p.scale;
+    if (zero_point) *zero_point = p.zero_point;
+    if (min_val) *min_val = p.min_val;
+    if (max_val) *max_val = p.max_val;
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_calibrate_per_channel_minmax(const float* data, int64_t n_data, int64_t rows,
+                                             int64_t cols, int32_t symmetric, float* scales,
+                                             int64_t* zero_points, float* min_vals,
+                                             float* max_vals) {
+    if (rows <= 0 || cols <= 0) return set_error(TKV_HIP_BAD_ARG, "rows/cols must be > 0");
+    if (n_data < rows * cols) return set_error(TKV_HIP_BAD_ARG, "data smaller than rows*cols");
+    void *dx, *dp;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, data, (size_t)(rows * cols) * 4, &dx));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, sizeof(tkv_hip_qparams_dev) * (size_t)rows, &dp));
+    auto* rp = static_cast<tkv_hip_qparams_dev*>(dp);
+    TKV_RC_TRY(launch_quant_rows(c, static_cast<float*>(dx), rows, cols, RM_CALIBRATE_FULL,
+                                 nullptr, nullptr, false, nullptr, rp, symmetric ? 1 : 0));
+    std::vector<tkv_hip_qparams_dev> hp((size_t)rows);
+    TKV_RC_TRY(download(c, hp.data(), rp, sizeof(tkv_hip_qparams_dev) * (size_t)rows));
+    for (int64_t r = 0; r < rows; r++) {
+        if (scales) scales[r] = hp[r].scale;
+        if (zero_points) zero_points[r] = hp[r].zero_point;
+        if (min_vals) min_vals[r] = hp[r].min_val;
+        if (max_vals) max_vals[r] = hp[r].max_val;
+    }
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_quantize_int8_symmetric_recipe(const float* src, int64_t n_src, int32_t* dst,
+                                               int64_t n_dst, float scale, int32_t recipe) {
+    TKV_RC_TRY(check_recipe(recipe));
+    if (n_src < 0 || n_dst < n_src) return set_error(TKV_HIP_BAD_ARG, "dst too small");
+    if (n_src == 0) return TKV_HIP_OK;
+    tkv_hip_qparams_dev p;
+    memset(&p, 0, sizeof(p));
+    p.scale = scale;
+    // engine.tkv:219-222: f32 reciprocal (primary) or f64 (alternate)
+    if ((double)scale > 0.00000001)
+        p.inv = recipe == TKV_HIP_RECIPE_PRIMARY ? (double)(1.0f / scale) : 1.0 / (double)scale;
+    else
+        p.inv = 1.0 / 0.00000001;
+    void *dx, *dq;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)n_src * 4, &dx));
+    TKV_HIP_TRY(hipMemcpyAsync(c->params, &p, sizeof(p), hipMemcpyHostToDevice, c->stream));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n_src * 4, &dq));
+    TKV_RC_TRY(launch_quant_i8_tensor(c, static_cast<float*>(dx), n_src, c->params, dq, true));
+    return download(c, dst, dq, (size_t)n_src * 4);
+}
+
+int32_t tkv_hip_quantize_int8_symmetric(const float* src, int64_t n_src, int32_t* dst,
+                                        int64_t n_dst, float scale) {
+    return tkv_hip_quantize_int8_symmetric_recipe(src, n_src, dst, n_dst, scale,
+                                                  TKV_HIP_RECIPE_PRIMARY);
+}
+
+int32_t tkv_hip_dequantize_int8_symmetric(const int32_t* src, int64_t n_src, float* dst,
+                                          int64_t n_dst, float scale) {
+    if (n_src < 0 || n_dst < n_src) return set_error(TKV_HIP_BAD_ARG, "dst too small");
+    if (n_src == 0) return TKV_HIP_OK;
+    void *dq, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)n_src * 4, &dq));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n_src * 4, &dy));
+    TKV_RC_TRY(launch_dequant_i8(c, dq, true, 1, n_src, scale, nullptr, static_cast<float*>(dy)));
+    return download(c, dst, dy, (size_t)n_src * 4);
+}
+
+int32_t tkv_hip_quantize_int8_per_channel(const float* src, int64_t n_src, int32_t* dst,
+                                          int64_t n_dst, int64_t rows, int64_t cols,
+                                          const float* scales, int64_t n_scales) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    if (n_dst < rows * cols || n_src < rows * cols) return set_error(TKV_HIP_BAD_ARG, "span too small");
+    if (n_scales < rows) return set_error(TKV_HIP_BAD_ARG, "scales smaller than rows");
+    if (rows * cols == 0) return TKV_HIP_OK;
+    void *dx, *ds, *dq;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)(rows * cols) * 4, &dx));
+    TKV_RC_TRY(upload(c, WS_SMALL, scales, (size_t)rows * 4, &ds));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)(rows * cols) * 4, &dq));
+    TKV_RC_TRY(launch_quant_rows(c, static_cast<float*>(dx), rows, cols, RM_PER_CHANNEL,
+                                 static_cast<float*>(ds), dq, true, nullptr, nullptr, 1));
+    return download(c, dst, dq, (size_t)(rows * cols) * 4);
+}
+
+int32_t tkv_hip_dequantize_int8_per_channel(const int32_t* src, int64_t n_src, float* dst,
+                                            int64_t n_dst, int64_t rows, int64_t cols,
+                                            const float* scales, int64_t n_scales) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    if (n_dst < rows * cols || n_src < rows * cols) return set_error(TKV_HIP_BAD_ARG, "span too small");
+    if (n_scales < rows) return set_error(TKV_HIP_BAD_ARG, "scales smaller than rows");
+    if (rows * cols == 0) return TKV_HIP_OK;
+    void *dq, *ds, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)(rows * cols) * 4, &dq));
+    TKV_RC_TRY(upload(c, WS_SMALL, scales, (size_t)rows * 4, &ds));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)(rows * cols) * 4, &dy));
+    TKV_RC_TRY(launch_dequant_i8(c, dq, true, rows, cols, 0.0f, static_cast<float*>(ds),
+                                 static_cast<float*>(dy)));
+    return download(c, dst, dy, (size_t)(rows * cols) * 4);
+}
+
+int32_t tkv_hip_quantize_dynamic_int8_rowwise(const float* src, int64_t n_src, int32_t* dst,
+                                              int64_t n_dst, int64_t rows, int64_t cols,
+                                              float* scales_out, int64_t n_scales_out) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    if (n_dst < rows * cols || n_src < rows * cols) return set_error(TKV_HIP_BAD_ARG, "span too small");
+    if (n_scales_out < rows) return set_error(TKV_HIP_BAD_ARG, "scales_out smaller than rows");
+    if (rows == 0) return TKV_HIP_OK;
+    if (cols == 0) {  // am = 1e-8 floor for every row
+        for (int64_t r = 0; r < rows; r++) scales_out[r] = (float)(0.00000001 / 127.0);
+        return TKV_HIP_OK;
+    }
+    void *dx, *dq, *ds;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)(rows * cols) * 4, &dx));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)(rows * cols) * 4, &dq));
+    TKV_RC_TRY(ctx_workspace(c, WS_SMALL, (size_t)rows * 4, &ds));
+    TKV_RC_TRY(launch_quant_rows(c, static_cast<float*>(dx), rows, cols, RM_DYNAMIC, nullptr, dq,
+                                 true, static_cast<float*>(ds), nullptr, 1));
+    TKV_HIP_TRY(hipMemcpyAsync(scales_out, ds, (size_t)rows * 4, hipMemcpyDeviceToHost, c->stream));
+    return download(c, dst, dq, (size_t)(rows * cols) * 4);
+}
+
+int32_t tkv_hip_quantize_fp8_e4m3(const float* src, int64_t n_src, int32_t* dst, int64_t n_dst) {
+    if (n_src < 0 || n_dst < n_src) return set_error(TKV_HIP_BAD_ARG, "dst too small");
+    if (n_src == 0) return TKV_HIP_OK;
+    void *dx, *dq;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)n_src * 4, &dx));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n_src * 4, &dq));
+    TKV_RC_TRY(launch_fp8_encode(c, static_cast<float*>(dx), n_src, nullptr, dq, true));
+    return download(c, dst, dq, (size_t)n_src * 4);
+}
+
+int32_t tkv_hip_dequantize_fp8_e4m3(const int32_t* src, int64_t n_src, float* dst,
+                                    int64_t n_dst) {
+    if (n_src < 0 || n_dst < n_src) return set_error(TKV_HIP_BAD_ARG, "dst too small");
+    if (n_src == 0) return TKV_HIP_OK;
+    void *dq, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)n_src * 4, &dq));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n_src * 4, &dy));
+    TKV_RC_TRY(launch_fp8_decode(c, dq, true, n_src, static_cast<float*>(dy)));
+    return download(c, dst, dy, (size_t)n_src * 4);
+}
+
+int32_t tkv_hip_matmul_int8_symmetric(const int32_t* pa, const int32_t* pw, const float* pbias,
+                                      int64_t n_bias, float* py, int64_t m, int64_t n, int64_t k,
+                                      float scale_a, float scale_w) {
+    return host_gemm_i8(pa, pw, pbias, n_bias, py, false, m, n, k, scale_a, scale_w, nullptr, 0,
+                        TKV_HIP_RECIPE_PRIMARY);
+}
+
+int32_t tkv_hip_matmul_int8_per_channel(const int32_t* pa, const int32_t* pw, const float* pbias,
+                                        int64_t n_bias, float* py, int64_t m, int64_t n,
+                                        int64_t k, float scale_a, const float* scales_w,
+                                        int64_t n_scales) {
+    if (n_scales < n || !scales_w) return set_error(TKV_HIP_BAD_ARG, "scales_w smaller than N");
+    return host_gemm_i8(pa, pw, pbias, n_bias, py, false, m, n, k, scale_a, 0.0f, scales_w,
+                        n_scales, TKV_HIP_RECIPE_PRIMARY);
+}
+
+int32_t tkv_hip_matmul_int8_recipe(const int32_t* pa, const int32_t* pw, const float* pbias,
+                                   int64_t n_bias, float* py, int64_t m, int64_t n, int64_t k,
+                                   float scale_a, float scale_w, const float* scales_w,
+                                   int64_t n_scales, int32_t recipe) {
+    if (scales_w && n_scales < n) return set_error(TKV_HIP_BAD_ARG, "scales_w smaller than N");
+    return host_gemm_i8(pa, pw, pbias, n_bias, py, false, m, n, k, scale_a, scale_w,
+                        n_scales > 0 ? scales_w : nullptr, n_scales, recipe);
+}
+
+int32_t tkv_hip_matmul_int8_accum(const int32_t* pa, const int32_t* pw, int32_t* acc, int64_t m,
+                                  int64_t n, int64_t k) {
+    return host_gemm_i8(pa, pw, nullptr, 0, acc, true, m, n, k, 0.0f, 0.0f, nullptr, 0,
+                        TKV_HIP_RECIPE_PRIMARY);
+}
+
+int32_t tkv_hip_matmul_fp8_e4m3(const int32_t* pa, const int32_t* pw, const float* pbias,
+                                int64_t n_bias, float* py, int64_t m, int64_t n, int64_t k) {
+    if (m < 0 || n < 0 || k < 0) return set_error(TKV_HIP_BAD_ARG, "negative GEMM size");
+    if (m == 0 || n == 0) return TKV_HIP_OK;
+    if (n_bias > 0 && n_bias < n) return set_error(TKV_HIP_BAD_ARG, "bias shorter than N");
+    int64_t kk = k > 0 ? k : 1;
+    int64_t ldk = (kk + 15) & ~int64_t(15);
+    std::vector<int8_t> ha, hw;
+    if (k > 0) {
+        // codes are e4m3 byte - 128: raw byte = code + 128 (0x00 is +0.0)
+        TKV_RC_TRY(pack_codes(pa, m, k, ldk, 128, -128, 127, ha));
+        TKV_RC_TRY(pack_codes(pw, n, k, ldk, 128, -128, 127, hw));
+    } else {
+        ha.assign((size_t)(m * ldk), 0);
+        hw.assign((size_t)(n * ldk), 0);
+    }
+    void *da, *dw, *db = nullptr, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_A, ha.data(), ha.size(), &da));
+    TKV_RC_TRY(upload(c, WS_W, hw.data(), hw.size(), &dw));
+    if (n_bias > 0) TKV_RC_TRY(upload(c, WS_SMALL, pbias, (size_t)n * 4, &db));
+    size_t ybytes = (size_t)(m * n) * 4;
+    TKV_RC_TRY(ctx_workspace(c, WS_Y, ybytes, &dy));
+    TKV_RC_TRY(launch_gemm_f8(c, static_cast<uint8_t*>(da), static_cast<uint8_t*>(dw), m, n, ldk,
+                              nullptr, 0, nullptr, static_cast<float*>(db),
+                              static_cast<float*>(dy)));
+    return download(c, py, dy, ybytes);
+}
+
+int32_t tkv_hip_quantized_gemm(const int32_t* aq, const int32_t* wq, const float* bias,
+                               int64_t n_bias, float* y, int64_t m, int64_t n, int64_t k,
+                               float scale_a, float scale_b, const float* scales_w,
+                               int64_t n_scales) {
+    // session.tkv:693-696: per-channel iff len(scales_w) > 0
+    if (n_scales > 0)
+        return tkv_hip_matmul_int8_per_channel(aq, wq, bias, n_bias, y, m, n, k, scale_a,
+                                               scales_w, n_scales);
+    return tkv_hip_matmul_int8_symmetric(aq, wq, bias, n_bias, y, m, n, k, scale_a, scale_b);
+}
+
+int32_t tkv_hip_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, int64_t nb,
+                               int64_t* y, int64_t ny, int64_t m, int64_t n, int64_t k) {
+    if (m < 0 || n < 0 || k < 0 || na < 0 || nb < 0 || ny < 0)
+        return set_error(TKV_HIP_BAD_ARG, "negative size");
+    if (m == 0 || n == 0) return TKV_HIP_OK;
+    // Out-of-range reads are zero in the reference (session.tkv:2822-2836):
+    // build A [m,k] and B^T [n,k] with those zeros, then one INT32 GEMM.
+    int64_t kk = k > 0 ? k : 1;
+    std::vector<int32_t> A((size_t)(m * kk), 0), Bt((size_t)(n * kk), 0);
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t p = 0; p < k; p++) {
+            int64_t ai = i * k + p;
+            if (ai < na) A[(size_t)(i * kk + p)] = a[ai];
+        }
+    for (int64_t p = 0; p < k; p++)
+        for (int64_t j = 0; j < n; j++) {
+            int64_t bi = p * n + j;
+            if (bi < nb) Bt[(size_t)(j * kk + p)] = b[bi];
+        }
+    std::vector<int32_t> acc((size_t)(m * n));
+    TKV_RC_TRY(host_gemm_i8(A.data(), Bt.data(), nullptr, 0, acc.data(), true, m, n, kk, 0.0f,
+                            0.0f, nullptr, 0, TKV_HIP_RECIPE_PRIMARY));
+    int64_t lim = m * n < ny ? m * n : ny;
+    for (int64_t i = 0; i < lim; i++) y[i] = acc[(size_t)i];
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_quantize_linear(const float* x, int64_t nx, const float* scales, int64_t n_scales,
+                                int64_t zero_point, int64_t outer, int64_t dim, int64_t inner,
+                                int32_t* y) {
+    if (nx < 0 || n_scales < 1) return set_error(TKV_HIP_BAD_ARG, "empty scale");
+    if (n_scales != 1 && (outer < 0 || dim < 1 || inner < 1 || n_scales < dim ||
+                          outer * dim * inner > nx))
+        return set_error(TKV_HIP_BAD_ARG, "per-axis view does not fit the input");
+    int64_t n = n_scales == 1 ? nx : outer * dim * inner;
+    if (n == 0) return TKV_HIP_OK;
+    void *dx, *ds, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, x, (size_t)n * 4, &dx));
+    TKV_RC_TRY(upload(c, WS_SMALL, scales, (size_t)n_scales * 4, &ds));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n * 4, &dy));
+    TKV_RC_TRY(launch_quantize_linear(c, static_cast<float*>(dx), n, static_cast<float*>(ds),
+                                      n_scales, zero_point, dim, inner, static_cast<int32_t*>(dy)));
+    return download(c, y, dy, (size_t)n * 4);
+}
+
+int32_t tkv_hip_dequantize_linear(const int32_t* x, int64_t nx, const float* scales,
+                                  int64_t n_scales, int64_t zero_point, int64_t outer,
+                                  int64_t dim, int64_t inner, float* y) {
+    if (nx < 0 || n_scales < 1) return set_error(TKV_HIP_BAD_ARG, "empty scale");
+    if (n_scales != 1 && (outer < 0 || dim < 1 || inner < 1 || n_scales < dim ||
+                          outer * dim * inner > nx))
+        return set_error(TKV_HIP_BAD_ARG, "per-axis view does not fit the input");
+    int64_t n = n_scales == 1 ? nx : outer * dim * inner;
+    if (n == 0) return TKV_HIP_OK;
+    void *dx, *ds, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, x, (size_t)n * 4, &dx));
+    TKV_RC_TRY(upload(c, WS_SMALL, scales, (size_t)n_scales * 4, &ds));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n * 4, &dy));
+    TKV_RC_TRY(launch_dequantize_linear(c, static_cast<int32_t*>(dx), n, static_cast<float*>(ds),
+                                        n_scales, zero_point, dim, inner, static_cast<float*>(dy)));
+    return download(c, y, dy, (size_t)n * 4);
+}
+
+int32_t tkv_hip_dynamic_quantize_linear(const float* x, int64_t nx, int32_t* y, float* y_scale,
+                                        float* y_zero_point) {
+    if (nx <= 0) return set_error(TKV_HIP_BAD_ARG, "DynamicQuantizeLinear needs a non-empty input");
+    void *dx, *dy;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    TKV_RC_TRY(upload(c, WS_IN, x, (size_t)nx * 4, &dx));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)nx * 4, &dy));
+    TKV_RC_TRY(launch_minmax_tensor(c, static_cast<float*>(dx), nx, MM_DYNAMIC_QL,
+                                    TKV_HIP_RECIPE_PRIMARY, c->params));
+    TKV_RC_TRY(launch_dynamic_ql(c, static_cast<float*>(dx), nx, c->params,
+                                 static_cast<int32_t*>(dy)));
+    tkv_hip_qparams_dev p;
+    TKV_HIP_TRY(hipMemcpyAsync(&p, c->params, sizeof(p), hipMemcpyDeviceToHost, c->stream));
+    TKV_RC_TRY(download(c, y, dy, (size_t)nx * 4));
+    if (y_scale) *y_scale = p.scale;
+    if (y_zero_point) *y_zero_point = (float)p.zero_point;
+    return TKV_HIP_OK;
+}
+
+// ===========================================================================
+// Device-pointer variants
+// ===========================================================================
+
+int32_t tkv_hip_dev_calibrate_minmax(int64_t ctx, const float* x, int64_t n, int32_t symmetric,
+                                     tkv_hip_qparams_dev* params) {
+    if (n <= 0 || !x || !params) return set_error(TKV_HIP_BAD_ARG, "empty input or NULL params");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_minmax_tensor(c, x, n, symmetric ? MM_SYMMETRIC : MM_ASYMMETRIC,
+                                TKV_HIP_RECIPE_PRIMARY, params);
+}
+
+int32_t tkv_hip_dev_calibrate_rows(int64_t ctx, const float* x, int64_t rows, int64_t cols,
+                                   float* scales) {
+    if (rows <= 0 || cols <= 0) return set_error(TKV_HIP_BAD_ARG, "rows/cols must be > 0");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_quant_rows(c, x, rows, cols, RM_CALIBRATE, nullptr, nullptr, false, scales,
+                             nullptr, 1);
+}
+
+int32_t tkv_hip_dev_quantize_int8_tensor(int64_t ctx, const float* x, int64_t n,
+                                         const tkv_hip_qparams_dev* params, int8_t* q) {
+    if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative length");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_quant_i8_tensor(c, x, n, params, q, false);
+}
+
+int32_t tkv_hip_dev_quantize_int8_dynamic_tensor(int64_t ctx, const float* x, int64_t n,
+                                                 int8_t* q, tkv_hip_qparams_dev* params) {
+    if (n <= 0 || !params) return set_error(TKV_HIP_BAD_ARG, "empty input or NULL params");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    TKV_RC_TRY(launch_minmax_tensor(c, x, n, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, params));
+    return launch_quant_i8_tensor(c, x, n, params, q, false);
+}
+
+int32_t tkv_hip_dev_quantize_int8_per_channel(int64_t ctx, const float* x, int64_t rows,
+                                              int64_t cols, const float* scales, int8_t* q) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_quant_rows(c, x, rows, cols, RM_PER_CHANNEL, scales, q, false, nullptr, nullptr,
+                             1);
+}
+
+int32_t tkv_hip_dev_quantize_dynamic_int8_rowwise(int64_t ctx, const float* x, int64_t rows,
+                                                  int64_t cols, int8_t* q, float* scales_out) {
+    if (rows < 0 || cols <= 0) return set_error(TKV_HIP_BAD_ARG, "bad rows/cols");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_quant_rows(c, x, rows, cols, RM_DYNAMIC, nullptr, q, false, scales_out, nullptr,
+                             1);
+}
+
+int32_t tkv_hip_dev_dequantize_int8(int64_t ctx, const int8_t* q, int64_t rows, int64_t cols,
+                                    float scale, const float* scales, float* y) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_dequant_i8(c, q, false, rows, cols, scale, scales, y);
+}
+
+int32_t tkv_hip_dev_quantize_fp8_e4m3(int64_t ctx, const float* x, int64_t n, uint8_t* q) {
+    if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative length");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_fp8_encode(c, x, n, nullptr, q, false);
+}
+
+int32_t tkv_hip_dev_quantize_fp8_e4m3_scaled(int64_t ctx, const float* x, int64_t n,
+                                             const tkv_hip_qparams_dev* params, uint8_t* q) {
+    if (n < 0 || !params) return set_error(TKV_HIP_BAD_ARG, "negative length or NULL params");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_fp8_encode(c, x, n, params, q, false);
+}
+
+int32_t tkv_hip_dev_dequantize_fp8_e4m3(int64_t ctx, const uint8_t* q, int64_t n, float* y) {
+    if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative length");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_fp8_decode(c, q, false, n, y);
+}
+
+int32_t tkv_hip_dev_matmul_int8(int64_t ctx, const int8_t* a, const int8_t* w, int64_t m,
+                                int64_t n, int64_t k, const float* scale_a, int64_t scale_a_stride,
+                                float scale_w, const float* scales_w, const float* bias, float* y,
+                                int32_t recipe) {
+    TKV_RC_TRY(check_recipe(recipe));
+    if (m < 0 || n < 0 || k < 0 || !scale_a || scale_a_stride < 0)
+        return set_error(TKV_HIP_BAD_ARG, "bad GEMM arguments");
+    I8Epilogue ep;
+    ep.mode = scales_w ? EPI_PER_CHANNEL : EPI_SYMMETRIC;
+    ep.recipe = recipe;
+    ep.scale_a = scale_a;
+    ep.scale_a_stride = scale_a_stride;
+    ep.scale_w = scale_w;
+    ep.scales_w = scales_w;
+    ep.bias = bias;
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_gemm_i8(c, a, w, m, n, k, ep, y);
+}
+
+int32_t tkv_hip_dev_matmul_int8_accum(int64_t ctx, const int8_t* a, const int8_t* w, int64_t m,
+                                      int64_t n, int64_t k, int32_t* acc) {
+    if (m < 0 || n < 0 || k < 0) return set_error(TKV_HIP_BAD_ARG, "negative GEMM size");
+    I8Epilogue ep;
+    memset(&ep, 0, sizeof(ep));
+    ep.mode = EPI_ACCUM_I32;
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_gemm_i8(c, a, w, m, n, k, ep, acc);
+}
+
+int32_t tkv_hip_dev_matmul_fp8_e4m3(int64_t ctx, const uint8_t* a, const uint8_t* w, int64_t m,
+                                    int64_t n, int64_t k, const float* scale_a,
+                                    int64_t scale_a_stride, const float* scales_w,
+                                    const float* bias, float* y) {
+    if (m < 0 || n < 0 || k < 0 || scale_a_stride < 0)
+        return set_error(TKV_HIP_BAD_ARG, "bad GEMM arguments");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_gemm_f8(c, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y);
+}
+
+}  // extern "C"

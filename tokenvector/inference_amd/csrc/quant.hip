@@ -1,0 +1,611 @@
+// quant.hip -- HBM-bound kernels of the PTQ path on gfx950:
+//   absmax / min-max calibration (per tensor, per row), f32 -> int8 quantize
+//   (per tensor, per channel, dynamic per row), f32 -> e4m3 encode,
+//   dequantize, and code-layout conversions for the host-pointer mirrors.
+//
+// Layout: f32 inputs are read as 16-byte float4 loads, four per thread per
+// loop trip for memory-level parallelism; int8 / e4m3 outputs leave as one
+// 32-bit store per float4.  Reductions use wave64 shuffles, then LDS, then a
+// last-block-done finalize (no grid barrier, no per-call memset).
+//
+// Numerics restate tv/quantization/engine.tkv and types.tkv exactly: f64
+// products and reciprocals where the reference computes in f64, round half to
+// even, saturating clamp.  Compiled with -ffp-contract=off.
+#include <float.h>
+
+#include "tkv_device.h"
+#include "tkv_internal.h"
+
+namespace tkv {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+// ---------------------------------------------------------------------------
+// Calibration finalize (engine.tkv:13-36 and session.tkv:2853-2876).
+// mn / mx are the reference's f64 locals holding f32 values.
+// ---------------------------------------------------------------------------
+__device__ void finalize_minmax(double mn, double mx, int mode, int recipe,
+                                tkv_hip_qparams_dev* out) {
+    tkv_hip_qparams_dev p;
+    p.reserved = 0.0;
+    if (mode == MM_SYMMETRIC) {
+        double am = fabs(mx);
+        if (fabs(mn) > am) am = fabs(mn);
+        if (am < 0.00000001) am = 0.00000001;
+        float scale = (float)(am / 127.0);
+        p.scale = scale;
+        p.min_val = (float)(-am);
+        p.max_val = (float)am;
+        p.zero_point = 0;
+        // quantize_int8_symmetric(x, q, p.scale): engine.tkv:219-222
+        if ((double)scale > 0.00000001)
+            p.inv = recipe == TKV_HIP_RECIPE_PRIMARY ? (double)(1.0f / scale) : 1.0 / (double)scale;
+        else
+            p.inv = 1.0 / 0.00000001;
+    } else if (mode == MM_ASYMMETRIC) {
+        if (fabs(mx - mn) < 0.00000001) mx = mn + 0.00000001;
+        double sc = (mx - mn) / 255.0;
+        double z = __builtin_rint(-mn / sc);
+        if (z != z) z = 0.0;
+        z = z - 128.0;
+        z = z < -128.0 ? -128.0 : (z > 127.0 ? 127.0 : z);
+        p.scale = (float)sc;
+        p.zero_point = (int32_t)z;
+        p.min_val = (float)mn;
+        p.max_val = (float)mx;
+        p.inv = 1.0 / sc;
+    } else if (mode == MM_FP8) {
+        // Per-tensor FP8 scale (extension, not in the reference): amax maps
+        // to kFp8Target; inv is the f32 reciprocal the scaled encode uses.
+        double am = fabs(mx);
+        if (fabs(mn) > am) am = fabs(mn);
+        if (am < 0.00000001) am = 0.00000001;
+        float scale = (float)(am / (double)kFp8Target);
+        p.scale = scale;
+        p.min_val = (float)(-am);
+        p.max_val = (float)am;
+        p.zero_point = 0;
+        p.inv = (double)(1.0f / scale);
+    } else {  // MM_DYNAMIC_QL
+        if (mn > 0.0) mn = 0.0;
+        if (mx < 0.0) mx = 0.0;
+        if (mx - mn < 0.00000001) mx = mn + 0.00000001;
+        double sc = (mx - mn) / 255.0;
+        double z = __builtin_rint(-mn / sc);
+        if (z != z) z = 0.0;
+        z = z < 0.0 ? 0.0 : (z > 255.0 ? 255.0 : z);
+        p.scale = (float)sc;
+        p.zero_point = (int32_t)z;
+        p.min_val = (float)mn;
+        p.max_val = (float)mx;
+        p.inv = 1.0 / sc;
+        p.reserved = sc;  // the unrounded f64 scale the node divides by
+    }
+    *out = p;
+}
+
+__device__ __forceinline__ void mm_acc(float v, int64_t idx, bool track_zero, float& mn,
+                                       float& mx, unsigned long long& zi) {
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+    if (track_zero && v == 0.0f && (unsigned long long)idx < zi) zi = (unsigned long long)idx;
+}
+
+// Per-tensor min / max (+ first zero) with last-block finalize.
+__global__ __launch_bounds__(kBlock) void k_minmax_tensor(
+    const float* __restrict__ x, int64_t n, int vec, int track_zero, int mode, int recipe,
+    RedPartial* __restrict__ partials, unsigned int* __restrict__ counter,
+    tkv_hip_qparams_dev* __restrict__ out) {
+    float mn = FLT_MAX * 2.0f, mx = -FLT_MAX * 2.0f;  // +-inf
+    unsigned long long zi = ~0ull;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    int64_t n4 = vec ? n / 4 : 0;
+    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) v[u] = x4[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            int64_t b = (i + u * stride) * 4;
+            mm_acc(v[u].x, b + 0, track_zero, mn, mx, zi);
+            mm_acc(v[u].y, b + 1, track_zero, mn, mx, zi);
+            mm_acc(v[u].z, b + 2, track_zero, mn, mx, zi);
+            mm_acc(v[u].w, b + 3, track_zero, mn, mx, zi);
+        }
+    }
+    for (; i < n4; i += stride) {
+        float4 v = x4[i];
+        mm_acc(v.x, i * 4 + 0, track_zero, mn, mx, zi);
+        mm_acc(v.y, i * 4 + 1, track_zero, mn, mx, zi);
+        mm_acc(v.z, i * 4 + 2, track_zero, mn, mx, zi);
+        mm_acc(v.w, i * 4 + 3, track_zero, mn, mx, zi);
+    }
+    for (int64_t j = n4 * 4 + tid; j < n; j += stride) mm_acc(x[j], j, track_zero, mn, mx, zi);
+
+    __shared__ float s_mn[kBlock / 64], s_mx[kBlock / 64];
+    __shared__ unsigned long long s_zi[kBlock / 64];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    zi = wave_min_u64(zi);
+    if (lane == 0) {
+        s_mn[wave] = mn;
+        s_mx[wave] = mx;
+        s_zi[wave] = zi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kBlock / 64; w++) {
+            mn = fminf(mn, s_mn[w]);
+            mx = fmaxf(mx, s_mx[w]);
+            zi = s_zi[w] < zi ? s_zi[w] : zi;
+        }
+        RedPartial p;
+        p.mn = mn;
+        p.mx = mx;
+        p.zidx = zi;
+        partials[blockIdx.x] = p;
+        __threadfence();
+        unsigned int prev = atomicAdd(counter, 1u);
+        s_last = (prev == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    mn = FLT_MAX * 2.0f;
+    mx = -FLT_MAX * 2.0f;
+    zi = ~0ull;
+    for (int b = threadIdx.x; b < (int)gridDim.x; b += kBlock) {
+        RedPartial p = partials[b];
+        mn = fminf(mn, p.mn);
+        mx = fmaxf(mx, p.mx);
+        zi = p.zidx < zi ? p.zidx : zi;
+    }
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    zi = wave_min_u64(zi);
+    __syncthreads();
+    if (lane == 0) {
+        s_mn[wave] = mn;
+        s_mx[wave] = mx;
+        s_zi[wave] = zi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kBlock / 64; w++) {
+            mn = fminf(mn, s_mn[w]);
+            mx = fmaxf(mx, s_mx[w]);
+            zi = s_zi[w] < zi ? s_zi[w] : zi;
+        }
+        double dmn = mn, dmx = mx;
+        // The reference keeps the first element reaching the extreme; values
+        // that compare equal are bit-identical except +-0, so a zero extreme
+        // takes the sign of the first zero in index order.
+        if (track_zero && zi != ~0ull) {
+            double z = x[zi];
+            if (mn == 0.0f) dmn = z;
+            if (mx == 0.0f) dmx = z;
+        }
+        finalize_minmax(dmn, dmx, mode, recipe, out);
+        *counter = 0u;
+    }
+}
+
+int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe,
+                         tkv_hip_qparams_dev* out) {
+    int vec = aligned(x, 16) ? 1 : 0;
+    int64_t work = vec ? n / 4 : n;
+    int64_t blocks = ceil_div(work, (int64_t)kBlock * kUnroll);
+    int64_t cap = (int64_t)c->num_cus * 8;
+    if (cap > kMaxReduceBlocks) cap = kMaxReduceBlocks;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    // Only the asymmetric QuantParams expose the sign of a zero extreme.
+    int track_zero = (mode == MM_ASYMMETRIC) ? 1 : 0;
+    hipLaunchKernelGGL(k_minmax_tensor, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, x, n,
+                       vec, track_zero, mode, recipe, c->partials, c->counter, out);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Per-tensor int8 quantize: q = clamp(rne(x * inv), +-127), inv from params
+// (engine.tkv:216-226).  OUT_I32 writes the reference's int32 codes.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+template <bool OUT_I32>
+__device__ __forceinline__ void store4(void* q, int64_t i4, int a, int b, int c, int d) {
+    if (OUT_I32) {
+        reinterpret_cast<int4*>(q)[i4] = make_int4(a, b, c, d);
+    } else {
+        reinterpret_cast<uint32_t*>(q)[i4] = pack4(a, b, c, d);
+    }
+}
+
+template <bool OUT_I32>
+__device__ __forceinline__ void store1(void* q, int64_t i, int a) {
+    if (OUT_I32)
+        reinterpret_cast<int32_t*>(q)[i] = a;
+    else
+        reinterpret_cast<int8_t*>(q)[i] = (int8_t)a;
+}
+
+template <bool OUT_I32>
+__global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restrict__ x,
+                                                            int64_t n, int vec,
+                                                            const tkv_hip_qparams_dev* __restrict__ p,
+                                                            void* __restrict__ q) {
+    const double inv = p->inv;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    int64_t n4 = vec ? n / 4 : 0;
+    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) v[u] = x4[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++)
+            store4<OUT_I32>(q, i + u * stride, rne_clamp((double)v[u].x * inv, -127.0, 127.0),
+                            rne_clamp((double)v[u].y * inv, -127.0, 127.0),
+                            rne_clamp((double)v[u].z * inv, -127.0, 127.0),
+                            rne_clamp((double)v[u].w * inv, -127.0, 127.0));
+    }
+    for (; i < n4; i += stride) {
+        float4 v = x4[i];
+        store4<OUT_I32>(q, i, rne_clamp((double)v.x * inv, -127.0, 127.0),
+                        rne_clamp((double)v.y * inv, -127.0, 127.0),
+                        rne_clamp((double)v.z * inv, -127.0, 127.0),
+                        rne_clamp((double)v.w * inv, -127.0, 127.0));
+    }
+    for (int64_t j = n4 * 4 + tid; j < n; j += stride)
+        store1<OUT_I32>(q, j, rne_clamp((double)x[j] * inv, -127.0, 127.0));
+}
+
+static int64_t stream_blocks(Ctx* c, int64_t work) {
+    int64_t blocks = ceil_div(work, (int64_t)kBlock * kUnroll);
+    int64_t cap = (int64_t)c->num_cus * 16;
+    if (blocks > cap) blocks = cap;
+    return blocks < 1 ? 1 : blocks;
+}
+
+int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* p,
+                           void* q, bool out_i32) {
+    if (n <= 0) return TKV_HIP_OK;
+    int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
+    int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
+    if (out_i32)
+        hipLaunchKernelGGL(k_quant_i8_tensor<true>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, p, q);
+    else
+        hipLaunchKernelGGL(k_quant_i8_tensor<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, p, q);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Row kernels: one wave64 per row.
+//   RM_DYNAMIC        quantize_dynamic_int8_rowwise   engine.tkv:266-285
+//   RM_PER_CHANNEL    quantize_int8_per_channel       engine.tkv:237-250
+//   RM_CALIBRATE      symmetric per-row scales        engine.tkv:202-213
+//   RM_CALIBRATE_FULL calibrate_minmax per row (both modes), full params
+// The second pass re-reads the row from cache (rows are 3-12 KB).
+// ---------------------------------------------------------------------------
+template <bool OUT_I32>
+__global__ __launch_bounds__(kBlock) void k_rows(const float* __restrict__ x, int64_t rows,
+                                                 int64_t cols, int vec, int mode,
+                                                 const float* __restrict__ scales_in,
+                                                 void* __restrict__ q,
+                                                 float* __restrict__ scales_out,
+                                                 tkv_hip_qparams_dev* __restrict__ row_params,
+                                                 int symmetric) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* __restrict__ xr = x + r * cols;
+    double inv = 0.0;
+    if (mode != RM_PER_CHANNEL) {
+        float mn = FLT_MAX * 2.0f, mx = -FLT_MAX * 2.0f;
+        unsigned long long zi = ~0ull;
+        const bool tz = (mode == RM_CALIBRATE_FULL && !symmetric);
+        if (vec) {
+            const float4* __restrict__ x4 = reinterpret_cast<const float4*>(xr);
+            for (int64_t c4 = lane; c4 < cols / 4; c4 += 64) {
+                float4 v = x4[c4];
+                mm_acc(v.x, c4 * 4 + 0, tz, mn, mx, zi);
+                mm_acc(v.y, c4 * 4 + 1, tz, mn, mx, zi);
+                mm_acc(v.z, c4 * 4 + 2, tz, mn, mx, zi);
+                mm_acc(v.w, c4 * 4 + 3, tz, mn, mx, zi);
+            }
+        } else {
+            for (int64_t c = lane; c < cols; c += 64) mm_acc(xr[c], c, tz, mn, mx, zi);
+        }
+        mn = wave_min(mn);
+        mx = wave_max(mx);
+        if (mode == RM_CALIBRATE_FULL) {
+            zi = wave_min_u64(zi);
+            if (lane == 0) {
+                double dmn = mn, dmx = mx;
+                if (tz && zi != ~0ull) {
+                    double z = xr[zi];
+                    if (mn == 0.0f) dmn = z;
+                    if (mx == 0.0f) dmx = z;
+                }
+                finalize_minmax(dmn, dmx, symmetric ? MM_SYMMETRIC : MM_ASYMMETRIC,
+                                TKV_HIP_RECIPE_PRIMARY, row_params + r);
+            }
+            return;
+        }
+        double am = fabs((double)mx);
+        if (fabs((double)mn) > am) am = fabs((double)mn);
+        if (am < 0.00000001) am = 0.00000001;
+        double sc = am / 127.0;
+        if (mode == RM_CALIBRATE) {
+            if (lane == 0) scales_out[r] = (float)sc;
+            return;
+        }
+        if (lane == 0) scales_out[r] = (float)sc;  // RM_DYNAMIC
+        inv = 1.0 / sc;
+    } else {
+        double sc = (double)scales_in[r];
+        if (sc <= 0.00000001) sc = 0.00000001;
+        inv = 1.0 / sc;
+    }
+    if (vec) {
+        const float4* __restrict__ x4 = reinterpret_cast<const float4*>(xr);
+        const int64_t base4 = r * (cols / 4);
+        for (int64_t c4 = lane; c4 < cols / 4; c4 += 64) {
+            float4 v = x4[c4];
+            store4<OUT_I32>(q, base4 + c4, rne_clamp((double)v.x * inv, -127.0, 127.0),
+                            rne_clamp((double)v.y * inv, -127.0, 127.0),
+                            rne_clamp((double)v.z * inv, -127.0, 127.0),
+                            rne_clamp((double)v.w * inv, -127.0, 127.0));
+        }
+    } else {
+        for (int64_t c = lane; c < cols; c += 64)
+            store1<OUT_I32>(q, r * cols + c, rne_clamp((double)xr[c] * inv, -127.0, 127.0));
+    }
+}
+
+int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mode,
+                      const float* scales_in, void* q, bool out_i32, float* scales_out,
+                      tkv_hip_qparams_dev* row_params, int symmetric) {
+    if (rows <= 0 || cols <= 0) return TKV_HIP_OK;
+    bool q_ok = (mode == RM_CALIBRATE || mode == RM_CALIBRATE_FULL) ? true
+                                                                     : aligned(q, out_i32 ? 16 : 4);
+    int vec = (cols % 4 == 0 && aligned(x, 16) && q_ok) ? 1 : 0;
+    int64_t blocks = ceil_div(rows, kBlock / 64);
+    if (out_i32)
+        hipLaunchKernelGGL(k_rows<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, x,
+                           rows, cols, vec, mode, scales_in, q, scales_out, row_params, symmetric);
+    else
+        hipLaunchKernelGGL(k_rows<false>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, x,
+                           rows, cols, vec, mode, scales_in, q, scales_out, row_params, symmetric);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Dequantize: y = fl32(q * s) with the product in f64 (engine.tkv:229-262).
+// ---------------------------------------------------------------------------
+template <bool IN_I32>
+__global__ __launch_bounds__(kBlock) void k_dequant_i8(const void* __restrict__ q, int64_t rows,
+                                                       int64_t cols, float scale,
+                                                       const float* __restrict__ scales,
+                                                       float* __restrict__ y) {
+    const int64_t n = rows * cols;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int v = IN_I32 ? reinterpret_cast<const int32_t*>(q)[i]
+                       : (int)reinterpret_cast<const int8_t*>(q)[i];
+        float s = scales ? scales[i / cols] : scale;
+        y[i] = (float)((double)v * (double)s);
+    }
+}
+
+int launch_dequant_i8(Ctx* c, const void* q, bool in_i32, int64_t rows, int64_t cols,
+                      float scale, const float* scales, float* y) {
+    int64_t n = rows * cols;
+    if (n <= 0) return TKV_HIP_OK;
+    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    if (in_i32)
+        hipLaunchKernelGGL(k_dequant_i8<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
+                           q, rows, cols, scale, scales, y);
+    else
+        hipLaunchKernelGGL(k_dequant_i8<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, q, rows, cols, scale, scales, y);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// e4m3 encode (matmul.tkv:60-66 / types.tkv:154-191).  Raw bytes out, or the
+// reference's int32 codes (byte - 128).  With `scaled` the input is first
+// multiplied by fl32(1 / scale) in f32 (extension for per-tensor FP8).
+// ---------------------------------------------------------------------------
+template <bool OUT_I32>
+__device__ __forceinline__ void store4_fp8(void* q, int64_t i4, uint32_t a, uint32_t b,
+                                           uint32_t c, uint32_t d) {
+    if (OUT_I32)
+        reinterpret_cast<int4*>(q)[i4] =
+            make_int4((int)a - 128, (int)b - 128, (int)c - 128, (int)d - 128);
+    else
+        reinterpret_cast<uint32_t*>(q)[i4] = a | (b << 8) | (c << 16) | (d << 24);
+}
+
+template <bool OUT_I32>
+__global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__ x, int64_t n,
+                                                       int vec,
+                                                       const tkv_hip_qparams_dev* __restrict__ sp,
+                                                       void* __restrict__ q) {
+    const float mul = sp ? 1.0f / sp->scale : 1.0f;
+    const bool scaled = sp != nullptr;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    int64_t n4 = vec ? n / 4 : 0;
+    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) v[u] = x4[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            if (scaled) {
+                v[u].x *= mul;
+                v[u].y *= mul;
+                v[u].z *= mul;
+                v[u].w *= mul;
+            }
+            store4_fp8<OUT_I32>(q, i + u * stride, e4m3_encode(v[u].x), e4m3_encode(v[u].y),
+                                e4m3_encode(v[u].z), e4m3_encode(v[u].w));
+        }
+    }
+    for (; i < n4; i += stride) {
+        float4 v = x4[i];
+        if (scaled) {
+            v.x *= mul;
+            v.y *= mul;
+            v.z *= mul;
+            v.w *= mul;
+        }
+        store4_fp8<OUT_I32>(q, i, e4m3_encode(v.x), e4m3_encode(v.y), e4m3_encode(v.z),
+                            e4m3_encode(v.w));
+    }
+    for (int64_t j = n4 * 4 + tid; j < n; j += stride) {
+        float v = x[j];
+        if (scaled) v *= mul;
+        uint32_t e = e4m3_encode(v);
+        if (OUT_I32)
+            reinterpret_cast<int32_t*>(q)[j] = (int)e - 128;
+        else
+            reinterpret_cast<uint8_t*>(q)[j] = (uint8_t)e;
+    }
+}
+
+int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* scaled,
+                      void* q, bool out_i32) {
+    if (n <= 0) return TKV_HIP_OK;
+    int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
+    int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
+    if (out_i32)
+        hipLaunchKernelGGL(k_fp8_encode<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
+                           x, n, vec, scaled, q);
+    else
+        hipLaunchKernelGGL(k_fp8_encode<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, scaled, q);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+template <bool IN_I32>
+__global__ __launch_bounds__(kBlock) void k_fp8_decode(const void* __restrict__ q, int64_t n,
+                                                       float* __restrict__ y) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        uint32_t v = IN_I32 ? (uint32_t)(reinterpret_cast<const int32_t*>(q)[i] + 128)
+                            : (uint32_t)reinterpret_cast<const uint8_t*>(q)[i];
+        y[i] = e4m3_decode_ref(v & 0xffu);
+    }
+}
+
+int launch_fp8_decode(Ctx* c, const void* q, bool in_i32, int64_t n, float* y) {
+    if (n <= 0) return TKV_HIP_OK;
+    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    if (in_i32)
+        hipLaunchKernelGGL(k_fp8_decode<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
+                           q, n, y);
+    else
+        hipLaunchKernelGGL(k_fp8_decode<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, q, n, y);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Code layout conversions for the host mirrors: int32 codes (List<int>) to
+// packed int8 rows with a padded leading dimension, and back.  code_bias
+// +128 maps the reference's FP8 codes to raw e4m3 bytes.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void k_i32_to_i8(const int32_t* __restrict__ src,
+                                                      int64_t rows, int64_t cols, int64_t ld_src,
+                                                      int8_t* __restrict__ dst, int64_t ld_dst,
+                                                      int code_bias) {
+    const int64_t n = rows * ld_dst;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t r = i / ld_dst, cidx = i - r * ld_dst;
+        int v = cidx < cols ? src[r * ld_src + cidx] + code_bias : 0;
+        dst[i] = (int8_t)v;
+    }
+}
+
+int launch_i32_to_i8(Ctx* c, const int32_t* src, int64_t rows, int64_t cols, int64_t ld_src,
+                     int8_t* dst, int64_t ld_dst, int code_bias) {
+    int64_t n = rows * ld_dst;
+    if (n <= 0) return TKV_HIP_OK;
+    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    hipLaunchKernelGGL(k_i32_to_i8, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, src, rows,
+                       cols, ld_src, dst, ld_dst, code_bias);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+__global__ __launch_bounds__(kBlock) void k_i8_to_i32(const int8_t* __restrict__ src, int64_t n,
+                                                      int32_t* __restrict__ dst, int code_bias) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        dst[i] = (int32_t)src[i] + code_bias;
+}
+
+int launch_i8_to_i32(Ctx* c, const int8_t* src, int64_t n, int32_t* dst, int code_bias) {
+    if (n <= 0) return TKV_HIP_OK;
+    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    hipLaunchKernelGGL(k_i8_to_i32, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, src, n,
+                       dst, code_bias);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// src int32 [rows, cols] (row-major) -> dst int8 [cols, ld_dst] (transposed,
+// zero-padded to ld_dst >= rows).  32x32 tiles through LDS.
+__global__ __launch_bounds__(kBlock) void k_i32_to_i8_transpose(const int32_t* __restrict__ src,
+                                                                int64_t rows, int64_t cols,
+                                                                int8_t* __restrict__ dst,
+                                                                int64_t ld_dst) {
+    __shared__ int8_t tile[32][33];
+    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int j = ty; j < 32; j += 8) {
+        int64_t r = r0 + j, cc = c0 + tx;
+        tile[j][tx] = (r < rows && cc < cols) ? (int8_t)src[r * cols + cc] : (int8_t)0;
+    }
+    __syncthreads();
+    for (int j = ty; j < 32; j += 8) {
+        int64_t orow = c0 + j, ocol = r0 + tx;  // dst[orow][ocol] = src[ocol][orow]
+        if (orow < cols && ocol < ld_dst) dst[orow * ld_dst + ocol] = tile[tx][j];
+    }
+}
+
+int launch_i32_to_i8_transpose(Ctx* c, const int32_t* src, int64_t rows, int64_t cols,
+                               int8_t* dst, int64_t ld_dst) {
+    if (rows <= 0 || cols <= 0) return TKV_HIP_OK;
+    dim3 grid((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(ld_dst, 32));
+    hipLaunchKernelGGL(k_i32_to_i8_transpose, grid, dim3(kBlock), 0, c->stream, src, rows, cols,
+                       dst, ld_dst);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+}  // namespace tkv

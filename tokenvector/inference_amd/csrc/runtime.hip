@@ -1,0 +1,281 @@
+// runtime.hip -- contexts, errors, device memory and events of libtkv_hip.
+//
+// No reference counterpart: this is the plumbing the reference's native
+// DLLs keep implicit (stream, workspace, error text).  State lives in
+// explicit contexts; the only process-wide values are read-only after first
+// use (the environment gate) or per-thread (last error, default context).
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "tkv_internal.h"
+
+namespace tkv {
+
+static thread_local std::string t_last_error;
+
+int set_error(int rc, const std::string& msg) {
+    t_last_error = msg;
+    return rc;
+}
+
+int fail_hip(hipError_t e, const char* what, const char* file, int line) {
+    char buf[512];
+    snprintf(buf, sizeof(buf), "%s failed: %s (%s:%d)", what, hipGetErrorString(e), file, line);
+    int rc = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? TKV_HIP_OOM
+                                                                          : TKV_HIP_DEVICE_ERROR;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) rc = TKV_HIP_NO_DEVICE;
+    return set_error(rc, buf);
+}
+
+bool hip_path_enabled() {
+    static const bool enabled = [] {
+        const char* v = getenv("TKV_QUANT_HIP");
+        return !(v && v[0] == '0' && v[1] == '\0');
+    }();
+    return enabled;
+}
+
+static int check_device(int device, int* num_cus) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return set_error(TKV_HIP_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count)
+        return set_error(TKV_HIP_NO_DEVICE, "device index out of range");
+    hipDeviceProp_t prop;
+    TKV_HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(TKV_HIP_NO_DEVICE,
+                         std::string("libtkv_hip is built for gfx950, device is ") + prop.gcnArchName);
+    *num_cus = prop.multiProcessorCount;
+    return TKV_HIP_OK;
+}
+
+int ctx_create(int device, Ctx** out) {
+    int cus = 0;
+    TKV_RC_TRY(check_device(device, &cus));
+    TKV_HIP_TRY(hipSetDevice(device));
+    Ctx* c = new Ctx();
+    c->device = device;
+    c->num_cus = cus;
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail_hip(e, "hipStreamCreateWithFlags", __FILE__, __LINE__);
+    }
+    c->stream = c->own_stream;
+    size_t red_bytes = sizeof(RedPartial) * kMaxReduceBlocks + 256 + sizeof(tkv_hip_qparams_dev) * 64;
+    void* red = nullptr;
+    e = hipMalloc(&red, red_bytes);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return fail_hip(e, "hipMalloc(reduction scratch)", __FILE__, __LINE__);
+    }
+    c->partials = static_cast<RedPartial*>(red);
+    c->counter = reinterpret_cast<unsigned int*>(static_cast<char*>(red) +
+                                                 sizeof(RedPartial) * kMaxReduceBlocks);
+    c->params = reinterpret_cast<tkv_hip_qparams_dev*>(static_cast<char*>(red) +
+                                                       sizeof(RedPartial) * kMaxReduceBlocks + 256);
+    // One-time zeroing at creation (never inside a caller's stream capture).
+    e = hipMemset(red, 0, red_bytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(red);
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return fail_hip(e, "hipMemset(reduction scratch)", __FILE__, __LINE__);
+    }
+    *out = c;
+    return TKV_HIP_OK;
+}
+
+int ctx_destroy(Ctx* c) {
+    if (!c) return TKV_HIP_OK;
+    // Teardown: errors here leave nothing the caller can act on.
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (int i = 0; i < Ctx::kSlots; i++)
+        if (c->ws[i]) (void)hipFree(c->ws[i]);
+    if (c->partials) (void)hipFree(c->partials);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return TKV_HIP_OK;
+}
+
+// Default contexts are per thread and intentionally never destroyed: HIP's
+// own teardown at process exit may run before thread_local destructors.
+static thread_local Ctx* t_default_ctx = nullptr;
+
+int ctx_get(int64_t handle, Ctx** out) {
+    if (handle != 0) {
+        *out = reinterpret_cast<Ctx*>(handle);
+        TKV_HIP_TRY(hipSetDevice((*out)->device));
+        return TKV_HIP_OK;
+    }
+    if (!t_default_ctx) {
+        int dev = 0;
+        if (const char* v = getenv("TKV_HIP_DEVICE")) dev = atoi(v);
+        TKV_RC_TRY(ctx_create(dev, &t_default_ctx));
+    }
+    *out = t_default_ctx;
+    TKV_HIP_TRY(hipSetDevice(t_default_ctx->device));
+    return TKV_HIP_OK;
+}
+
+int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out) {
+    if (bytes == 0) bytes = 256;
+    if (c->ws_bytes[slot] < bytes) {
+        if (c->ws[slot]) {
+            TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+            TKV_HIP_TRY(hipFree(c->ws[slot]));
+            c->ws[slot] = nullptr;
+            c->ws_bytes[slot] = 0;
+        }
+        size_t sz = (bytes + 0xFFFFF) & ~size_t(0xFFFFF);
+        TKV_HIP_TRY(hipMalloc(&c->ws[slot], sz));
+        c->ws_bytes[slot] = sz;
+    }
+    *out = c->ws[slot];
+    return TKV_HIP_OK;
+}
+
+}  // namespace tkv
+
+using namespace tkv;
+
+extern "C" {
+
+int32_t tkv_hip_version(void) { return 100; }
+
+int32_t tkv_hip_device_count(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+    int n = 0;
+    for (int i = 0; i < count; i++) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, i) == hipSuccess &&
+            strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+            n++;
+    }
+    return n;
+}
+
+int32_t tkv_hip_last_error(char* buf, int32_t len) {
+    const std::string& s = t_last_error;
+    if (buf && len > 0) {
+        size_t n = s.size() < (size_t)(len - 1) ? s.size() : (size_t)(len - 1);
+        memcpy(buf, s.data(), n);
+        buf[n] = '\0';
+    }
+    return (int32_t)s.size();
+}
+
+int32_t tkv_hip_ctx_create(int32_t device, int64_t* ctx_out) {
+    if (!ctx_out) return set_error(TKV_HIP_BAD_ARG, "ctx_out is NULL");
+    Ctx* c = nullptr;
+    TKV_RC_TRY(ctx_create(device, &c));
+    *ctx_out = reinterpret_cast<int64_t>(c);
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_ctx_destroy(int64_t ctx) {
+    if (ctx == 0) return TKV_HIP_OK;
+    return ctx_destroy(reinterpret_cast<Ctx*>(ctx));
+}
+
+int32_t tkv_hip_ctx_set_stream(int64_t ctx, void* stream) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    c->stream = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_ctx_get_stream(int64_t ctx, void** stream_out) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    *stream_out = c->stream;
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_ctx_synchronize(int64_t ctx) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_malloc(int64_t ctx, int64_t bytes, void** ptr_out) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (bytes < 0 || !ptr_out) return set_error(TKV_HIP_BAD_ARG, "bad malloc arguments");
+    TKV_HIP_TRY(hipMalloc(ptr_out, bytes > 0 ? (size_t)bytes : 256));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_free(int64_t ctx, void* ptr) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (ptr) {
+        TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+        TKV_HIP_TRY(hipFree(ptr));
+    }
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_memcpy_h2d(int64_t ctx, void* dst, const void* src, int64_t bytes) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (bytes <= 0) return TKV_HIP_OK;
+    TKV_HIP_TRY(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, c->stream));
+    TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_memcpy_d2h(int64_t ctx, void* dst, const void* src, int64_t bytes) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (bytes <= 0) return TKV_HIP_OK;
+    TKV_HIP_TRY(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, c->stream));
+    TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_memset(int64_t ctx, void* dst, int32_t value, int64_t bytes) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (bytes <= 0) return TKV_HIP_OK;
+    TKV_HIP_TRY(hipMemsetAsync(dst, value, (size_t)bytes, c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_event_create(int64_t* ev_out) {
+    hipEvent_t e;
+    TKV_HIP_TRY(hipEventCreate(&e));
+    *ev_out = reinterpret_cast<int64_t>(e);
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_event_destroy(int64_t ev) {
+    if (ev) TKV_HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_event_record(int64_t ctx, int64_t ev) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    TKV_HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_event_elapsed_ms(int64_t ev_start, int64_t ev_end, float* ms_out) {
+    TKV_HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev_end)));
+    TKV_HIP_TRY(hipEventElapsedTime(ms_out, reinterpret_cast<hipEvent_t>(ev_start),
+                                    reinterpret_cast<hipEvent_t>(ev_end)));
+    return TKV_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+// tkv_internal.h -- shared host/device internals of libtkv_hip (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstddef>
+#include <string>
+
+#include "../../../include/tkv_hip.h"
+
+namespace tkv {
+
+// ---------------------------------------------------------------------------
+// Errors: one message per calling thread, rc codes from tkv_hip.h.
+// ---------------------------------------------------------------------------
+int set_error(int rc, const std::string& msg);
+int fail_hip(hipError_t e, const char* what, const char* file, int line);
+
+#define TKV_HIP_TRY(expr)                                                  \
+    do {                                                                   \
+        hipError_t _tkv_e = (expr);                                        \
+        if (_tkv_e != hipSuccess)                                          \
+            return ::tkv::fail_hip(_tkv_e, #expr, __FILE__, __LINE__);     \
+    } while (0)
+
+#define TKV_RC_TRY(expr)              \
+    do {                              \
+        int _tkv_rc = (expr);         \
+        if (_tkv_rc != TKV_HIP_OK)    \
+            return _tkv_rc;           \
+    } while (0)
+
+#define TKV_LAUNCH_CHECK() TKV_HIP_TRY(hipGetLastError())
+
+// ---------------------------------------------------------------------------
+// Context: device, stream, grow-only workspaces.  A context is driven by one
+// thread at a time; the default context of each thread is thread_local.
+// ---------------------------------------------------------------------------
+constexpr int kMaxReduceBlocks = 2048;
+
+struct RedPartial {
+    float mn;
+    float mx;
+    unsigned long long zidx;  // first index holding a zero (either sign)
+};
+
+struct Ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int num_cus = 256;
+    // reduction scratch: kMaxReduceBlocks partials, then one counter; the
+    // counter is zeroed at creation and re-zeroed by the last block of every
+    // reduction, so it needs no per-call clearing.
+    RedPartial* partials = nullptr;
+    unsigned int* counter = nullptr;
+    tkv_hip_qparams_dev* params = nullptr;  // 64 slots of per-call params
+    // grow-only workspaces
+    static constexpr int kSlots = 8;
+    void* ws[kSlots] = {};
+    size_t ws_bytes[kSlots] = {};
+};
+
+int ctx_create(int device, Ctx** out);
+int ctx_destroy(Ctx* c);
+// ctx handle 0 -> calling thread's default context (device from
+// TKV_HIP_DEVICE, default 0).
+int ctx_get(int64_t handle, Ctx** out);
+// Device workspace slot `slot` of at least `bytes` (contents undefined).
+int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out);
+// Environment gate: TKV_QUANT_HIP=0 turns every host mirror into a
+// TKV_HIP_UNSUPPORTED return so .tkv callers keep their own loops.
+bool hip_path_enabled();
+
+// ---------------------------------------------------------------------------
+// Launch helpers
+// ---------------------------------------------------------------------------
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Kernel-family launchers (implemented in the .hip files).
+// quant.hip
+int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe,
+                         tkv_hip_qparams_dev* out);
+enum MinMaxMode { MM_SYMMETRIC = 0, MM_ASYMMETRIC = 1, MM_DYNAMIC_QL = 2, MM_FP8 = 3 };
+// FP8 scaling target: amax maps to 240, the largest e4m3 value the
+// reference encoder reaches without its >= 248 saturation step.
+constexpr float kFp8Target = 240.0f;
+int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* p,
+                           void* q, bool out_i32);
+int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mode,
+                      const float* scales_in, void* q, bool out_i32, float* scales_out,
+                      tkv_hip_qparams_dev* row_params, int symmetric);
+enum RowMode { RM_DYNAMIC = 0, RM_PER_CHANNEL = 1, RM_CALIBRATE = 2, RM_CALIBRATE_FULL = 3 };
+int launch_dequant_i8(Ctx* c, const void* q, bool in_i32, int64_t rows, int64_t cols,
+                      float scale, const float* scales, float* y);
+int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* scaled,
+                      void* q, bool out_i32);
+int launch_fp8_decode(Ctx* c, const void* q, bool in_i32, int64_t n, float* y);
+int launch_i32_to_i8(Ctx* c, const int32_t* src, int64_t rows, int64_t cols, int64_t ld_src,
+                     int8_t* dst, int64_t ld_dst, int code_bias);
+int launch_i8_to_i32(Ctx* c, const int8_t* src, int64_t n, int32_t* dst, int code_bias);
+int launch_i32_to_i8_transpose(Ctx* c, const int32_t* src, int64_t rows, int64_t cols,
+                               int8_t* dst, int64_t ld_dst);
+// qdq.hip
+int launch_quantize_linear(Ctx* c, const float* x, int64_t nx, const float* scales,
+                           int64_t n_scales, int64_t zp, int64_t dim, int64_t inner,
+                           int32_t* y);
+int launch_dequantize_linear(Ctx* c, const int32_t* x, int64_t nx, const float* scales,
+                             int64_t n_scales, int64_t zp, int64_t dim, int64_t inner,
+                             float* y);
+int launch_dynamic_ql(Ctx* c, const float* x, int64_t nx, const tkv_hip_qparams_dev* p,
+                      int32_t* y);
+// gemm_i8.hip
+struct I8Epilogue {
+    int mode;                  // EPI_* below
+    int recipe;                // TKV_HIP_RECIPE_*
+    const float* scale_a;      // device, indexed by m * scale_a_stride
+    int64_t scale_a_stride;
+    float scale_w;             // symmetric weight scale
+    const float* scales_w;     // device [N] (per-channel) or null
+    const float* bias;         // device [N] or null
+};
+enum { EPI_PER_CHANNEL = 0, EPI_SYMMETRIC = 1, EPI_ACCUM_I32 = 2 };
+int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
+                   const I8Epilogue& ep, void* y);
+// gemm_f8.hip
+int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
+                   int64_t k, const float* scale_a, int64_t scale_a_stride,
+                   const float* scales_w, const float* bias, float* y);
+
+}  // namespace tkv

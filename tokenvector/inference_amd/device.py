@@ -1,0 +1,249 @@
+"""Device-pointer side of libtkv_hip: contexts, buffers, the packed-code
+kernels and the resident quantized weight / linear.
+
+These wrap the ``tkv_hip_dev_*`` / ``tkv_hip_weight_*`` entry points, which
+take device pointers and run asynchronously on the context's stream.  Device
+memory comes from the library itself (``tkv_hip_malloc``), so no framework is
+needed to drive the GPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+
+ACT_PER_TENSOR = 0
+ACT_PER_TOKEN = 1
+WEIGHT_INT8 = 0
+WEIGHT_FP8 = 1
+
+
+def _vp(x) -> C.c_void_p:
+    if x is None:
+        return C.c_void_p(0)
+    if isinstance(x, DeviceBuffer):
+        return C.c_void_p(x.ptr)
+    return C.c_void_p(int(x))
+
+
+class Context:
+    """A libtkv_hip context: one HIP stream plus grow-only workspaces."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_int64()
+        _lib.check(_lib.lib().tkv_hip_ctx_create(int(device), C.byref(h)))
+        self.handle = h.value
+
+    def synchronize(self) -> None:
+        _lib.check(_lib.lib().tkv_hip_ctx_synchronize(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.check(_lib.lib().tkv_hip_ctx_destroy(self.handle))
+            self.handle = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class DeviceBuffer:
+    """A device allocation owned by Python (freed on close / GC)."""
+
+    def __init__(self, ctx: Context, nbytes: int, dtype=np.uint8, shape=None):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        p = C.c_void_p()
+        _lib.check(_lib.lib().tkv_hip_malloc(ctx.handle, self.nbytes, C.byref(p)))
+        self.ptr = p.value or 0
+
+    @classmethod
+    def empty(cls, ctx: Context, shape, dtype) -> "DeviceBuffer":
+        shape = (shape,) if np.isscalar(shape) else tuple(shape)
+        n = int(np.prod(shape)) if len(shape) else 1
+        return cls(ctx, n * np.dtype(dtype).itemsize, dtype, shape)
+
+    @classmethod
+    def from_host(cls, ctx: Context, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        b = cls(ctx, arr.nbytes, arr.dtype, arr.shape)
+        b.upload(arr)
+        return b
+
+    def upload(self, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes > self.nbytes:
+            raise ValueError("host array larger than device buffer")
+        _lib.check(_lib.lib().tkv_hip_memcpy_h2d(self.ctx.handle, C.c_void_p(self.ptr),
+                                                 arr.ctypes.data_as(C.c_void_p), arr.nbytes))
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        _lib.check(_lib.lib().tkv_hip_memcpy_d2h(self.ctx.handle, out.ctypes.data_as(C.c_void_p),
+                                                 C.c_void_p(self.ptr), out.nbytes))
+        return out
+
+    def close(self) -> None:
+        if self.ptr:
+            _lib.check(_lib.lib().tkv_hip_free(self.ctx.handle, C.c_void_p(self.ptr)))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def params_buffer(ctx: Context) -> DeviceBuffer:
+    """Room for one tkv_hip_qparams_dev."""
+    return DeviceBuffer(ctx, C.sizeof(_lib.QParamsDev), np.uint8)
+
+
+def read_params(buf: DeviceBuffer) -> _lib.QParamsDev:
+    raw = buf.download()
+    return _lib.QParamsDev.from_buffer_copy(raw.tobytes()[: C.sizeof(_lib.QParamsDev)])
+
+
+class Event:
+    """HIP event on a context's stream (timing)."""
+
+    def __init__(self):
+        h = C.c_int64()
+        _lib.check(_lib.lib().tkv_hip_event_create(C.byref(h)))
+        self.handle = h.value
+
+    def record(self, ctx: Context) -> None:
+        _lib.check(_lib.lib().tkv_hip_event_record(ctx.handle, self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        _lib.check(_lib.lib().tkv_hip_event_elapsed_ms(self.handle, end.handle, C.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            _lib.lib().tkv_hip_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+# ---- packed-code kernels (device pointers) ---------------------------------
+
+def calibrate_minmax(ctx, x, n, symmetric, params) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_calibrate_minmax(ctx.handle, _vp(x), int(n), int(symmetric),
+                                                       _vp(params)))
+
+
+def calibrate_rows(ctx, x, rows, cols, scales) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_calibrate_rows(ctx.handle, _vp(x), int(rows), int(cols),
+                                                     _vp(scales)))
+
+
+def quantize_int8_tensor(ctx, x, n, params, q) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_int8_tensor(ctx.handle, _vp(x), int(n),
+                                                           _vp(params), _vp(q)))
+
+
+def quantize_int8_dynamic_tensor(ctx, x, n, q, params) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_int8_dynamic_tensor(ctx.handle, _vp(x), int(n),
+                                                                   _vp(q), _vp(params)))
+
+
+def quantize_int8_per_channel(ctx, x, rows, cols, scales, q) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_int8_per_channel(ctx.handle, _vp(x), int(rows),
+                                                                int(cols), _vp(scales), _vp(q)))
+
+
+def quantize_dynamic_int8_rowwise(ctx, x, rows, cols, q, scales_out) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_dynamic_int8_rowwise(
+        ctx.handle, _vp(x), int(rows), int(cols), _vp(q), _vp(scales_out)))
+
+
+def dequantize_int8(ctx, q, rows, cols, scale, scales, y) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_dequantize_int8(ctx.handle, _vp(q), int(rows), int(cols),
+                                                      float(scale), _vp(scales), _vp(y)))
+
+
+def quantize_fp8_e4m3(ctx, x, n, q) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_fp8_e4m3(ctx.handle, _vp(x), int(n), _vp(q)))
+
+
+def quantize_fp8_e4m3_scaled(ctx, x, n, params, q) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_fp8_e4m3_scaled(ctx.handle, _vp(x), int(n),
+                                                               _vp(params), _vp(q)))
+
+
+def dequantize_fp8_e4m3(ctx, q, n, y) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_dequantize_fp8_e4m3(ctx.handle, _vp(q), int(n), _vp(y)))
+
+
+def matmul_int8(ctx, a, w, m, n, k, scale_a, scale_a_stride, scale_w, scales_w, bias, y,
+                recipe=0) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_matmul_int8(ctx.handle, _vp(a), _vp(w), int(m), int(n),
+                                                  int(k), _vp(scale_a), int(scale_a_stride),
+                                                  float(scale_w), _vp(scales_w), _vp(bias),
+                                                  _vp(y), int(recipe)))
+
+
+def matmul_int8_accum(ctx, a, w, m, n, k, acc) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_matmul_int8_accum(ctx.handle, _vp(a), _vp(w), int(m), int(n),
+                                                        int(k), _vp(acc)))
+
+
+def matmul_fp8_e4m3(ctx, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_matmul_fp8_e4m3(ctx.handle, _vp(a), _vp(w), int(m), int(n),
+                                                      int(k), _vp(scale_a), int(scale_a_stride),
+                                                      _vp(scales_w), _vp(bias), _vp(y)))
+
+
+class QuantizedLinear:
+    """A device-resident quantized weight [N, K] (+ bias) and its forward."""
+
+    def __init__(self, ctx: Context, handle: int):
+        self.ctx = ctx
+        self.handle = handle
+        codes, scales, bias = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        n, k, fmt = C.c_int64(), C.c_int64(), C.c_int32()
+        _lib.check(_lib.lib().tkv_hip_weight_info(handle, C.byref(codes), C.byref(scales),
+                                                  C.byref(bias), C.byref(n), C.byref(k),
+                                                  C.byref(fmt)))
+        self.codes, self.scales, self.bias = codes.value, scales.value, bias.value
+        self.n, self.k, self.format = n.value, k.value, fmt.value
+
+    @classmethod
+    def from_float(cls, ctx: Context, w, n: int, k: int, bias=None,
+                   fmt: int = WEIGHT_INT8) -> "QuantizedLinear":
+        h = C.c_int64()
+        _lib.check(_lib.lib().tkv_hip_weight_create(ctx.handle, _vp(w), int(n), int(k), _vp(bias),
+                                                    int(fmt), C.byref(h)))
+        return cls(ctx, h.value)
+
+    @classmethod
+    def from_int8(cls, ctx: Context, codes, scales, n: int, k: int, bias=None) -> "QuantizedLinear":
+        h = C.c_int64()
+        _lib.check(_lib.lib().tkv_hip_weight_create_int8(ctx.handle, _vp(codes), _vp(scales), int(n),
+                                                         int(k), _vp(bias), C.byref(h)))
+        return cls(ctx, h.value)
+
+    def forward(self, x, m: int, y, act_mode: int = ACT_PER_TENSOR) -> None:
+        _lib.check(_lib.lib().tkv_hip_linear_forward(self.ctx.handle, self.handle, _vp(x), int(m),
+                                                     int(act_mode), _vp(y)))
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.check(_lib.lib().tkv_hip_weight_free(self.handle))
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
