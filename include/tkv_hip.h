@@ -242,13 +242,22 @@ int32_t tkv_hip_dev_matmul_int8(int64_t ctx, const int8_t* a, const int8_t* w, i
 /* INT32 accumulators only (MatMulInteger core; exactness checks). */
 int32_t tkv_hip_dev_matmul_int8_accum(int64_t ctx, const int8_t* a, const int8_t* w,
                                       int64_t m, int64_t n, int64_t k, int32_t* acc);
-/* FP8 e4m3 GEMM: raw e4m3 bytes A [M,K], W [N,K]; f32 accumulate;
- * y = fl32(acc + bias[n]) (matmul.tkv:46-58).  With scale_a / scales_w
- * non-NULL the extension epilogue y = acc * sa * scales_w[n] + bias[n]. */
+/* FP8 e4m3 GEMM: raw e4m3 bytes A [M,K], W [N,K]; y = fl32(acc + bias[n])
+ * (matmul.tkv:46-58).  Products are the reference decoder's (decoded exactly
+ * to f16, f16 MFMA), accumulated at f32-class precision.  With scale_a /
+ * scales_w non-NULL the extension epilogue y = acc * sa * scales_w[n] + bias[n]. */
 int32_t tkv_hip_dev_matmul_fp8_e4m3(int64_t ctx, const uint8_t* a, const uint8_t* w,
                                     int64_t m, int64_t n, int64_t k, const float* scale_a,
                                     int64_t scale_a_stride, const float* scales_w,
                                     const float* bias, float* y);
+/* Same contract on the full-rate FP8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
+ * hardware OCP e4m3 decode (subnormal codes read twice the reference's value)
+ * and the MFMA's reduced-precision dot-product accumulation; outputs agree
+ * with the reference within 2^-10 * sum_k |a_k w_k| per element. */
+int32_t tkv_hip_dev_matmul_fp8_e4m3_fast(int64_t ctx, const uint8_t* a, const uint8_t* w,
+                                         int64_t m, int64_t n, int64_t k, const float* scale_a,
+                                         int64_t scale_a_stride, const float* scales_w,
+                                         const float* bias, float* y);
 
 /* ---- device-resident quantized weight (pack once, run many) ------------ */
 /* Calibrates W f32 [N,K] (device pointer) per output channel and quantizes
@@ -256,7 +265,8 @@ int32_t tkv_hip_dev_matmul_fp8_e4m3(int64_t ctx, const uint8_t* a, const uint8_t
  * scales and an optional bias on the device.  Mirrors the offline
  * calibrate_per_channel_minmax + quantize_int8_per_channel steps of CS1. */
 #define TKV_HIP_WEIGHT_INT8 0
-#define TKV_HIP_WEIGHT_FP8 1
+#define TKV_HIP_WEIGHT_FP8 1      /* GEMM with the reference decoder's products */
+#define TKV_HIP_WEIGHT_FP8_FAST 2 /* GEMM on the full-rate FP8 MFMA            */
 int32_t tkv_hip_weight_create(int64_t ctx, const float* w, int64_t n, int64_t k,
                               const float* bias, int32_t format, int64_t* handle_out);
 /* Pre-quantized int8 weight codes [N,K] + per-channel scales (device). */

@@ -347,23 +347,48 @@ def _fp8_codes(shape, allow_subnormal):
     return (RNG.choice(codes, shape) - 128).astype(np.int32)
 
 
-def _fp8_bound(a, w, bias, m, n, k):
-    acc, asum = O.matmul_fp8_e4m3_exact(a, w, m, n, k)
+def _fp8_ref(a, w, bias, m, n, k):
+    """Reference output, sum_k |a_k w_k| and the ulp of the reference output."""
+    _, asum = O.matmul_fp8_e4m3_exact(a, w, m, n, k)
     ref = O.matmul_fp8_e4m3(a, w, bias, m, n, k)
     ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
-    return ref, k * 2.0 ** -24 * asum + 2 * ulp
+    return ref.astype(np.float64), asum, ulp
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 1, 64), (37, 100, 96), (128, 256, 768), (64, 96, 3072)])
-def test_fp8_gemm_normal_codes(hip, m, n, k):
-    say(f"fp8 gemm {m}x{n}x{k}")
-    a = _fp8_codes((m, k), False)
-    w = _fp8_codes((n, k), False)
+FP8_SHAPES = [(1, 1, 64), (37, 100, 96), (128, 256, 768), (64, 96, 3072), (130, 200, 200)]
+
+
+@pytest.mark.parametrize("m,n,k", FP8_SHAPES)
+def test_fp8_gemm_reference_products(hip, m, n, k):
+    """matmul_fp8_e4m3 drop-in: the reference decoder's products (subnormal
+    codes included) summed at f32-class precision.  Stated bound:
+    |y - y_ref| <= 8 * 2^-24 * sum_k |a_k w_k| + ulp(y_ref)."""
+    say(f"fp8 gemm (reference products) {m}x{n}x{k}")
+    a, w = _fp8_codes((m, k), True), _fp8_codes((n, k), True)
     b = RNG.normal(0, 1, n).astype(np.float32)
     y = np.zeros(m * n, np.float32)
     Q.matmul_fp8_e4m3(a, w, b, y, m, n, k)
-    ref, tol = _fp8_bound(a, w, b, m, n, k)
-    err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
+    ref, asum, ulp = _fp8_ref(a, w, b, m, n, k)
+    err = np.abs(y.astype(np.float64) - ref)
+    tol = 8 * 2.0 ** -24 * asum + ulp
+    assert np.all(err <= tol), float((err / tol).max())
+
+
+@pytest.mark.parametrize("m,n,k", FP8_SHAPES)
+def test_fp8_gemm_fast(ctx, m, n, k):
+    """Full-rate FP8 MFMA path, normal codes: stated bound
+    |y - y_ref| <= 2^-10 * sum_k |a_k w_k| + ulp(y_ref)."""
+    say(f"fp8 gemm (fast) {m}x{n}x{k}")
+    a, w = _fp8_codes((m, k), False), _fp8_codes((n, k), False)
+    b = RNG.normal(0, 1, n).astype(np.float32)
+    da = D.DeviceBuffer.from_host(ctx, (a + 128).astype(np.uint8))
+    dw = D.DeviceBuffer.from_host(ctx, (w + 128).astype(np.uint8))
+    db = D.DeviceBuffer.from_host(ctx, b)
+    dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+    D.matmul_fp8_e4m3(ctx, da, dw, m, n, k, None, 0, None, db, dy, fast=True)
+    ref, asum, ulp = _fp8_ref(a, w, b, m, n, k)
+    err = np.abs(dy.download().reshape(-1).astype(np.float64) - ref)
+    tol = 2.0 ** -10 * asum + ulp
     assert np.all(err <= tol), float((err / tol).max())
 
 

@@ -74,7 +74,8 @@ int host_gemm_i8(const int32_t* pa, const int32_t* pw, const float* pbias, int64
         return host_gemm_i8(za.data(), zw.data(), pbias, n_bias, py, accum, m, n, 1, scale_a,
                             scale_w, scales_w, n_scales, recipe);
     }
-    int64_t ldk = (k + 15) & ~int64_t(15);
+    const int64_t ka = gemm_k_align();
+    int64_t ldk = (k + ka - 1) / ka * ka;  // zero-padded: no repack in the launcher
     std::vector<int8_t> ha, hw;
     TKV_RC_TRY(pack_codes(pa, m, k, ldk, 0, -128, 127, ha));
     TKV_RC_TRY(pack_codes(pw, n, k, ldk, 0, -128, 127, hw));
@@ -309,7 +310,9 @@ int32_t tkv_hip_matmul_int8_recipe(const int32_t* pa, const int32_t* pw, const f
                                    int64_t n_bias, float* py, int64_t m, int64_t n, int64_t k,
                                    float scale_a, float scale_w, const float* scales_w,
                                    int64_t n_scales, int32_t recipe) {
-    if (scales_w && n_scales < n) return set_error(TKV_HIP_BAD_ARG, "scales_w smaller than N");
+    // n_scales == 0 selects the symmetric GEMM (len(scales_w) == 0)
+    if (scales_w && n_scales > 0 && n_scales < n)
+        return set_error(TKV_HIP_BAD_ARG, "scales_w smaller than N");
     return host_gemm_i8(pa, pw, pbias, n_bias, py, false, m, n, k, scale_a, scale_w,
                         n_scales > 0 ? scales_w : nullptr, n_scales, recipe);
 }
@@ -326,7 +329,8 @@ int32_t tkv_hip_matmul_fp8_e4m3(const int32_t* pa, const int32_t* pw, const floa
     if (m == 0 || n == 0) return TKV_HIP_OK;
     if (n_bias > 0 && n_bias < n) return set_error(TKV_HIP_BAD_ARG, "bias shorter than N");
     int64_t kk = k > 0 ? k : 1;
-    int64_t ldk = (kk + 15) & ~int64_t(15);
+    const int64_t ka = gemm_k_align();
+    int64_t ldk = (kk + ka - 1) / ka * ka;
     std::vector<int8_t> ha, hw;
     if (k > 0) {
         // codes are e4m3 byte - 128: raw byte = code + 128 (0x00 is +0.0)
@@ -346,7 +350,7 @@ int32_t tkv_hip_matmul_fp8_e4m3(const int32_t* pa, const int32_t* pw, const floa
     TKV_RC_TRY(ctx_workspace(c, WS_Y, ybytes, &dy));
     TKV_RC_TRY(launch_gemm_f8(c, static_cast<uint8_t*>(da), static_cast<uint8_t*>(dw), m, n, ldk,
                               nullptr, 0, nullptr, static_cast<float*>(db),
-                              static_cast<float*>(dy)));
+                              static_cast<float*>(dy), false));
     return download(c, py, dy, ybytes);
 }
 
@@ -574,7 +578,18 @@ int32_t tkv_hip_dev_matmul_fp8_e4m3(int64_t ctx, const uint8_t* a, const uint8_t
         return set_error(TKV_HIP_BAD_ARG, "bad GEMM arguments");
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
-    return launch_gemm_f8(c, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y);
+    return launch_gemm_f8(c, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y, false);
+}
+
+int32_t tkv_hip_dev_matmul_fp8_e4m3_fast(int64_t ctx, const uint8_t* a, const uint8_t* w,
+                                         int64_t m, int64_t n, int64_t k, const float* scale_a,
+                                         int64_t scale_a_stride, const float* scales_w,
+                                         const float* bias, float* y) {
+    if (m < 0 || n < 0 || k < 0 || scale_a_stride < 0)
+        return set_error(TKV_HIP_BAD_ARG, "bad GEMM arguments");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_gemm_f8(c, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y, true);
 }
 
 }  // extern "C"

@@ -58,7 +58,8 @@ static int weight_alloc(Ctx* c, Weight* wt, int64_t n, int64_t k, int format, co
     wt->format = format;
     wt->n = n;
     wt->k = k;
-    wt->ldk = (k + 15) & ~int64_t(15);
+    const int64_t ka = gemm_k_align();
+    wt->ldk = (k + ka - 1) / ka * ka;  // the GEMM slice depth: no per-call repack
     TKV_HIP_TRY(hipMalloc(&wt->codes, (size_t)(n * wt->ldk)));
     TKV_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&wt->scales), (size_t)n * 4));
     TKV_HIP_TRY(hipMemsetAsync(wt->codes, 0, (size_t)(n * wt->ldk), c->stream));
@@ -92,7 +93,8 @@ int32_t tkv_hip_weight_create(int64_t ctx, const float* w, int64_t n, int64_t k,
     TKV_RC_TRY(ctx_get(ctx, &c));
     if (!w || !handle_out || n <= 0 || k <= 0)
         return set_error(TKV_HIP_BAD_ARG, "weight_create: empty weight or NULL output");
-    if (format != TKV_HIP_WEIGHT_INT8 && format != TKV_HIP_WEIGHT_FP8)
+    if (format != TKV_HIP_WEIGHT_INT8 && format != TKV_HIP_WEIGHT_FP8 &&
+        format != TKV_HIP_WEIGHT_FP8_FAST)
         return set_error(TKV_HIP_BAD_ARG, "weight_create: unknown format");
     Weight* wt = new (std::nothrow) Weight();
     if (!wt) return set_error(TKV_HIP_OOM, "weight_create: host allocation failed");
@@ -186,7 +188,7 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
     if (!wt || !x || !y || m < 0) return set_error(TKV_HIP_BAD_ARG, "linear_forward: bad arguments");
     if (m == 0) return TKV_HIP_OK;
     if (wt->ldk != wt->k)
-        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of 16");
+        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of 64");
     const int64_t k = wt->k;
     void* qa;
     TKV_RC_TRY(ctx_workspace(c, 0, (size_t)(m * k), &qa));
@@ -221,7 +223,8 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
     TKV_RC_TRY(launch_minmax_tensor(c, x, m * k, MM_FP8, TKV_HIP_RECIPE_PRIMARY, ap));
     TKV_RC_TRY(launch_fp8_encode(c, x, m * k, ap, qa, false));
     return launch_gemm_f8(c, static_cast<uint8_t*>(qa), static_cast<uint8_t*>(wt->codes), m, wt->n,
-                          k, &ap->scale, 0, wt->scales, wt->bias, y);
+                          k, &ap->scale, 0, wt->scales, wt->bias, y,
+                          wt->format == TKV_HIP_WEIGHT_FP8_FAST);
 }
 
 }  // extern "C"

@@ -92,12 +92,15 @@ __device__ __forceinline__ void mm_acc(float v, int64_t idx, bool track_zero, fl
     if (track_zero && v == 0.0f && (unsigned long long)idx < zi) zi = (unsigned long long)idx;
 }
 
-// Per-tensor min / max (+ first zero) with last-block finalize.
-__global__ __launch_bounds__(kBlock) void k_minmax_tensor(
-    const float* __restrict__ x, int64_t n, int vec, int track_zero, int mode, int recipe,
-    RedPartial* __restrict__ partials, unsigned int* __restrict__ counter,
-    tkv_hip_qparams_dev* __restrict__ out) {
-    float mn = FLT_MAX * 2.0f, mx = -FLT_MAX * 2.0f;  // +-inf
+// Per-tensor min / max (+ first zero): one partial per block, then a
+// one-block finalize kernel.  The kernel boundary orders the partial stores
+// before the finalize reads, across XCDs and their separate L2s, without
+// device-scope fences in the streaming kernel.
+template <bool TRACK_ZERO>
+__global__ __launch_bounds__(kBlock) void k_minmax_partials(const float* __restrict__ x,
+                                                            int64_t n, int vec,
+                                                            RedPartial* __restrict__ partials) {
+    float mn = __builtin_inff(), mx = -__builtin_inff();
     unsigned long long zi = ~0ull;
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -111,28 +114,27 @@ __global__ __launch_bounds__(kBlock) void k_minmax_tensor(
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             int64_t b = (i + u * stride) * 4;
-            mm_acc(v[u].x, b + 0, track_zero, mn, mx, zi);
-            mm_acc(v[u].y, b + 1, track_zero, mn, mx, zi);
-            mm_acc(v[u].z, b + 2, track_zero, mn, mx, zi);
-            mm_acc(v[u].w, b + 3, track_zero, mn, mx, zi);
+            mm_acc(v[u].x, b + 0, TRACK_ZERO, mn, mx, zi);
+            mm_acc(v[u].y, b + 1, TRACK_ZERO, mn, mx, zi);
+            mm_acc(v[u].z, b + 2, TRACK_ZERO, mn, mx, zi);
+            mm_acc(v[u].w, b + 3, TRACK_ZERO, mn, mx, zi);
         }
     }
     for (; i < n4; i += stride) {
         float4 v = x4[i];
-        mm_acc(v.x, i * 4 + 0, track_zero, mn, mx, zi);
-        mm_acc(v.y, i * 4 + 1, track_zero, mn, mx, zi);
-        mm_acc(v.z, i * 4 + 2, track_zero, mn, mx, zi);
-        mm_acc(v.w, i * 4 + 3, track_zero, mn, mx, zi);
+        mm_acc(v.x, i * 4 + 0, TRACK_ZERO, mn, mx, zi);
+        mm_acc(v.y, i * 4 + 1, TRACK_ZERO, mn, mx, zi);
+        mm_acc(v.z, i * 4 + 2, TRACK_ZERO, mn, mx, zi);
+        mm_acc(v.w, i * 4 + 3, TRACK_ZERO, mn, mx, zi);
     }
-    for (int64_t j = n4 * 4 + tid; j < n; j += stride) mm_acc(x[j], j, track_zero, mn, mx, zi);
+    for (int64_t j = n4 * 4 + tid; j < n; j += stride) mm_acc(x[j], j, TRACK_ZERO, mn, mx, zi);
 
     __shared__ float s_mn[kBlock / 64], s_mx[kBlock / 64];
     __shared__ unsigned long long s_zi[kBlock / 64];
-    __shared__ int s_last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     mn = wave_min(mn);
     mx = wave_max(mx);
-    zi = wave_min_u64(zi);
+    if (TRACK_ZERO) zi = wave_min_u64(zi);
     if (lane == 0) {
         s_mn[wave] = mn;
         s_mx[wave] = mx;
@@ -150,26 +152,28 @@ __global__ __launch_bounds__(kBlock) void k_minmax_tensor(
         p.mx = mx;
         p.zidx = zi;
         partials[blockIdx.x] = p;
-        __threadfence();
-        unsigned int prev = atomicAdd(counter, 1u);
-        s_last = (prev == gridDim.x - 1);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    mn = FLT_MAX * 2.0f;
-    mx = -FLT_MAX * 2.0f;
-    zi = ~0ull;
-    for (int b = threadIdx.x; b < (int)gridDim.x; b += kBlock) {
+}
+
+__global__ __launch_bounds__(kBlock) void k_minmax_finalize(const float* __restrict__ x,
+                                                            int nparts, int track_zero, int mode,
+                                                            int recipe,
+                                                            const RedPartial* __restrict__ partials,
+                                                            tkv_hip_qparams_dev* __restrict__ out) {
+    float mn = __builtin_inff(), mx = -__builtin_inff();
+    unsigned long long zi = ~0ull;
+    for (int b = threadIdx.x; b < nparts; b += kBlock) {
         RedPartial p = partials[b];
         mn = fminf(mn, p.mn);
         mx = fmaxf(mx, p.mx);
         zi = p.zidx < zi ? p.zidx : zi;
     }
+    __shared__ float s_mn[kBlock / 64], s_mx[kBlock / 64];
+    __shared__ unsigned long long s_zi[kBlock / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     mn = wave_min(mn);
     mx = wave_max(mx);
     zi = wave_min_u64(zi);
-    __syncthreads();
     if (lane == 0) {
         s_mn[wave] = mn;
         s_mx[wave] = mx;
@@ -192,7 +196,6 @@ __global__ __launch_bounds__(kBlock) void k_minmax_tensor(
             if (mx == 0.0f) dmx = z;
         }
         finalize_minmax(dmn, dmx, mode, recipe, out);
-        *counter = 0u;
     }
 }
 
@@ -207,8 +210,15 @@ int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe
     if (blocks < 1) blocks = 1;
     // Only the asymmetric QuantParams expose the sign of a zero extreme.
     int track_zero = (mode == MM_ASYMMETRIC) ? 1 : 0;
-    hipLaunchKernelGGL(k_minmax_tensor, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, x, n,
-                       vec, track_zero, mode, recipe, c->partials, c->counter, out);
+    if (track_zero)
+        hipLaunchKernelGGL(k_minmax_partials<true>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, c->partials);
+    else
+        hipLaunchKernelGGL(k_minmax_partials<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, c->partials);
+    TKV_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_minmax_finalize, dim3(1), dim3(kBlock), 0, c->stream, x, (int)blocks,
+                       track_zero, mode, recipe, c->partials, out);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -76,11 +76,10 @@ int ctx_create(int device, Ctx** out) {
         return fail_hip(e, "hipMalloc(reduction scratch)", __FILE__, __LINE__);
     }
     c->partials = static_cast<RedPartial*>(red);
-    c->counter = reinterpret_cast<unsigned int*>(static_cast<char*>(red) +
-                                                 sizeof(RedPartial) * kMaxReduceBlocks);
     c->params = reinterpret_cast<tkv_hip_qparams_dev*>(static_cast<char*>(red) +
                                                        sizeof(RedPartial) * kMaxReduceBlocks + 256);
-    // One-time zeroing at creation (never inside a caller's stream capture).
+    // One-time zeroing at creation, so params read before any calibration
+    // are defined (never inside a caller's stream capture).
     e = hipMemset(red, 0, red_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {

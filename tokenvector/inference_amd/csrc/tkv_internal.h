@@ -50,11 +50,9 @@ struct Ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     int num_cus = 256;
-    // reduction scratch: kMaxReduceBlocks partials, then one counter; the
-    // counter is zeroed at creation and re-zeroed by the last block of every
-    // reduction, so it needs no per-call clearing.
+    // reduction scratch: kMaxReduceBlocks per-block partials (written by the
+    // partials kernel, read by the finalize kernel; no clearing needed)
     RedPartial* partials = nullptr;
-    unsigned int* counter = nullptr;
     tkv_hip_qparams_dev* params = nullptr;  // 64 slots of per-call params
     // grow-only workspaces
     static constexpr int kSlots = 8;
@@ -112,7 +110,7 @@ int launch_dequantize_linear(Ctx* c, const int32_t* x, int64_t nx, const float* 
                              float* y);
 int launch_dynamic_ql(Ctx* c, const float* x, int64_t nx, const tkv_hip_qparams_dev* p,
                       int32_t* y);
-// gemm_i8.hip
+// gemm.hip
 struct I8Epilogue {
     int mode;                  // EPI_* below
     int recipe;                // TKV_HIP_RECIPE_*
@@ -125,9 +123,13 @@ struct I8Epilogue {
 enum { EPI_PER_CHANNEL = 0, EPI_SYMMETRIC = 1, EPI_ACCUM_I32 = 2 };
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
                    const I8Epilogue& ep, void* y);
-// gemm_f8.hip
+// fast: full-rate FP8 MFMA (hardware OCP decode and rounding); otherwise the
+// reference decoder's products on f16 MFMA.
 int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                    int64_t k, const float* scale_a, int64_t scale_a_stride,
-                   const float* scales_w, const float* bias, float* y);
+                   const float* scales_w, const float* bias, float* y, bool fast);
+// K granularity of the GEMM main loop: operands whose row stride is a
+// multiple of it (and 16-byte aligned) run without repacking.
+int64_t gemm_k_align();
 
 }  // namespace tkv

@@ -19,6 +19,7 @@ ACT_PER_TENSOR = 0
 ACT_PER_TOKEN = 1
 WEIGHT_INT8 = 0
 WEIGHT_FP8 = 1
+WEIGHT_FP8_FAST = 2
 
 
 def _vp(x) -> C.c_void_p:
@@ -198,10 +199,14 @@ def matmul_int8_accum(ctx, a, w, m, n, k, acc) -> None:
                                                         int(k), _vp(acc)))
 
 
-def matmul_fp8_e4m3(ctx, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y) -> None:
-    _lib.check(_lib.lib().tkv_hip_dev_matmul_fp8_e4m3(ctx.handle, _vp(a), _vp(w), int(m), int(n),
-                                                      int(k), _vp(scale_a), int(scale_a_stride),
-                                                      _vp(scales_w), _vp(bias), _vp(y)))
+def matmul_fp8_e4m3(ctx, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y,
+                    fast: bool = False) -> None:
+    """FP8 GEMM on raw e4m3 bytes; fast=True runs the full-rate FP8 MFMA
+    (stated tolerance), otherwise the reference decoder's products."""
+    fn = (_lib.lib().tkv_hip_dev_matmul_fp8_e4m3_fast if fast
+          else _lib.lib().tkv_hip_dev_matmul_fp8_e4m3)
+    _lib.check(fn(ctx.handle, _vp(a), _vp(w), int(m), int(n), int(k), _vp(scale_a),
+                  int(scale_a_stride), _vp(scales_w), _vp(bias), _vp(y)))
 
 
 class QuantizedLinear:
