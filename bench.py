@@ -203,7 +203,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(the multi-GPU split is a design note only; one GPU is measured)", file=sys.stderr)
         sys.exit(2)
 
     r = run_gpu(args.steps, args.warmup)
@@ -220,7 +220,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (LCG31 + Box-Muller, seeds per SURVEY 8d; random-init GPT-2 shapes)",
+        "data": "synthetic (LCG31 + Box-Muller generator of tv/training/gpt2_ref.tkv, fixed seeds; random-init GPT-2 shapes)",
         "config": {"workload": "configs[2]: all GPT-2-124M linears W8A8, M=8192, 12 layers "
                                "(per step: 48 x [absmax calibrate + int8 quantize + INT8 GEMM + "
                                "dequant/bias epilogue])",

@@ -21,6 +21,15 @@
  * (list[f32] stores, f32 fields and returns).  Where that typing cannot be
  * pinned without running the reference compiler, a recipe switch selects the
  * alternate reading (TKVO_RECIPE_*).
+ *
+ * Parity unpinned (compiler typing only; the arithmetic of both readings is
+ * pinned by the tests):
+ *   - tkvo_quantize_int8_symmetric: whether 1.0/scale (engine.tkv:219-222)
+ *     is evaluated in f32 (primary) or f64 (TKVO_RECIPE_ALTERNATE);
+ *   - tkvo_matmul_int8_per_channel / _symmetric: whether the i64 * f32
+ *     epilogue chains (matmul.tkv:5,14 and :29) run in f64 (primary) or f32.
+ * No reference test reaches a rounding tie that separates the readings, and
+ * the reference compiler (tkvc, .NET) is not available to run.
  */
 #ifndef TKV_ORACLE_H
 #define TKV_ORACLE_H

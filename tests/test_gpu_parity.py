@@ -309,7 +309,7 @@ def test_matmul_integer_node(hip):
     say("MatMulInteger")
     node = S.new_node("mi", S.OperatorType_MatMulInteger)
     (y,) = node.execute([([1, 2, 3, 4], [2, 2]), ([1, 1, 1, 1], [2, 2])], [[2, 2]])
-    assert list(y) == [3, 3, 7, 7]        # inference_tests.tkv:1159-1176
+    assert list(y) == [3, 3, 7, 7]        # inference_tests.tkv:896-922
     m, n, k = 33, 17, 45
     a = RNG.integers(-128, 128, m * k - 5).astype(np.int32)
     b = RNG.integers(-128, 128, k * n).astype(np.int32)

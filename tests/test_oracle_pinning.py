@@ -6,8 +6,6 @@ parity checker.  Each check is independent of the oracle's own code:
 * library routines (numpy IEEE float32 arithmetic, numpy int64 matmul,
   numpy rint, torch float8 casts, Python Fractions);
 * exhaustive comparison with an independently formulated encoder.
-
-Functions of the oracle and what pins them are tabulated in DESIGN.md.
 """
 from fractions import Fraction
 
@@ -51,13 +49,13 @@ def test_kat_fp8_roundtrip(enc, dec, vals, tol):
 
 
 def test_kat_matmul_integer():
-    # inference_tests.tkv:1159-1176: [[1,2],[3,4]] . ones -> [[3,3],[7,7]]
+    # inference_tests.tkv:896-922: [[1,2],[3,4]] . ones -> [[3,3],[7,7]]
     y = O.matmul_integer([1, 2, 3, 4], [1, 1, 1, 1], 4, 2, 2, 2)
     assert list(y) == [3, 3, 7, 7]
 
 
 def test_kat_dynamic_quantize_linear():
-    # inference_tests.tkv:1177-1193: [0,1,2] -> scale 2/255, zp 0, y0 -128, y2 127
+    # inference_tests.tkv:923-948: [0,1,2] -> scale 2/255, zp 0, y0 -128, y2 127
     y, ys, yz = O.dynamic_quantize_linear([0.0, 1.0, 2.0])
     assert abs(float(ys) - 2.0 / 255.0) < 0.000001 and float(yz) == 0.0
     assert y[0] == -128 and y[2] == 127
