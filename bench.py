@@ -169,7 +169,68 @@ def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
     return out
 
 
-def cpu_baseline(rows=2048):
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_gemm_i8_traffic_gpt2_m8192.md")
+
+
+def traffic_probe(reps=3, copy_bytes=1 << 30):
+    """The command profiled by the two rocprofv3 --pmc passes (FETCH_SIZE,
+    then WRITE_SIZE) that give the GEMM's HBM traffic.  It first copies
+    `copy_bytes` `reps` times with the library's plain copy kernel (k_copy16,
+    known bytes: the counters' scale factor), then runs each GPT-2 linear's
+    activation quantize + INT8 GEMM `reps` times on distinct buffers, so that
+    every GEMM launch starts with its operands outside the caches."""
+    import oracle as O
+    from tokenvector.inference_amd import _lib
+    from tokenvector.inference_amd import device as D
+
+    if _lib.lib().tkv_hip_device_count() < 1:
+        raise SystemExit("bench.py: no gfx950 device visible")
+    ctx = D.Context(0)
+    src = D.DeviceBuffer(ctx, copy_bytes)
+    dst = D.DeviceBuffer(ctx, copy_bytes)
+    ctx.synchronize()
+    for _ in range(reps):
+        dst.copy_from(src)
+    ctx.synchronize()
+    src.close()
+    dst.close()
+    log(f"traffic probe: {reps} x k_copy16 of {copy_bytes} bytes")
+    for j, (name, n, k) in enumerate(SHAPES):
+        w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 11 + j, 0.02))
+        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 61 + j, 0.01))
+        q = D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_INT8)
+        xh = O.gi_noise(M * k, 0, 1.0)
+        bufs = [(D.DeviceBuffer.from_host(ctx, xh), D.DeviceBuffer.empty(ctx, (M, k), np.int8),
+                 D.DeviceBuffer.empty(ctx, (M, n), np.float32), D.params_buffer(ctx))
+                for _ in range(reps)]
+        ctx.synchronize()
+        for dx, qa, dy, p in bufs:
+            D.quantize_int8_dynamic_tensor(ctx, dx, M * k, qa, p)
+            D.matmul_int8(ctx, qa, q.codes, M, n, k, p.ptr, 0, 0.0, q.scales, q.bias, dy)
+        ctx.synchronize()
+        log(f"traffic probe: {reps} x {name} GEMM M={M} N={n} K={k} "
+            f"(algorithmic {gemm_bytes(M, n, k)} bytes per launch)")
+        for t in bufs:
+            for buf in t:
+                buf.close()
+        q.close()
+    ctx.close()
+
+
+def read_traffic():
+    """HBM bytes per GEMM launch, averaged over the four shapes as the bench
+    weights them, from the committed PMC summary (None if absent)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch_avg:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(rows=4096):
     """The oracle's scalar restatement of the reference loops (one thread),
     on a bounded sample of the same workload: `rows` activation rows of each
     of the four linear shapes (calibrate + quantize + INT8 GEMM + epilogue)."""
@@ -199,12 +260,17 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=2048)
+    ap.add_argument("--cpu-rows", type=int, default=4096)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the launches profiled for HBM traffic (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
               "(the multi-GPU split is a design note only; one GPU is measured)", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_probe:
+        traffic_probe()
+        return
 
     r = run_gpu(args.steps, args.warmup)
     gemm = r["gemm"]
@@ -229,7 +295,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm["achieved_tops"], 1),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm["achieved_tops"] / PEAK_INT8_TOPS, 4),
-                     "traffic": None,
+                     "traffic": read_traffic(),
+                     "algorithmic_bytes_per_launch": round(
+                         float(np.mean([gemm_bytes(M, n, k) for (_, n, k) in SHAPES]))),
                      "kernel": "k_gemm_i8 (INT8 MFMA GEMM + fused dequant epilogue)",
                      "avg_launch_us": round(gemm["avg_launch_us"], 2),
                      "per_shape": gemm["per_shape"]},

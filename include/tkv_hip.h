@@ -89,6 +89,10 @@ int32_t tkv_hip_free(int64_t ctx, void* ptr);
 int32_t tkv_hip_memcpy_h2d(int64_t ctx, void* dst, const void* src, int64_t bytes);
 int32_t tkv_hip_memcpy_d2h(int64_t ctx, void* dst, const void* src, int64_t bytes);
 int32_t tkv_hip_memset(int64_t ctx, void* dst, int32_t value, int64_t bytes);
+/* Device-to-device copy, asynchronous on the context's stream.  16-byte
+ * aligned pointers and sizes run one plain streaming kernel (k_copy16) that
+ * moves exactly `bytes` each way. */
+int32_t tkv_hip_memcpy_d2d(int64_t ctx, void* dst, const void* src, int64_t bytes);
 /* Stream-ordered event timing (bench harness). */
 int32_t tkv_hip_event_create(int64_t* ev_out);
 int32_t tkv_hip_event_destroy(int64_t ev);
@@ -274,7 +278,8 @@ int32_t tkv_hip_weight_create_int8(int64_t ctx, const int8_t* codes, const float
                                    int64_t n, int64_t k, const float* bias,
                                    int64_t* handle_out);
 int32_t tkv_hip_weight_free(int64_t handle);
-/* Read back the weight's codes / scales (device pointers owned by the handle). */
+/* Read back the weight's codes / scales (device pointers owned by the handle).
+ * *k is the codes' row stride (K rounded up to 128; rows are zero padded). */
 int32_t tkv_hip_weight_info(int64_t handle, void** codes, float** scales, float** bias,
                             int64_t* n, int64_t* k, int32_t* format);
 /* Quantized linear: y[M,N] = dequant(quant(x) . W^T) + bias.

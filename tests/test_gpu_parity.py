@@ -305,6 +305,16 @@ def test_int8_full_size_properties(ctx, n, k):
     assert _same_f32(y[ii, jj], want)
 
 
+@pytest.mark.parametrize("nbytes", [16, 4096, 1000003, 48 << 20])
+def test_memcpy_d2d(ctx, nbytes):
+    say(f"memcpy_d2d {nbytes}")
+    src = RNG.integers(0, 256, nbytes, dtype=np.uint8)
+    ds = D.DeviceBuffer.from_host(ctx, src)
+    dd = D.DeviceBuffer.empty(ctx, nbytes, np.uint8)
+    dd.copy_from(ds)
+    assert np.array_equal(dd.download(), src)
+
+
 def test_matmul_integer_node(hip):
     say("MatMulInteger")
     node = S.new_node("mi", S.OperatorType_MatMulInteger)

@@ -188,7 +188,7 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
     if (!wt || !x || !y || m < 0) return set_error(TKV_HIP_BAD_ARG, "linear_forward: bad arguments");
     if (m == 0) return TKV_HIP_OK;
     if (wt->ldk != wt->k)
-        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of 64");
+        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of the GEMM K step (128)");
     const int64_t k = wt->k;
     void* qa;
     TKV_RC_TRY(ctx_workspace(c, 0, (size_t)(m * k), &qa));

@@ -4,6 +4,7 @@
 // DLLs keep implicit (stream, workspace, error text).  State lives in
 // explicit contexts; the only process-wide values are read-only after first
 // use (the environment gate) or per-thread (last error, default context).
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -142,6 +143,18 @@ int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out) {
     return TKV_HIP_OK;
 }
 
+// Plain streaming copy: 16 B per lane, grid-stride.  It reads and writes
+// exactly `n16 * 16` bytes each, which makes it the known-size yardstick that
+// HBM counters (FETCH_SIZE / WRITE_SIZE) are scaled against.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256) k_copy16(const u32x4* __restrict__ src,
+                                               u32x4* __restrict__ dst, int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(&src[i]), &dst[i]);
+}
+
 }  // namespace tkv
 
 using namespace tkv;
@@ -240,6 +253,26 @@ int32_t tkv_hip_memcpy_d2h(int64_t ctx, void* dst, const void* src, int64_t byte
     if (bytes <= 0) return TKV_HIP_OK;
     TKV_HIP_TRY(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, c->stream));
     TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_memcpy_d2d(int64_t ctx, void* dst, const void* src, int64_t bytes) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (bytes <= 0) return TKV_HIP_OK;
+    if (!dst || !src) return set_error(TKV_HIP_BAD_ARG, "memcpy_d2d: NULL pointer");
+    const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) |
+                           (uintptr_t)bytes) & 15) == 0;
+    if (!aligned) {
+        TKV_HIP_TRY(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, c->stream));
+        return TKV_HIP_OK;
+    }
+    const int64_t n16 = bytes / 16;
+    const int64_t want = (n16 + 255) / 256;
+    const unsigned grid = (unsigned)std::min<int64_t>(want, (int64_t)c->num_cus * 8);
+    k_copy16<<<grid, 256, 0, c->stream>>>(static_cast<const u32x4*>(src), static_cast<u32x4*>(dst),
+                                          n16);
+    TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
 

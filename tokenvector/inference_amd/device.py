@@ -85,6 +85,14 @@ class DeviceBuffer:
         _lib.check(_lib.lib().tkv_hip_memcpy_h2d(self.ctx.handle, C.c_void_p(self.ptr),
                                                  arr.ctypes.data_as(C.c_void_p), arr.nbytes))
 
+    def copy_from(self, src: "DeviceBuffer", nbytes: Optional[int] = None) -> None:
+        """Device-to-device copy on the context's stream (asynchronous)."""
+        n = self.nbytes if nbytes is None else int(nbytes)
+        if n > self.nbytes or n > src.nbytes:
+            raise ValueError("copy larger than a buffer")
+        _lib.check(_lib.lib().tkv_hip_memcpy_d2d(self.ctx.handle, C.c_void_p(self.ptr),
+                                                 C.c_void_p(src.ptr), n))
+
     def download(self) -> np.ndarray:
         out = np.empty(self.shape, self.dtype)
         _lib.check(_lib.lib().tkv_hip_memcpy_d2h(self.ctx.handle, out.ctypes.data_as(C.c_void_p),
