@@ -403,6 +403,67 @@ def test_fp8_gemm_fast(ctx, m, n, k):
 
 
 # ---------------------------------------------------------------------------
+# Every GEMM tile configuration (TKV_GEMM_CFG forces one per launch)
+# ---------------------------------------------------------------------------
+
+GEMM_CFGS = list(range(10))
+CFG_SHAPES = [(1, 1, 128), (37, 100, 200), (300, 500, 384), (1100, 2304, 768), (513, 768, 3072)]
+
+
+@pytest.fixture
+def gemm_cfg(monkeypatch):
+    def force(cfg):
+        monkeypatch.setenv("TKV_GEMM_CFG", str(cfg))
+    return force
+
+
+@pytest.mark.parametrize("cfg", GEMM_CFGS)
+def test_gemm_every_config_int8(ctx, gemm_cfg, cfg):
+    """INT32 accumulators (exact) and the per-token / per-channel epilogue
+    (bit-exact) for every tile configuration, ragged and full shapes."""
+    gemm_cfg(cfg)
+    for m, n, k in CFG_SHAPES:
+        say(f"cfg {cfg} int8 {m}x{n}x{k}")
+        a = RNG.integers(-127, 128, (m, k)).astype(np.int8)
+        w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
+        da, dw = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, w)
+        dacc = D.DeviceBuffer.empty(ctx, (m, n), np.int32)
+        D.matmul_int8_accum(ctx, da, dw, m, n, k, dacc)
+        acc = a.astype(np.float64) @ w.astype(np.float64).T       # exact: |acc| < 2^53
+        assert np.array_equal(dacc.download().astype(np.float64), acc), (cfg, m, n, k)
+        sa = RNG.uniform(0.005, 0.05, m).astype(np.float32)
+        sw = RNG.uniform(1e-4, 3e-4, n).astype(np.float32)
+        b = RNG.normal(0, 0.01, n).astype(np.float32)
+        dsa, dsw, db = (D.DeviceBuffer.from_host(ctx, v) for v in (sa, sw, b))
+        dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+        D.matmul_int8(ctx, da, dw, m, n, k, dsa, 1, 0.0, dsw, db, dy)
+        want = ((acc * sa.astype(np.float64)[:, None]) * sw.astype(np.float64)[None, :]
+                + b.astype(np.float64)[None, :]).astype(np.float32)
+        assert _same_f32(dy.download(), want), (cfg, m, n, k)
+
+
+@pytest.mark.parametrize("cfg", GEMM_CFGS)
+def test_gemm_every_config_fp8(ctx, gemm_cfg, cfg):
+    """Both FP8 policies under every tile configuration, to their stated
+    bounds (reference products: 8 * 2^-24 * sum|p| + ulp; fast: 2^-10)."""
+    gemm_cfg(cfg)
+    for m, n, k in [(37, 100, 200), (300, 500, 384)]:
+        say(f"cfg {cfg} fp8 {m}x{n}x{k}")
+        a, w = _fp8_codes((m, k), False), _fp8_codes((n, k), False)
+        b = RNG.normal(0, 1, n).astype(np.float32)
+        da = D.DeviceBuffer.from_host(ctx, (a + 128).astype(np.uint8))
+        dw = D.DeviceBuffer.from_host(ctx, (w + 128).astype(np.uint8))
+        db = D.DeviceBuffer.from_host(ctx, b)
+        dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+        ref, asum, ulp = _fp8_ref(a, w, b, m, n, k)
+        for fast, rel in ((False, 8 * 2.0 ** -24), (True, 2.0 ** -10)):
+            D.matmul_fp8_e4m3(ctx, da, dw, m, n, k, None, 0, None, db, dy, fast=fast)
+            err = np.abs(dy.download().reshape(-1).astype(np.float64) - ref)
+            tol = rel * asum + ulp
+            assert np.all(err <= tol), (cfg, fast, float((err / tol).max()))
+
+
+# ---------------------------------------------------------------------------
 # Resident weights + W8A8 linear (device pointers, no host sync in between)
 # ---------------------------------------------------------------------------
 

@@ -487,8 +487,7 @@ int32_t tkv_hip_dev_quantize_int8_dynamic_tensor(int64_t ctx, const float* x, in
     if (n <= 0 || !params) return set_error(TKV_HIP_BAD_ARG, "empty input or NULL params");
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
-    TKV_RC_TRY(launch_minmax_tensor(c, x, n, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, params));
-    return launch_quant_i8_tensor(c, x, n, params, q, false);
+    return launch_quant_i8_dynamic(c, x, n, TKV_HIP_RECIPE_PRIMARY, params, q, false);
 }
 
 int32_t tkv_hip_dev_quantize_int8_per_channel(int64_t ctx, const float* x, int64_t rows,

@@ -14,6 +14,8 @@
 // Data movement and tiling live in gemm_tile.h.  All arithmetic here is
 // compiled with -ffp-contract=off.
 #include <cstdlib>
+#include <type_traits>
+#include <utility>
 
 #include "gemm_tile.h"
 #include "tkv_internal.h"
@@ -25,131 +27,218 @@ namespace gemm {
 // row (r / 4) * 8 + (lane / 32) * 4 + (r % 4).
 __device__ __forceinline__ int acc_row(int r, int khalf) { return (r >> 2) * 8 + khalf * 4 + (r & 3); }
 
-// Activation scales of this lane's output rows, all loaded before any
-// epilogue arithmetic so their latencies overlap (a single load when the
-// scale is per tensor).
-template <class C>
-__device__ __forceinline__ void row_scales(const float* __restrict__ sa_ptr, int64_t stride, int m0,
-                                           int M, int wm, int khalf, float (&sa)[C::TM][16]) {
-    if (stride == 0) {
-        const float s = sa_ptr[0];
-#pragma unroll
-        for (int i = 0; i < C::TM; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) sa[i][r] = s;
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = m0 + wm * C::WTM + i * 32 + acc_row(r, khalf);
-            sa[i][r] = row < M ? sa_ptr[(int64_t)row * stride] : 0.0f;
-        }
-}
-
 // Output stores bypass cache allocation: Y is written once and not re-read
 // by this kernel, so it should not evict the A / W slices other tiles reuse.
 template <class T>
 __device__ __forceinline__ void put(T* p, T v) { __builtin_nontemporal_store(v, p); }
 
-template <int MODE, int RECIPE>
+// An accumulator value as an opaque register: the epilogue arithmetic of a
+// deferred tile then cannot be hoisted out of the next tile's K loop (where
+// every converted value would occupy registers for the whole loop).
+template <class T>
+__device__ __forceinline__ T pin(T v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Writes part of the calling wave's TM x TN blocks of 32 x 32 outputs of the
+// tile at (m0, n0): parts P0 .. P0 + NP - 1, part p being accumulator
+// registers 4 * (p % 4) .. 4 * (p % 4) + 3 of row block p / 4 (four output
+// rows per lane) across all TN column blocks; C::TM * 4 parts make the tile.
+// value(i, j, r) is the output held in accumulator register r of block
+// (i, j).  Row bases are wave-uniform (scalar registers); the lane part is one
+// 32-bit element offset (launchers keep N < 2^28).  Tiles fully inside
+// [M, N] (all but the edges) store without any checks.
+template <class C, int P0, int NP, class T, class F>
+__device__ __forceinline__ void write_tile(T* __restrict__ Y, int m0, int n0, int M, int N,
+                                           F&& value) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5, lc = lane & 31;
+    const int rbase = m0 + wm * C::WTM, cbase = n0 + wn * C::WTN;
+    const uint32_t loff = (uint32_t)(khalf * 4) * (uint32_t)N + (uint32_t)lc;
+    auto body = [&](auto check) {
+#pragma unroll
+        for (int p = P0; p < P0 + NP; p++) {
+            const int i = p / 4;
+#pragma unroll
+            for (int r = (p % 4) * 4; r < (p % 4) * 4 + 4; r++) {
+                const int rrow = i * 32 + (r >> 2) * 8 + (r & 3);
+                T* rowp = Y + (int64_t)(rbase + rrow) * N + cbase;
+#pragma unroll
+                for (int j = 0; j < C::TN; j++) {
+                    const T v = value(i, j, r);
+                    if (!decltype(check)::value ||
+                        (rbase + rrow + khalf * 4 < M && cbase + j * 32 + lc < N))
+                        put(rowp + loff + j * 32, v);
+                }
+            }
+        }
+    };
+    if (rbase + C::WTM <= M && cbase + C::WTN <= N)
+        body(std::false_type{});
+    else
+        body(std::true_type{});
+}
+
+// INT8 dequant epilogue (MODE = EPI_*, RECIPE = TKV_HIP_RECIPE_*).
+//   per-channel, primary:  y = fl32(fl64(fl64(acc * sa) * sw) + b)
+//     When |acc| < 2^29 (K < 2^15) acc * sa is exact in f64 and so is
+//     sa * sw (24 + 24 bits); then fl64(fl64(acc * sa) * sw) and
+//     fl64(acc * fl64(sa * sw)) both round the same real number once, and the
+//     per-column product c = sa * sw saves one f64 multiply per output
+//     (per-tensor sa only: fold = 1).
+//   symmetric, primary:    y = fl32(fl64(acc * fl32(sa * sw)) + b)
+//   alternate recipes:     the same chains in f32.
+// Per-tile epilogue operands: activation scale(s) of the lane's rows (one
+// per-tensor value, or ROWS: one per accumulator row), weight scale and bias
+// of its columns.  They are loaded when the tile starts: VMEM results retire
+// in issue order, so loads issued before the K loop are complete by the
+// epilogue instead of waiting there behind the previous tile's stores.
+template <class C, bool ROWS>
+struct EpiOperands {
+    float sa_r[ROWS ? C::TM : 1][ROWS ? 16 : 1];
+    float sw[C::TN], b[C::TN];
+    __device__ __forceinline__ float sa(int i, int r) const {
+        if constexpr (ROWS)
+            return sa_r[i][r];
+        else
+            return sa_r[0][0];
+    }
+};
+
+// Rows past M read row M - 1 and columns past N column N - 1 (never stored).
+template <class C, bool ROWS>
+__device__ __forceinline__ void load_operands(const float* __restrict__ sa_ptr, int64_t stride,
+                                              const float* __restrict__ scales_w,
+                                              const float* __restrict__ bias, int m0, int n0,
+                                              int M, int N, EpiOperands<C, ROWS>& o) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
+    if (sa_ptr) {
+        if constexpr (ROWS) {
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + wm * C::WTM + i * 32 + acc_row(r, khalf);
+                    o.sa_r[i][r] = sa_ptr[(int64_t)(row < M ? row : M - 1) * stride];
+                }
+        } else {
+            o.sa_r[0][0] = sa_ptr[0];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) {
+        int col = n0 + wn * C::WTN + j * 32 + (lane & 31);
+        col = col < N ? col : N - 1;
+        o.sw[j] = scales_w ? scales_w[col] : 1.0f;
+        o.b[j] = bias ? bias[col] : 0.0f;
+    }
+}
+
+template <int MODE, int RECIPE, bool ROWS>
 struct EpiI8 {
     const float* scale_a;
     int64_t scale_a_stride;
     float scale_w;
     const float* scales_w;
     const float* bias;
+    int fold;
 
-    template <class C, class P>
-    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN], int m0,
-                                          int n0, int M, int N, void* __restrict__ Y) const {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
-        float sa[C::TM][16];
-        if (MODE != EPI_ACCUM_I32) row_scales<C>(scale_a, scale_a_stride, m0, M, wm, khalf, sa);
+    template <class C>
+    using Operands = EpiOperands<C, ROWS>;
+
+    template <class C>
+    __device__ __forceinline__ Operands<C> load(int m0, int n0, int M, int N) const {
+        Operands<C> o;
+        if (MODE != EPI_ACCUM_I32)
+            load_operands<C, ROWS>(scale_a, scale_a_stride,
+                                   MODE == EPI_PER_CHANNEL ? scales_w : nullptr, bias, m0, n0, M,
+                                   N, o);
+        return o;
+    }
+
+    template <class C, class P, int P0 = 0, int NP = C::TM * 4>
+    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
+                                          const Operands<C>& o, int m0, int n0, int M, int N,
+                                          void* __restrict__ Y) const {
+        if (MODE == EPI_ACCUM_I32) {
+            write_tile<C, P0, NP>(static_cast<int32_t*>(Y), m0, n0, M, N,
+                          [&](int i, int j, int r) { return pin(acc[i][j][r]); });
+            return;
+        }
+        float* Yf = static_cast<float*>(Y);
+        if (MODE == EPI_PER_CHANNEL && RECIPE == TKV_HIP_RECIPE_PRIMARY) {
+            if (fold) {
+                double c[C::TN];
 #pragma unroll
-        for (int j = 0; j < C::TN; j++) {
-            const int col = n0 + wn * C::WTN + j * 32 + (lane & 31);
-            if (col >= N) continue;
-            float sw = 0.0f, b = 0.0f;
-            if (MODE == EPI_PER_CHANNEL) sw = scales_w[col];
-            if (MODE != EPI_ACCUM_I32 && bias) b = bias[col];
-#pragma unroll
-            for (int i = 0; i < C::TM; i++) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * C::WTM + i * 32 + acc_row(r, khalf);
-                    if (row >= M) continue;
-                    const int64_t o = (int64_t)row * N + col;
-                    const int32_t a = acc[i][j][r];
-                    if (MODE == EPI_ACCUM_I32) {
-                        put(reinterpret_cast<int32_t*>(Y) + o, a);
-                        continue;
-                    }
-                    float y;
-                    if (MODE == EPI_PER_CHANNEL) {
-                        if (RECIPE == TKV_HIP_RECIPE_PRIMARY) {
-                            double v = (double)a * (double)sa[i][r];
-                            v = v * (double)sw;
-                            v = v + (double)b;
-                            y = (float)v;
-                        } else {
-                            float t = (float)a * sa[i][r];
-                            t = t * sw;
-                            y = t + b;
-                        }
-                    } else {
-                        const double s = RECIPE == TKV_HIP_RECIPE_PRIMARY
-                                             ? (double)(sa[i][r] * scale_w)
-                                             : (double)sa[i][r] * (double)scale_w;
-                        double v = (double)a * s;
-                        v = v + (double)b;
-                        y = (float)v;
-                    }
-                    put(reinterpret_cast<float*>(Y) + o, y);
-                }
+                for (int j = 0; j < C::TN; j++) c[j] = (double)o.sa(0, 0) * (double)o.sw[j];
+                write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+                    double v = (double)pin(acc[i][j][r]) * c[j];
+                    v = v + (double)o.b[j];
+                    return (float)v;
+                });
+            } else {
+                write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+                    double v = (double)pin(acc[i][j][r]) * (double)o.sa(i, r);
+                    v = v * (double)o.sw[j];
+                    v = v + (double)o.b[j];
+                    return (float)v;
+                });
             }
+        } else if (MODE == EPI_PER_CHANNEL) {
+            write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+                float t = (float)pin(acc[i][j][r]) * o.sa(i, r);
+                t = t * o.sw[j];
+                return t + o.b[j];
+            });
+        } else {
+            write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+                const double s = RECIPE == TKV_HIP_RECIPE_PRIMARY
+                                     ? (double)(o.sa(i, r) * scale_w)
+                                     : (double)o.sa(i, r) * (double)scale_w;
+                double v = (double)pin(acc[i][j][r]) * s;
+                v = v + (double)o.b[j];
+                return (float)v;
+            });
         }
     }
 };
 
-template <bool SCALED>
+// FP8 epilogue: y = fl32(fl64(acc) + b), or with per-token / per-channel
+// scales y = fl32(fl64(fl64(fl64(acc) * sa) * sw) + b).  acc * kAccScale is
+// exact (a power of two undoing the operand pre-scale).
+template <bool SCALED, bool ROWS>
 struct EpiF8 {
     const float* scale_a;  // used when SCALED (extension epilogue)
     int64_t scale_a_stride;
     const float* scales_w;
     const float* bias;
 
-    template <class C, class P>
-    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN], int m0,
-                                          int n0, int M, int N, void* __restrict__ Y) const {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
-        float sa[C::TM][16];
-        if (SCALED) row_scales<C>(scale_a, scale_a_stride, m0, M, wm, khalf, sa);
-#pragma unroll
-        for (int j = 0; j < C::TN; j++) {
-            const int col = n0 + wn * C::WTN + j * 32 + (lane & 31);
-            if (col >= N) continue;
-            const double b = bias ? (double)bias[col] : 0.0;
-            const double sw = SCALED ? (double)scales_w[col] : 1.0;
-#pragma unroll
-            for (int i = 0; i < C::TM; i++) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * C::WTM + i * 32 + acc_row(r, khalf);
-                    if (row >= M) continue;
-                    double v = (double)(acc[i][j][r] * P::kAccScale);  // exact power of 2
-                    if (SCALED) {
-                        v = v * (double)sa[i][r];
-                        v = v * sw;
-                    }
-                    v = v + b;
-                    put(reinterpret_cast<float*>(Y) + (int64_t)row * N + col, (float)v);
-                }
+    template <class C>
+    using Operands = EpiOperands<C, ROWS>;
+
+    template <class C>
+    __device__ __forceinline__ Operands<C> load(int m0, int n0, int M, int N) const {
+        Operands<C> o;
+        load_operands<C, ROWS>(SCALED ? scale_a : nullptr, scale_a_stride,
+                               SCALED ? scales_w : nullptr, bias, m0, n0, M, N, o);
+        return o;
+    }
+
+    template <class C, class P, int P0 = 0, int NP = C::TM * 4>
+    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
+                                          const Operands<C>& o, int m0, int n0, int M, int N,
+                                          void* __restrict__ Y) const {
+        write_tile<C, P0, NP>(static_cast<float*>(Y), m0, n0, M, N, [&](int i, int j, int r) {
+            double v = (double)(pin(acc[i][j][r]) * P::kAccScale);
+            if (SCALED) {
+                v = v * (double)o.sa(i, r);
+                v = v * (double)o.sw[j];
             }
-        }
+            v = v + (double)o.b[j];
+            return (float)v;
+        });
     }
 };
 
@@ -176,6 +265,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm(const uint8_t* __restrict__
             for (int j = 0; j < C::TN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        const auto eo = ep.template load<C>(m0, n0, M, N);
         mainloop<C, P>(A, W, M, N, ldk, m0, n0, smem, acc);
         const int vn = v + (int)gridDim.x;
         const bool more = vn < tiles;
@@ -187,7 +277,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm(const uint8_t* __restrict__
             barrier();  // every wave is done reading the ring
             prologue<C>(A, W, M, N, ldk, m0n, n0n, smem);
         }
-        ep.template store<C, P>(acc, m0, n0, M, N, Y);
+        ep.template store<C, P>(acc, eo, m0, n0, M, N, Y);
         if (!more) break;
         v = vn;
         m0 = m0n;
@@ -195,20 +285,179 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm(const uint8_t* __restrict__
     }
 }
 
+// ep.store of part `part` (wave-uniform, run time) of a tile: a chain of
+// scalar compares selecting the compile-time part.
+template <class C, class P, class E, int... I>
+__device__ __forceinline__ void store_part_dyn(const E& ep, int part,
+                                               const typename P::Acc (&acc)[C::TM][C::TN],
+                                               const typename E::template Operands<C>& o,
+                                               int m0, int n0, int M,
+                                               int N, void* __restrict__ Y,
+                                               std::integer_sequence<int, I...>) {
+    ((part == I ? ep.template store<C, P, I, 1>(acc, o, m0, n0, M, N, Y) : void()), ...);
+}
+
+// Warp-specialised persistent GEMM (CfgWS).  Workgroup b owns tiles b, b + G,
+// ...; its K slices form one stream s = 0 .. my_tiles * nk - 1 that the
+// producer waves keep STAGES - 1 slices ahead of, across tile boundaries.
+// Both roles pass one s_barrier per slice (plus one before the first):
+//   producers: issue slice s + STAGES - 1 into the slot freed by slice s - 1,
+//              wait (own vmcnt) for slice s + 1, barrier;
+//   consumers: MFMAs on slice s, barrier; after a tile's last slice, the
+//              epilogue.  They never wait on vmcnt for operand data, so the
+//              epilogue's stores drain while the next tile's slices stream in.
+// The barrier after slice s both publishes slice s + 1 to the consumers and
+// tells the producers that slice s's slot is free again.
+template <class C, class P, class E>
+__global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restrict__ A,
+                                                        const uint8_t* __restrict__ W, int M,
+                                                        int N, int ldk, E ep,
+                                                        void* __restrict__ Y) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS_BYTES];
+    const int tiles_n = (N + C::BN - 1) / C::BN;
+    const int tiles = ((M + C::BM - 1) / C::BM) * tiles_n;
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    const int my_tiles = b < tiles ? (tiles - 1 - b) / G + 1 : 0;
+    const int nk = ldk / C::BK;
+    const int total = my_tiles * nk;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+
+    if (wave >= C::CW) {
+        // Producer.  `ops` counts this wave's VMEM instructions; done[q % S]
+        // holds the count right after slice q's DMAs, so waiting for slice q
+        // is vmcnt(ops - done[q % S]) (vmcnt retires in issue order).  The
+        // issue cursor (ti, kt) advances without divisions; lane offsets are
+        // recomputed once per tile.
+        const int pw = wave - C::CW;
+        int issued = 0, ops = 0, ti = 0, kt = 0;
+        int done[C::STAGES];
+        WsLane<C> L;
+        const uint8_t *a_tile = A, *w_tile = W;
+        auto issue_next = [&]() {
+            if (kt == 0) {
+                const int t = xcd_tile(b + ti * G, tiles);
+                const int tm = t / tiles_n;
+                const int m0 = tm * C::BM, n0 = (t - tm * tiles_n) * C::BN;
+                a_tile = A + (int64_t)m0 * ldk;
+                w_tile = W + (int64_t)n0 * ldk;
+                ws_lane_offsets<C>(M, N, ldk, m0, n0, pw, lane, L);
+            }
+            const int slot = issued % C::STAGES;
+            ws_issue<C>(a_tile, w_tile, kt * C::BK, L, smem + slot * C::STAGE_BYTES, pw);
+            ops += C::LPS;
+#pragma unroll
+            for (int i = 0; i < C::STAGES; i++)
+                if (i == slot) done[i] = ops;
+            issued++;
+            if (++kt == nk) {
+                kt = 0;
+                ti++;
+            }
+        };
+        auto wait_for = [&](int q) {
+            int d = 0;
+#pragma unroll
+            for (int i = 0; i < C::STAGES; i++)
+                if (i == q % C::STAGES) d = done[i];
+            wait_vmcnt_dyn(ops - d);
+        };
+        while (issued < C::STAGES - 1 && issued < total) issue_next();
+        if (total > 0) wait_for(0);
+        barrier();
+        for (int s = 0; s < total; s++) {
+            if (issued < total) issue_next();
+            if (s + 1 < total) wait_for(s + 1);
+            barrier();
+        }
+        return;
+    }
+
+    const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
+    int a_row[C::TM], w_row[C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) a_row[i] = wm * C::WTM + i * 32 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) w_row[j] = wn * C::WTN + j * 32 + (lane & 31);
+    barrier();
+    int s = 0;
+    if constexpr (!C::DEFER) {
+        for (int ti = 0; ti < my_tiles; ti++) {
+            const int t = xcd_tile(b + ti * G, tiles);
+            const int m0 = (t / tiles_n) * C::BM, n0 = (t % tiles_n) * C::BN;
+            typename P::Acc acc[C::TM][C::TN];
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+            const auto eo = ep.template load<C>(m0, n0, M, N);
+            for (int kt = 0; kt < nk; kt++, s++) {
+                const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
+                P::template slice<C>(sa, sa + C::A_BYTES, a_row, w_row, khalf, acc);
+                barrier();
+            }
+            ep.template store<C, P>(acc, eo, m0, n0, M, N, Y);
+        }
+    } else {
+        // The previous tile's accumulators (pacc) are stored one part per K
+        // slice of the current tile, after that slice's MFMAs are issued.
+        constexpr int NPART = C::TM * 4;
+        typename P::Acc pacc[C::TM][C::TN];
+        typename E::template Operands<C> peo;
+        int pm0 = 0, pn0 = 0;
+        bool have = false;
+        auto store_part = [&](int part) {
+            store_part_dyn<C, P>(ep, part, pacc, peo, pm0, pn0, M, N, Y,
+                                 std::make_integer_sequence<int, NPART>{});
+        };
+        for (int ti = 0; ti < my_tiles; ti++) {
+            const int t = xcd_tile(b + ti * G, tiles);
+            const int m0 = (t / tiles_n) * C::BM, n0 = (t % tiles_n) * C::BN;
+            typename P::Acc acc[C::TM][C::TN];
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+            const auto eo = ep.template load<C>(m0, n0, M, N);
+            for (int kt = 0; kt < nk; kt++, s++) {
+                const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
+                P::template slice<C>(sa, sa + C::A_BYTES, a_row, w_row, khalf, acc);
+                if (have && kt < NPART) store_part(kt);
+                barrier();
+            }
+            if (have)
+                for (int p = nk; p < NPART; p++) store_part(p);
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++) pacc[i][j] = acc[i][j];
+            peo = eo;
+            pm0 = m0;
+            pn0 = n0;
+            have = true;
+        }
+        if (have) ep.template store<C, P>(pacc, peo, pm0, pn0, M, N, Y);
+    }
+}
+
 // ---- tile configurations ---------------------------------------------------
 // K slices are 128 bytes: one full L2 line per row per DMA (64-byte slices
 // fetch every line twice and halve the DMA throughput).
 //            BM   BN  WM WN   BK  STAGES
-typedef Cfg<128, 192, 2, 2, 128, 3> Cfg0;  // 120 KB
-typedef Cfg<64, 192, 2, 2, 128, 3> Cfg1;   //  96 KB, fewer rows when tiles < CUs
-typedef Cfg<128, 128, 2, 2, 128, 3> Cfg2;  //  96 KB, N not a multiple of 192
-typedef Cfg<64, 128, 2, 2, 128, 3> Cfg3;   //  72 KB
-typedef Cfg<128, 192, 2, 2, 128, 2> Cfg4;  //  80 KB, two workgroups per CU
-typedef Cfg<128, 256, 4, 2, 128, 2> Cfg5;  //  96 KB, 8 waves, 32x128 wave tiles
-typedef Cfg<256, 256, 4, 2, 128, 2> Cfg6;  // 128 KB, 8 waves, 64x128 wave tiles
-typedef Cfg<256, 192, 4, 2, 128, 2> Cfg7;  // 112 KB, 8 waves, 64x96 wave tiles
-typedef Cfg<128, 192, 4, 2, 128, 3> Cfg8;  // 120 KB, 8 waves, 32x96 wave tiles
-typedef Cfg<128, 192, 2, 2, 64, 4> Cfg9;   //  80 KB, 64-byte slices
+typedef Cfg<64, 128, 2, 2, 128, 3> Cfg0;   //  72 KB, small M (tiles < CUs)
+typedef Cfg<128, 192, 4, 2, 128, 3> Cfg1;  // 120 KB, 8 waves, 32x96 wave tiles
+// warp-specialised:  BM   BN  WM WN   BK  STAGES PW DEFER
+typedef CfgWS<128, 192, 4, 2, 128, 3, 4> Cfg2;     // 120 KB, 8 consumers (32x96) + 4 producers
+typedef CfgWS<128, 192, 2, 2, 128, 3, 4> Cfg3;     // 120 KB, 4 consumers (64x96) + 4 producers
+typedef CfgWS<128, 128, 2, 2, 128, 3, 4> Cfg4;     //  96 KB, 4 consumers (64x64) + 4 producers
+typedef CfgWS<64, 128, 2, 2, 128, 3, 4> Cfg5;      //  72 KB, 4 consumers (32x64) + 4 producers
+typedef CfgWS<128, 192, 4, 2, 128, 4, 4> Cfg6;     // 160 KB, 3 slices in flight
+typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 1> Cfg7;  // Cfg2 + stores deferred into next tile
+typedef CfgWS<128, 128, 2, 2, 128, 3, 4, 1> Cfg8;  // Cfg4 + deferred stores
+typedef CfgWS<128, 192, 4, 2, 128, 4, 4, 1> Cfg9;  // Cfg6 + deferred stores
 
 constexpr int kBK = 128;
 
@@ -218,15 +467,17 @@ static int64_t tiles_of(int64_t m, int64_t n) {
 }
 
 // Tile choice: the largest tile that still gives every CU work.  The
-// environment variable TKV_GEMM_CFG (0..9) forces one (tuning sweeps).
+// environment variable TKV_GEMM_CFG (0..9; 2.. are the warp-specialised
+// configurations) forces one (tuning sweeps).
 static int pick_cfg(Ctx* c, int64_t m, int64_t n) {
     if (const char* v = getenv("TKV_GEMM_CFG")) {
         int f = atoi(v);
         if (f >= 0 && f <= 9) return f;
     }
-    // 128x192 with 8 waves measured best on all four GPT-2 shapes at M=8192;
-    // smaller 64x128 tiles keep every CU busy when M is small.
-    return tiles_of<Cfg8>(m, n) >= c->num_cus ? 8 : 3;
+    // Warp-specialised 128x192 tiles with deferred stores measured best on all
+    // four GPT-2 shapes at M = 8192; 64x128 tiles keep every CU busy when M
+    // is small.
+    return tiles_of<Cfg7>(m, n) >= c->num_cus ? 7 : 0;
 }
 
 template <class C, class P, class E>
@@ -244,20 +495,33 @@ static int launch_cfg(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
     return TKV_HIP_OK;
 }
 
+template <class C, class P, class E>
+static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
+                     int64_t ldk, const E& ep, void* y) {
+    const int64_t per_cu = 163840 / C::LDS_BYTES > 0 ? 163840 / C::LDS_BYTES : 1;
+    const int64_t resident = (int64_t)c->num_cus * per_cu;
+    const int64_t tiles = tiles_of<C>(m, n);
+    const int64_t grid = tiles < resident ? tiles : resident;
+    hipLaunchKernelGGL((k_gemm_ws<C, P, E>), dim3((unsigned)grid), dim3(C::THREADS), 0,
+                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
 template <class P, class E>
 static int launch_any(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                       int64_t ldk, const E& ep, void* y) {
     switch (pick_cfg(c, m, n)) {
         case 0: return launch_cfg<Cfg0, P>(c, a, w, m, n, ldk, ep, y);
         case 1: return launch_cfg<Cfg1, P>(c, a, w, m, n, ldk, ep, y);
-        case 2: return launch_cfg<Cfg2, P>(c, a, w, m, n, ldk, ep, y);
-        case 3: return launch_cfg<Cfg3, P>(c, a, w, m, n, ldk, ep, y);
-        case 4: return launch_cfg<Cfg4, P>(c, a, w, m, n, ldk, ep, y);
-        case 5: return launch_cfg<Cfg5, P>(c, a, w, m, n, ldk, ep, y);
-        case 6: return launch_cfg<Cfg6, P>(c, a, w, m, n, ldk, ep, y);
-        case 7: return launch_cfg<Cfg7, P>(c, a, w, m, n, ldk, ep, y);
-        case 8: return launch_cfg<Cfg8, P>(c, a, w, m, n, ldk, ep, y);
-        default: return launch_cfg<Cfg9, P>(c, a, w, m, n, ldk, ep, y);
+        case 2: return launch_ws<Cfg2, P>(c, a, w, m, n, ldk, ep, y);
+        case 3: return launch_ws<Cfg3, P>(c, a, w, m, n, ldk, ep, y);
+        case 4: return launch_ws<Cfg4, P>(c, a, w, m, n, ldk, ep, y);
+        case 5: return launch_ws<Cfg5, P>(c, a, w, m, n, ldk, ep, y);
+        case 6: return launch_ws<Cfg6, P>(c, a, w, m, n, ldk, ep, y);
+        case 7: return launch_ws<Cfg7, P>(c, a, w, m, n, ldk, ep, y);
+        case 8: return launch_ws<Cfg8, P>(c, a, w, m, n, ldk, ep, y);
+        default: return launch_ws<Cfg9, P>(c, a, w, m, n, ldk, ep, y);
     }
 }
 
@@ -284,9 +548,9 @@ static int prepare_operands(Ctx* c, const void** a, const void** w, int64_t m, i
 }
 
 static int check_sizes(int64_t m, int64_t n, int64_t k, const char* what) {
-    if (k <= 0 || m >= (1ll << 31) || n >= (1ll << 31) || k >= (1ll << 17))
+    if (k <= 0 || m >= (1ll << 31) || n >= (1ll << 28) || k >= (1ll << 17))
         return set_error(TKV_HIP_UNSUPPORTED,
-                         std::string(what) + ": K must be in [1, 2^17) and M, N < 2^31");
+                         std::string(what) + ": K must be in [1, 2^17), M < 2^31 and N < 2^28");
     return TKV_HIP_OK;
 }
 
@@ -303,20 +567,31 @@ int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t 
     TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));
     const uint8_t* ua = static_cast<const uint8_t*>(pa);
     const uint8_t* uw = static_cast<const uint8_t*>(pw);
-#define TKV_EPI(MODE, RECIPE)                                                                \
-    gemm::launch_any<gemm::PolicyI8>(                                                        \
-        c, ua, uw, m, n, ldk,                                                                \
-        gemm::EpiI8<MODE, RECIPE>{e.scale_a, e.scale_a_stride, e.scale_w, e.scales_w, e.bias}, y)
+#define TKV_EPI(MODE, RECIPE, ROWS)                                                          \
+    gemm::launch_any<gemm::PolicyI8>(c, ua, uw, m, n, ldk,                                   \
+                                     gemm::EpiI8<MODE, RECIPE, ROWS>{e.scale_a, e.scale_a_stride, \
+                                                                     e.scale_w, e.scales_w,   \
+                                                                     e.bias, fold},           \
+                                     y)
     const bool primary = e.recipe == TKV_HIP_RECIPE_PRIMARY;
+    const bool rows = e.scale_a_stride != 0;
+    // |acc| <= 128^2 * K < 2^29 makes acc * scale_a exact in f64
+    const int fold = (!rows && k < (1 << 15)) ? 1 : 0;
     switch (e.mode) {
         case EPI_PER_CHANNEL:
-            return primary ? TKV_EPI(EPI_PER_CHANNEL, TKV_HIP_RECIPE_PRIMARY)
-                           : TKV_EPI(EPI_PER_CHANNEL, TKV_HIP_RECIPE_ALTERNATE);
+            if (rows)
+                return primary ? TKV_EPI(EPI_PER_CHANNEL, TKV_HIP_RECIPE_PRIMARY, true)
+                               : TKV_EPI(EPI_PER_CHANNEL, TKV_HIP_RECIPE_ALTERNATE, true);
+            return primary ? TKV_EPI(EPI_PER_CHANNEL, TKV_HIP_RECIPE_PRIMARY, false)
+                           : TKV_EPI(EPI_PER_CHANNEL, TKV_HIP_RECIPE_ALTERNATE, false);
         case EPI_SYMMETRIC:
-            return primary ? TKV_EPI(EPI_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY)
-                           : TKV_EPI(EPI_SYMMETRIC, TKV_HIP_RECIPE_ALTERNATE);
+            if (rows)
+                return primary ? TKV_EPI(EPI_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, true)
+                               : TKV_EPI(EPI_SYMMETRIC, TKV_HIP_RECIPE_ALTERNATE, true);
+            return primary ? TKV_EPI(EPI_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, false)
+                           : TKV_EPI(EPI_SYMMETRIC, TKV_HIP_RECIPE_ALTERNATE, false);
         default:
-            return TKV_EPI(EPI_ACCUM_I32, TKV_HIP_RECIPE_PRIMARY);
+            return TKV_EPI(EPI_ACCUM_I32, TKV_HIP_RECIPE_PRIMARY, false);
     }
 #undef TKV_EPI
 }
@@ -333,12 +608,17 @@ int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_
     TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));
     const uint8_t* ua = static_cast<const uint8_t*>(pa);
     const uint8_t* uw = static_cast<const uint8_t*>(pw);
-    if (scales_w) {
-        gemm::EpiF8<true> ep{scale_a, scale_a_stride, scales_w, bias};
+    if (scales_w && scale_a_stride != 0) {
+        gemm::EpiF8<true, true> ep{scale_a, scale_a_stride, scales_w, bias};
         return fast ? gemm::launch_any<gemm::PolicyF8>(c, ua, uw, m, n, ldk, ep, y)
                     : gemm::launch_any<gemm::PolicyF8Ref>(c, ua, uw, m, n, ldk, ep, y);
     }
-    gemm::EpiF8<false> ep{nullptr, 0, nullptr, bias};
+    if (scales_w) {
+        gemm::EpiF8<true, false> ep{scale_a, 0, scales_w, bias};
+        return fast ? gemm::launch_any<gemm::PolicyF8>(c, ua, uw, m, n, ldk, ep, y)
+                    : gemm::launch_any<gemm::PolicyF8Ref>(c, ua, uw, m, n, ldk, ep, y);
+    }
+    gemm::EpiF8<false, false> ep{nullptr, 0, nullptr, bias};
     return fast ? gemm::launch_any<gemm::PolicyF8>(c, ua, uw, m, n, ldk, ep, y)
                 : gemm::launch_any<gemm::PolicyF8Ref>(c, ua, uw, m, n, ldk, ep, y);
 }

@@ -51,11 +51,51 @@ struct Cfg {
     static constexpr int A_BYTES = BM * BK, W_BYTES = BN * BK;
     static constexpr int STAGE_BYTES = A_BYTES + W_BYTES;
     static constexpr int LDS_BYTES = STAGE_BYTES * STAGES;
+    static constexpr int FRAG_DEPTH = BK / 32;  // k-steps of fragments read ahead (all)
+    static constexpr int DEFER = 0;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32x32 blocks");
     static_assert(BM % (ROWS_PER_DMA * WAVES) == 0 && BN % (ROWS_PER_DMA * WAVES) == 0,
                   "tile rows must split evenly over wave DMAs");
     static_assert(LDS_BYTES <= 163840, "LDS capacity of a gfx950 workgroup");
     static_assert(LPS * (STAGES - 1) <= 63, "vmcnt range");
+};
+
+// Warp-specialised variant: CW = WM x WN consumer waves read LDS, run the
+// MFMAs and the epilogue; PW producer waves only issue the operand DMA.
+// vmcnt is per wave and retires in issue order, so when one wave issued both
+// DMA and output stores, every wait for the next slice also waited for the
+// stores issued before it.  With the roles split, the consumers' stores
+// drain while the producers keep the ring full, and no consumer ever waits on
+// vmcnt for operand data.
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int PW_, int DEFER_ = 0,
+          int FD_ = 0>
+struct CfgWS {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_, STAGES = STAGES_;
+    static constexpr int CW = WM * WN, PW = PW_;
+    static constexpr int WAVES = CW + PW;
+    static constexpr int THREADS = WAVES * 64;
+    static constexpr int WTM = BM / WM, WTN = BN / WN;
+    static constexpr int TM = WTM / 32, TN = WTN / 32;
+    static constexpr int CH = BK / 16;
+    static constexpr int ROWS_PER_DMA = 64 / CH;
+    static constexpr int A_BLK = BM / ROWS_PER_DMA, W_BLK = BN / ROWS_PER_DMA;
+    static constexpr int LPS = (A_BLK + W_BLK) / PW;  // DMA instructions per producer wave per slice
+    static constexpr int A_BYTES = BM * BK, W_BYTES = BN * BK;
+    static constexpr int STAGE_BYTES = A_BYTES + W_BYTES;
+    static constexpr int LDS_BYTES = STAGE_BYTES * STAGES;
+    // DEFER: a tile's output stores are spread over the next tile's K slices
+    // (the consumer keeps the finished accumulators), so HBM writes proceed
+    // during the MFMA work instead of in bursts between tiles.  The extra
+    // accumulator set is paid for by reading fragments only two k-steps ahead.
+    // FD (fragment depth, k-steps read ahead; 0 = automatic) trades registers
+    // for LDS latency hiding, e.g. to fit four waves per SIMD.
+    static constexpr int DEFER = DEFER_;
+    static constexpr int FRAG_DEPTH = FD_ ? FD_ : (DEFER ? 2 : BK / 32);
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32x32 blocks");
+    static_assert(BM % ROWS_PER_DMA == 0 && BN % ROWS_PER_DMA == 0, "rows per DMA block");
+    static_assert((A_BLK + W_BLK) % PW == 0, "DMA blocks must split evenly over producers");
+    static_assert(LDS_BYTES <= 163840, "LDS capacity of a gfx950 workgroup");
+    static_assert(STAGES >= 2 && LPS * (STAGES - 1) <= 63, "vmcnt range");
 };
 
 // Chunk swizzle for 64 banks: rows r..r+15 at the same logical chunk map to 16
@@ -73,9 +113,20 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Workgroup barrier without the workgroup-scope memory fence of
-// __syncthreads (which would drain every outstanding DMA with vmcnt(0));
-// the "memory" clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+// __syncthreads (which would drain every outstanding DMA with vmcnt(0)).
+// s_barrier itself does not wait for memory operations: lgkmcnt(0) first
+// makes this wave's LDS reads complete, so a slot released by the barrier is
+// no longer being read when a producer's DMA refills it.  The "memory"
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar)
+// value: tile offsets derived from it stay in SGPRs.
+__device__ __forceinline__ int wave_id() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
 
 // Tile order: contiguous tile ranges per XCD (workgroups are dispatched to
 // XCDs round-robin by workgroup id).
@@ -114,6 +165,59 @@ __device__ __forceinline__ void issue_slice(const uint8_t* __restrict__ A,
     }
 }
 
+// Producer wave `pw` of a CfgWS workgroup owns DMA blocks d * PW + pw
+// (d < LPS) of every slice; block b fills LDS bytes [b * 1024, b * 1024 +
+// 1024) of the slot, A blocks first.  WsLane holds, for the current tile, the
+// lane's byte offset of each block relative to the tile's first A or W row
+// (32-bit: below 256 * 2^17), so issuing a slice costs one scalar base and no
+// per-lane address arithmetic.
+template <class C>
+struct WsLane {
+    uint32_t off[C::LPS];
+};
+
+template <class C>
+__device__ __forceinline__ void ws_lane_offsets(int M, int N, int ldk, int m0, int n0, int pw,
+                                                int lane, WsLane<C>& L) {
+    const int lrow = lane / C::CH, lch = lane % C::CH;
+#pragma unroll
+    for (int d = 0; d < C::LPS; d++) {
+        const int blk = d * C::PW + pw;
+        const bool is_a = blk < C::A_BLK;
+        const int row = (is_a ? blk : blk - C::A_BLK) * C::ROWS_PER_DMA + lrow;
+        const int c = lch ^ swz<C::CH>(row);
+        const int lim = is_a ? M - 1 - m0 : N - 1 - n0;  // rows past the matrix read its last row
+        L.off[d] = (uint32_t)(row < lim ? row : lim) * (uint32_t)ldk + (uint32_t)(c * 16);
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void ws_issue(const uint8_t* __restrict__ a_tile,
+                                         const uint8_t* __restrict__ w_tile, int k0,
+                                         const WsLane<C>& L, uint8_t* slot, int pw) {
+#pragma unroll
+    for (int d = 0; d < C::LPS; d++) {
+        const int blk = d * C::PW + pw;
+        const bool is_a = blk < C::A_BLK;
+        const uint8_t* base = (is_a ? a_tile : w_tile) + k0;
+        uint8_t* dst = slot + (is_a ? blk * 1024 : C::A_BYTES + (blk - C::A_BLK) * 1024);
+        __builtin_amdgcn_global_load_lds((const void*)(base + L.off[d]), (lds_ptr)dst, 16, 0, 0);
+    }
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform run-time n in [0, 63].
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+    switch (n) {
+#define TKV_W(i) case i: wait_vmcnt<i>(); break;
+#define TKV_W8(i) TKV_W(i) TKV_W(i + 1) TKV_W(i + 2) TKV_W(i + 3) TKV_W(i + 4) TKV_W(i + 5) \
+    TKV_W(i + 6) TKV_W(i + 7)
+        TKV_W8(0) TKV_W8(8) TKV_W8(16) TKV_W8(24) TKV_W8(32) TKV_W8(40) TKV_W8(48) TKV_W8(56)
+#undef TKV_W8
+#undef TKV_W
+        default: wait_vmcnt<0>(); break;
+    }
+}
+
 template <class C>
 __device__ __forceinline__ v4i lds_chunk(const uint8_t* base, int row, int ch) {
     return *reinterpret_cast<const v4i*>(base + row * C::BK + ((ch ^ swz<C::CH>(row)) << 4));
@@ -137,7 +241,7 @@ template <class C>
 __device__ __forceinline__ void prologue(const uint8_t* __restrict__ A,
                                          const uint8_t* __restrict__ W, int M, int N, int ldk,
                                          int m0, int n0, uint8_t* smem) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int nk = ldk / C::BK;
 #pragma unroll
     for (int s = 0; s < C::STAGES - 1; s++)
@@ -157,7 +261,7 @@ __device__ __forceinline__ void mainloop(const uint8_t* __restrict__ A,
                                          const uint8_t* __restrict__ W, int M, int N, int ldk,
                                          int m0, int n0, uint8_t* smem,
                                          typename P::Acc (&acc)[C::TM][C::TN]) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int wm = wave / C::WN, wn = wave % C::WN;
     const int nk = ldk / C::BK;
     int a_row[C::TM], w_row[C::TN];
@@ -187,51 +291,42 @@ __device__ __forceinline__ void mainloop(const uint8_t* __restrict__ A,
     }
 }
 
-// Interleave the next step's LDS fragment reads with this step's MFMAs
-// (one ds_read after each MFMA while both remain), so LDS latency hides
-// behind MFMA execution instead of stalling the pipe at every step.
-template <int NMFMA, int NREAD>
-__device__ __forceinline__ void interleave_mfma_reads() {
-#pragma unroll
-    for (int i = 0; i < NMFMA; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    }
-#pragma unroll
-    for (int i = NMFMA; i < NREAD; i++) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-}
-
 // INT8: v_mfma_i32_32x32x32_i8, 16 K-bytes per lane per 32-K step.
 struct PolicyI8 {
     typedef v16i Acc;
+    // Fragments are read C::FRAG_DEPTH k-steps ahead of the MFMAs that use
+    // them, with scheduling barriers between the groups: ds_read returns in
+    // order, so each MFMA waits only for its own operands (lgkmcnt(n), n =
+    // reads issued after them) while later reads overlap earlier MFMAs.
+    // Without the barriers the scheduler sinks every read down to its use and
+    // exposes the LDS latency before each MFMA.
     template <class C>
     __device__ __forceinline__ static void slice(const uint8_t* sa, const uint8_t* sw,
                                                  const int (&a_row)[C::TM],
                                                  const int (&w_row)[C::TN], int khalf,
                                                  Acc (&acc)[C::TM][C::TN]) {
-        constexpr int KS = C::BK / 32;
-        v4i af[2][C::TM], bf[2][C::TN];
+        constexpr int KS = C::BK / 32, D = C::FRAG_DEPTH;
+        v4i af[KS][C::TM], bf[KS][C::TN];
+        auto load = [&](int ks) {
+            const int ch = ks * 2 + khalf;
 #pragma unroll
-        for (int i = 0; i < C::TM; i++) af[0][i] = lds_chunk<C>(sa, a_row[i], khalf);
+            for (int i = 0; i < C::TM; i++) af[ks][i] = lds_chunk<C>(sa, a_row[i], ch);
 #pragma unroll
-        for (int j = 0; j < C::TN; j++) bf[0][j] = lds_chunk<C>(sw, w_row[j], khalf);
+            for (int j = 0; j < C::TN; j++) bf[ks][j] = lds_chunk<C>(sw, w_row[j], ch);
+        };
+#pragma unroll
+        for (int ks = 0; ks < D - 1 && ks < KS; ks++) load(ks);
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const int cur = ks & 1, nx = cur ^ 1;
-            if (ks + 1 < KS) {
-                const int ch = (ks + 1) * 2 + khalf;
-#pragma unroll
-                for (int i = 0; i < C::TM; i++) af[nx][i] = lds_chunk<C>(sa, a_row[i], ch);
-#pragma unroll
-                for (int j = 0; j < C::TN; j++) bf[nx][j] = lds_chunk<C>(sw, w_row[j], ch);
-            }
+            if (ks + D - 1 < KS) load(ks + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < C::TM; i++)
 #pragma unroll
                 for (int j = 0; j < C::TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][i], bf[cur][j],
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j],
                                                                       acc[i][j], 0, 0, 0);
-            if (ks + 1 < KS) interleave_mfma_reads<C::TM * C::TN, C::TM + C::TN>();
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 };
@@ -247,18 +342,34 @@ struct PolicyF8 {
                                                  const int (&a_row)[C::TM],
                                                  const int (&w_row)[C::TN], int khalf,
                                                  Acc (&acc)[C::TM][C::TN]) {
+        constexpr int KS = C::BK / 64;
+        v4i alo[KS][C::TM], ahi[KS][C::TM], blo[KS][C::TN], bhi[KS][C::TN];
 #pragma unroll
-        for (int ks = 0; ks < C::BK / 64; ks++) {
+        for (int ks = 0; ks < KS; ks++) {
             const int ch = ks * 4 + khalf * 2;
+#pragma unroll
+            for (int i = 0; i < C::TM; i++) {
+                alo[ks][i] = lds_chunk<C>(sa, a_row[i], ch);
+                ahi[ks][i] = lds_chunk<C>(sa, a_row[i], ch + 1);
+            }
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                blo[ks][j] = lds_chunk<C>(sw, w_row[j], ch);
+                bhi[ks][j] = lds_chunk<C>(sw, w_row[j], ch + 1);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
             v8i af[C::TM], bf[C::TN];
 #pragma unroll
             for (int i = 0; i < C::TM; i++) {
-                v4i lo = lds_chunk<C>(sa, a_row[i], ch), hi = lds_chunk<C>(sa, a_row[i], ch + 1);
+                const v4i lo = alo[ks][i], hi = ahi[ks][i];
                 af[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
-                v4i lo = lds_chunk<C>(sw, w_row[j], ch), hi = lds_chunk<C>(sw, w_row[j], ch + 1);
+                const v4i lo = blo[ks][j], hi = bhi[ks][j];
                 bf[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
 #pragma unroll
@@ -315,23 +426,28 @@ struct PolicyF8Ref {
                                                  const int (&a_row)[C::TM],
                                                  const int (&w_row)[C::TN], int khalf,
                                                  Acc (&acc)[C::TM][C::TN]) {
+        constexpr int KS = C::BK / 32;  // 16 K-bytes per lane per 32-K step
+        v4i af[KS][C::TM], bf[KS][C::TN];
 #pragma unroll
-        for (int ks = 0; ks < C::BK / 32; ks++) {
-            const int ch = ks * 2 + khalf;  // 16 K-bytes per lane per 32-K step
-            v4i af[C::TM], bf[C::TN];
+        for (int ks = 0; ks < KS; ks++) {
+            const int ch = ks * 2 + khalf;
 #pragma unroll
-            for (int i = 0; i < C::TM; i++) af[i] = lds_chunk<C>(sa, a_row[i], ch);
+            for (int i = 0; i < C::TM; i++) af[ks][i] = lds_chunk<C>(sa, a_row[i], ch);
 #pragma unroll
-            for (int j = 0; j < C::TN; j++) bf[j] = lds_chunk<C>(sw, w_row[j], ch);
+            for (int j = 0; j < C::TN; j++) bf[ks][j] = lds_chunk<C>(sw, w_row[j], ch);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 v8h ah[C::TM], bh[C::TN];
 #pragma unroll
                 for (int i = 0; i < C::TM; i++)
-                    ah[i] = dec8_f16((uint32_t)af[i][2 * h], (uint32_t)af[i][2 * h + 1]);
+                    ah[i] = dec8_f16((uint32_t)af[ks][i][2 * h], (uint32_t)af[ks][i][2 * h + 1]);
 #pragma unroll
                 for (int j = 0; j < C::TN; j++)
-                    bh[j] = dec8_f16((uint32_t)bf[j][2 * h], (uint32_t)bf[j][2 * h + 1]);
+                    bh[j] = dec8_f16((uint32_t)bf[ks][j][2 * h], (uint32_t)bf[ks][j][2 * h + 1]);
 #pragma unroll
                 for (int i = 0; i < C::TM; i++)
 #pragma unroll

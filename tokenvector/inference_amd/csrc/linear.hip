@@ -201,8 +201,7 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
         ep.scales_w = wt->scales;
         ep.bias = wt->bias;
         if (act_mode == TKV_HIP_ACT_PER_TENSOR) {
-            TKV_RC_TRY(launch_minmax_tensor(c, x, m * k, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, ap));
-            TKV_RC_TRY(launch_quant_i8_tensor(c, x, m * k, ap, qa, false));
+            TKV_RC_TRY(launch_quant_i8_dynamic(c, x, m * k, TKV_HIP_RECIPE_PRIMARY, ap, qa, false));
             ep.scale_a = &ap->scale;
             ep.scale_a_stride = 0;
         } else if (act_mode == TKV_HIP_ACT_PER_TOKEN) {

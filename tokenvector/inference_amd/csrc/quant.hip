@@ -5,8 +5,10 @@
 //
 // Layout: f32 inputs are read as 16-byte float4 loads, four per thread per
 // loop trip for memory-level parallelism; int8 / e4m3 outputs leave as one
-// 32-bit store per float4.  Reductions use wave64 shuffles, then LDS, then a
-// last-block-done finalize (no grid barrier, no per-call memset).
+// 32-bit store per float4.  Reductions use wave64 shuffles, then LDS, then
+// one partial per block; the consumer of the partials (a one-block finalize,
+// or every block of the quantize kernel) reduces them after the kernel
+// boundary, which orders them across XCDs without device-scope fences.
 //
 // Numerics restate tv/quantization/engine.tkv and types.tkv exactly: f64
 // products and reciprocals where the reference computes in f64, round half to
@@ -19,6 +21,7 @@
 namespace tkv {
 
 constexpr int kBlock = 256;
+constexpr int kRedBlock = 1024;  // calibration partial blocks: one per CU
 constexpr int kUnroll = 4;
 
 // ---------------------------------------------------------------------------
@@ -97,13 +100,13 @@ __device__ __forceinline__ void mm_acc(float v, int64_t idx, bool track_zero, fl
 // before the finalize reads, across XCDs and their separate L2s, without
 // device-scope fences in the streaming kernel.
 template <bool TRACK_ZERO>
-__global__ __launch_bounds__(kBlock) void k_minmax_partials(const float* __restrict__ x,
-                                                            int64_t n, int vec,
-                                                            RedPartial* __restrict__ partials) {
+__global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __restrict__ x,
+                                                               int64_t n, int vec,
+                                                               RedPartial* __restrict__ partials) {
     float mn = __builtin_inff(), mx = -__builtin_inff();
     unsigned long long zi = ~0ull;
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kRedBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kRedBlock + threadIdx.x;
     int64_t n4 = vec ? n / 4 : 0;
     const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
     int64_t i = tid;
@@ -129,8 +132,8 @@ __global__ __launch_bounds__(kBlock) void k_minmax_partials(const float* __restr
     }
     for (int64_t j = n4 * 4 + tid; j < n; j += stride) mm_acc(x[j], j, TRACK_ZERO, mn, mx, zi);
 
-    __shared__ float s_mn[kBlock / 64], s_mx[kBlock / 64];
-    __shared__ unsigned long long s_zi[kBlock / 64];
+    __shared__ float s_mn[kRedBlock / 64], s_mx[kRedBlock / 64];
+    __shared__ unsigned long long s_zi[kRedBlock / 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     mn = wave_min(mn);
     mx = wave_max(mx);
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(kBlock) void k_minmax_partials(const float* __restr
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < kBlock / 64; w++) {
+        for (int w = 1; w < kRedBlock / 64; w++) {
             mn = fminf(mn, s_mn[w]);
             mx = fmaxf(mx, s_mx[w]);
             zi = s_zi[w] < zi ? s_zi[w] : zi;
@@ -155,11 +158,14 @@ __global__ __launch_bounds__(kBlock) void k_minmax_partials(const float* __restr
     }
 }
 
-__global__ __launch_bounds__(kBlock) void k_minmax_finalize(const float* __restrict__ x,
-                                                            int nparts, int track_zero, int mode,
-                                                            int recipe,
-                                                            const RedPartial* __restrict__ partials,
-                                                            tkv_hip_qparams_dev* __restrict__ out) {
+// Reduces the per-block partials (every thread of a kBlock-thread block
+// takes part; the result is returned to all of them) to the reference's f64
+// min / max locals.  The reference keeps the first element reaching an
+// extreme; values that compare equal are bit-identical except +-0, so a zero
+// extreme takes the sign of the first zero in index order.
+__device__ void reduce_partials(const float* __restrict__ x, int nparts, int track_zero,
+                                const RedPartial* __restrict__ partials, double& dmn,
+                                double& dmx) {
     float mn = __builtin_inff(), mx = -__builtin_inff();
     unsigned long long zi = ~0ull;
     for (int b = threadIdx.x; b < nparts; b += kBlock) {
@@ -180,44 +186,63 @@ __global__ __launch_bounds__(kBlock) void k_minmax_finalize(const float* __restr
         s_zi[wave] = zi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < kBlock / 64; w++) {
-            mn = fminf(mn, s_mn[w]);
-            mx = fmaxf(mx, s_mx[w]);
-            zi = s_zi[w] < zi ? s_zi[w] : zi;
-        }
-        double dmn = mn, dmx = mx;
-        // The reference keeps the first element reaching the extreme; values
-        // that compare equal are bit-identical except +-0, so a zero extreme
-        // takes the sign of the first zero in index order.
-        if (track_zero && zi != ~0ull) {
-            double z = x[zi];
-            if (mn == 0.0f) dmn = z;
-            if (mx == 0.0f) dmx = z;
-        }
-        finalize_minmax(dmn, dmx, mode, recipe, out);
+    mn = s_mn[0];
+    mx = s_mx[0];
+    zi = s_zi[0];
+    for (int w = 1; w < kBlock / 64; w++) {
+        mn = fminf(mn, s_mn[w]);
+        mx = fmaxf(mx, s_mx[w]);
+        zi = s_zi[w] < zi ? s_zi[w] : zi;
     }
+    dmn = mn;
+    dmx = mx;
+    if (track_zero && zi != ~0ull) {
+        const double z = x[zi];
+        if (mn == 0.0f) dmn = z;
+        if (mx == 0.0f) dmx = z;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_minmax_finalize(const float* __restrict__ x,
+                                                            int nparts, int track_zero, int mode,
+                                                            int recipe,
+                                                            const RedPartial* __restrict__ partials,
+                                                            tkv_hip_qparams_dev* __restrict__ out) {
+    double dmn, dmx;
+    reduce_partials(x, nparts, track_zero, partials, dmn, dmx);
+    if (threadIdx.x == 0) finalize_minmax(dmn, dmx, mode, recipe, out);
+}
+
+// One partial per CU (kRedBlock threads each, for enough loads in flight):
+// few enough that every block of a consumer kernel can reduce them itself.
+static int64_t partial_blocks(Ctx* c, int64_t work) {
+    int64_t blocks = ceil_div(work, (int64_t)kRedBlock * kUnroll);
+    const int64_t cap = c->num_cus < kMaxReduceBlocks ? c->num_cus : kMaxReduceBlocks;
+    if (blocks > cap) blocks = cap;
+    return blocks < 1 ? 1 : blocks;
+}
+
+static int launch_partials(Ctx* c, const float* x, int64_t n, int track_zero, int64_t* nparts) {
+    const int vec = aligned(x, 16) ? 1 : 0;
+    const int64_t blocks = partial_blocks(c, vec ? n / 4 : n);
+    if (track_zero)
+        hipLaunchKernelGGL(k_minmax_partials<true>, dim3((unsigned)blocks), dim3(kRedBlock), 0,
+                           c->stream, x, n, vec, c->partials);
+    else
+        hipLaunchKernelGGL(k_minmax_partials<false>, dim3((unsigned)blocks), dim3(kRedBlock), 0,
+                           c->stream, x, n, vec, c->partials);
+    TKV_LAUNCH_CHECK();
+    *nparts = blocks;
+    return TKV_HIP_OK;
 }
 
 int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe,
                          tkv_hip_qparams_dev* out) {
-    int vec = aligned(x, 16) ? 1 : 0;
-    int64_t work = vec ? n / 4 : n;
-    int64_t blocks = ceil_div(work, (int64_t)kBlock * kUnroll);
-    int64_t cap = (int64_t)c->num_cus * 8;
-    if (cap > kMaxReduceBlocks) cap = kMaxReduceBlocks;
-    if (blocks > cap) blocks = cap;
-    if (blocks < 1) blocks = 1;
     // Only the asymmetric QuantParams expose the sign of a zero extreme.
-    int track_zero = (mode == MM_ASYMMETRIC) ? 1 : 0;
-    if (track_zero)
-        hipLaunchKernelGGL(k_minmax_partials<true>, dim3((unsigned)blocks), dim3(kBlock), 0,
-                           c->stream, x, n, vec, c->partials);
-    else
-        hipLaunchKernelGGL(k_minmax_partials<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
-                           c->stream, x, n, vec, c->partials);
-    TKV_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_minmax_finalize, dim3(1), dim3(kBlock), 0, c->stream, x, (int)blocks,
+    const int track_zero = (mode == MM_ASYMMETRIC) ? 1 : 0;
+    int64_t nparts;
+    TKV_RC_TRY(launch_partials(c, x, n, track_zero, &nparts));
+    hipLaunchKernelGGL(k_minmax_finalize, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts,
                        track_zero, mode, recipe, c->partials, out);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
@@ -249,12 +274,27 @@ __device__ __forceinline__ void store1(void* q, int64_t i, int a) {
         reinterpret_cast<int8_t*>(q)[i] = (int8_t)a;
 }
 
-template <bool OUT_I32>
+// FUSED: the scale is computed here from the calibration partials (every
+// block reduces them itself, so no finalize kernel runs in between); block 0
+// also publishes the QuantParams to *p.  Otherwise *p is read.
+template <bool OUT_I32, bool FUSED>
 __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restrict__ x,
                                                             int64_t n, int vec,
-                                                            const tkv_hip_qparams_dev* __restrict__ p,
-                                                            void* __restrict__ q) {
-    const double inv = p->inv;
+                                                            tkv_hip_qparams_dev* __restrict__ p,
+                                                            void* __restrict__ q, int nparts,
+                                                            int recipe,
+                                                            const RedPartial* __restrict__ partials) {
+    double inv;
+    if constexpr (FUSED) {
+        double dmn, dmx;
+        reduce_partials(x, nparts, 0, partials, dmn, dmx);
+        tkv_hip_qparams_dev prm;
+        finalize_minmax(dmn, dmx, MM_SYMMETRIC, recipe, &prm);
+        inv = prm.inv;
+        if (blockIdx.x == 0 && threadIdx.x == 0) *p = prm;
+    } else {
+        inv = p->inv;
+    }
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     int64_t n4 = vec ? n / 4 : 0;
@@ -294,12 +334,33 @@ int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qpar
     if (n <= 0) return TKV_HIP_OK;
     int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
     int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
+    auto* pp = const_cast<tkv_hip_qparams_dev*>(p);  // read only when not fused
     if (out_i32)
-        hipLaunchKernelGGL(k_quant_i8_tensor<true>, dim3((unsigned)blocks), dim3(kBlock), 0,
-                           c->stream, x, n, vec, p, q);
+        hipLaunchKernelGGL((k_quant_i8_tensor<true, false>), dim3((unsigned)blocks), dim3(kBlock),
+                           0, c->stream, x, n, vec, pp, q, 0, 0, c->partials);
     else
-        hipLaunchKernelGGL(k_quant_i8_tensor<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
-                           c->stream, x, n, vec, p, q);
+        hipLaunchKernelGGL((k_quant_i8_tensor<false, false>), dim3((unsigned)blocks), dim3(kBlock),
+                           0, c->stream, x, n, vec, pp, q, 0, 0, c->partials);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// calibrate_minmax(x, 1) then quantize_int8_symmetric(x, q, scale) in two
+// kernels: per-CU partials, then the quantize kernel finalizing the scale in
+// every block.  *p receives the QuantParams.
+int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
+                            tkv_hip_qparams_dev* p, void* q, bool out_i32) {
+    if (n <= 0) return launch_minmax_tensor(c, x, n, MM_SYMMETRIC, recipe, p);
+    int64_t nparts;
+    TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
+    int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
+    int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
+    if (out_i32)
+        hipLaunchKernelGGL((k_quant_i8_tensor<true, true>), dim3((unsigned)blocks), dim3(kBlock),
+                           0, c->stream, x, n, vec, p, q, (int)nparts, recipe, c->partials);
+    else
+        hipLaunchKernelGGL((k_quant_i8_tensor<false, true>), dim3((unsigned)blocks), dim3(kBlock),
+                           0, c->stream, x, n, vec, p, q, (int)nparts, recipe, c->partials);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -87,6 +87,9 @@ enum MinMaxMode { MM_SYMMETRIC = 0, MM_ASYMMETRIC = 1, MM_DYNAMIC_QL = 2, MM_FP8
 constexpr float kFp8Target = 240.0f;
 int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* p,
                            void* q, bool out_i32);
+// calibrate_minmax(x, 1) + quantize_int8_symmetric in two kernels; *p = QuantParams.
+int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
+                            tkv_hip_qparams_dev* p, void* q, bool out_i32);
 int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mode,
                       const float* scales_in, void* q, bool out_i32, float* scales_out,
                       tkv_hip_qparams_dev* row_params, int symmetric);
