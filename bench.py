@@ -34,6 +34,8 @@ M = 8192
 LAYERS = 12
 SHAPES = [("qkv", 2304, 768), ("attn_out", 768, 768), ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)]
 PEAK_INT8_TOPS = 5000.0      # MI355X dense INT8 MFMA
+PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
+PEAK_F16_TFLOPS = 2500.0     # MI355X dense FP16 MFMA
 PEAK_HBM_GBPS = 8000.0       # MI355X HBM3E
 
 
@@ -118,17 +120,120 @@ def run_gpu(steps, warmup):
                            "ceiling_tops": round(ceil, 1),
                            "frac_of_ceiling": round(ops / (tm * 1e-3) / 1e12 / ceil, 3)}
 
+    # The same 48 GEMMs replayed back to back on the last step's codes: the
+    # per-launch events above also hold the dispatch gap after each quantize
+    # kernel; this is the kernel time with only the GEMM-to-GEMM gap.
+    e0, e1 = D.Event(), D.Event()
+    e0.record(ctx)
+    for _ in range(2):
+        for lin in layers:
+            for j, (name, n, k, q, dx, dy, qa, db) in enumerate(lin):
+                D.matmul_int8(ctx, qa, q.codes, M, n, k, params[j].ptr, 0, 0.0, q.scales, q.bias,
+                              dy)
+    e1.record(ctx)
+    ctx.synchronize()
+    b2b_us = e0.elapsed_ms(e1) * 1e3 / (2 * n_gemm)
+
     # ---- config 2: quantize / calibrate bandwidth at M = 65536 x 768 ----
     quant = bench_quant(ctx, D, O)
+    fp8 = bench_fp8(ctx, D, O)
+    decode = bench_decode(ctx, D, O)
     ctx.close()
     return {
         "ms_per_step": ms_per_step,
         "value": ops_step / (ms_per_step * 1e-3) / 1e12,
         "gemm": {"avg_launch_us": avg_gemm_ms * 1e3, "achieved_tops": achieved_tops,
-                 "launches_timed": len(gemm_ms), "per_shape": per_shape},
+                 "launches_timed": len(gemm_ms), "per_shape": per_shape,
+                 "back_to_back_us": b2b_us},
         "quant": quant,
+        "fp8": fp8,
+        "decode": decode,
         "ops_per_step": ops_step,
     }
+
+
+def _time_us(ctx, D, fn, reps):
+    for i in range(2):
+        fn(i)
+    e0, e1 = D.Event(), D.Event()
+    ctx.synchronize()
+    e0.record(ctx)
+    for i in range(reps):
+        fn(i)
+    e1.record(ctx)
+    ctx.synchronize()
+    return e0.elapsed_ms(e1) * 1e3 / reps
+
+
+def bench_fp8(ctx, D, O, ms=(2048, 8192, 32768), reps=10):
+    """FP8-e4m3 W8A8 GEMM on the four GPT-2 shapes.  Activations are
+    per-tensor scaled into e4m3 and weights per-channel (both outside the
+    timed launches); the timed launch is the GEMM with the per-token /
+    per-channel dequant + bias epilogue, for the full-rate FP8 MFMA path and
+    for the reference-products path.  Two input sets are cycled."""
+    out = {}
+    for (name, n, k) in SHAPES:
+        w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 21, 0.02))
+        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 22, 0.01))
+        lin = D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_FP8_FAST)
+        w.close()
+        for m in ms:
+            xh = O.gi_noise(m * k, 23, 1.0)
+            sets = []
+            for _ in range(2):
+                dx = D.DeviceBuffer.from_host(ctx, xh)
+                q = D.DeviceBuffer.empty(ctx, (m, k), np.uint8)
+                p = D.params_buffer(ctx)
+                D.quantize_fp8_e4m3_dynamic_tensor(ctx, dx, m * k, q, p)
+                sets.append((dx, q, p, D.DeviceBuffer.empty(ctx, (m, n), np.float32)))
+            flops = 2.0 * m * n * k
+            row = {}
+            for fast, key, peak in ((True, "fast", PEAK_FP8_TFLOPS), (False, "reference_products",
+                                                                         PEAK_F16_TFLOPS)):
+                us = _time_us(ctx, D, lambda i: D.matmul_fp8_e4m3(
+                    ctx, sets[i % 2][1], lin.codes, m, n, k, sets[i % 2][2].ptr, 0, lin.scales,
+                    lin.bias, sets[i % 2][3], fast=fast), reps)
+                tf = flops / (us * 1e-6) / 1e12
+                row[key] = {"us": round(us, 2), "tflops": round(tf, 1),
+                            "frac_of_peak": round(tf / peak, 3)}
+            out[f"{name}_m{m}"] = row
+            for t in sets:
+                for buf in t:
+                    buf.close()
+        lin.close()
+    out["note"] = ("fast: v_mfma_scale_f32_32x32x64_f8f6f4, peak 5000 TFLOP/s; reference_products: "
+                   "reference-decoded operands on v_mfma_f32_32x32x16_f16, peak 2500 TFLOP/s")
+    return out
+
+
+def bench_decode(ctx, D, O, ms=(1, 4, 16, 32), reps=50):
+    """decode batches, INT8 weights pre-quantized per channel,
+    activations quantized per token inside the timed call
+    (tkv_hip_linear_forward, ACT_PER_TOKEN: rowwise quantize + skinny GEMM).
+    12 layers' distinct weights are cycled per shape, as a model would."""
+    shapes = [("qkv", 2304, 768), ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)]
+    out = {}
+    for (name, n, k) in shapes:
+        lins = []
+        for l in range(LAYERS):
+            w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 300 + l, 0.02))
+            b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 400 + l, 0.01))
+            lins.append((D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_INT8), b))
+            w.close()
+        for m in ms:
+            dx = D.DeviceBuffer.from_host(ctx, O.gi_noise(m * k, 24, 1.0))
+            dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+            us = _time_us(ctx, D, lambda i: lins[i % LAYERS][0].forward(dx, m, dy, D.ACT_PER_TOKEN),
+                          reps)
+            out[f"{name}_m{m}"] = {"us": round(us, 2),
+                                   "weight_GBps": round(n * k / (us * 1e-6) / 1e9, 1)}
+            dx.close()
+            dy.close()
+        for lin, b in lins:
+            lin.close()
+            b.close()
+    out["note"] = "per call: per-token int8 quantize + skinny INT8 GEMM + dequant/bias; weight bytes / call time"
+    return out
 
 
 def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
@@ -300,8 +405,11 @@ def main():
                          float(np.mean([gemm_bytes(M, n, k) for (_, n, k) in SHAPES]))),
                      "kernel": "k_gemm_i8 (INT8 MFMA GEMM + fused dequant epilogue)",
                      "avg_launch_us": round(gemm["avg_launch_us"], 2),
+                     "back_to_back_us": round(gemm["back_to_back_us"], 2),
                      "per_shape": gemm["per_shape"]},
         "quantize": r["quant"],
+        "fp8": r["fp8"],
+        "decode": r["decode"],
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_rows)

@@ -228,6 +228,12 @@ int32_t tkv_hip_dev_quantize_fp8_e4m3(int64_t ctx, const float* x, int64_t n, ui
  * encode(fl32(x * fl32(1 / scale))), scale read from params. */
 int32_t tkv_hip_dev_quantize_fp8_e4m3_scaled(int64_t ctx, const float* x, int64_t n,
                                              const tkv_hip_qparams_dev* params, uint8_t* q);
+/* Extension: per-tensor FP8 activation quantize (not in the reference):
+ * params.scale = fl32(max|x| / 240) (floor 1e-8), then the scaled encode
+ * above.  240 is the largest value the reference encoder reaches before its
+ * >= 248 saturation step. */
+int32_t tkv_hip_dev_quantize_fp8_e4m3_dynamic_tensor(int64_t ctx, const float* x, int64_t n,
+                                                     uint8_t* q, tkv_hip_qparams_dev* params);
 /* dequantize_fp8_e4m3 (reference decoder).  matmul.tkv:68-73 */
 int32_t tkv_hip_dev_dequantize_fp8_e4m3(int64_t ctx, const uint8_t* q, int64_t n, float* y);
 

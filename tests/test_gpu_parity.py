@@ -191,6 +191,26 @@ def test_fp8_encode_bit_patterns(ctx):
     assert np.array_equal(qb.download(), O.fp8_encode_bits(bits))
 
 
+@pytest.mark.parametrize("n", [1, 1000, 8192 * 768])
+def test_fp8_dynamic_tensor(ctx, n):
+    """Per-tensor FP8 activation quantize (extension used by the FP8 linear):
+    scale = fl32(max|x| / 240), codes = encode(fl32(x * fl32(1 / scale)))."""
+    say(f"fp8 dynamic tensor n={n}")
+    x = _x(n, 31, 1.0)
+    if n > 100:
+        x = O.add_outliers(x, 0.001, 3, 4, 20.0)
+    dx = D.DeviceBuffer.from_host(ctx, x)
+    dq = D.DeviceBuffer.empty(ctx, n, np.uint8)
+    p = D.params_buffer(ctx)
+    D.quantize_fp8_e4m3_dynamic_tensor(ctx, dx, n, dq, p)
+    am = max(float(np.max(np.abs(x.astype(np.float64)))), 1e-8)
+    scale = np.float32(am / 240.0)
+    assert _same_f32([D.read_params(p).scale], [scale])
+    inv = np.float32(1.0) / scale
+    want = O.fp8_encode_bits((x * inv).astype(np.float32).view(np.uint32))
+    assert np.array_equal(dq.download(), want)
+
+
 def test_fp8_decode_all_codes(hip):
     say("fp8 decode")
     codes = np.arange(-128, 128, dtype=np.int32)
@@ -406,7 +426,7 @@ def test_fp8_gemm_fast(ctx, m, n, k):
 # Every GEMM tile configuration (TKV_GEMM_CFG forces one per launch)
 # ---------------------------------------------------------------------------
 
-GEMM_CFGS = list(range(10))
+GEMM_CFGS = list(range(11))
 CFG_SHAPES = [(1, 1, 128), (37, 100, 200), (300, 500, 384), (1100, 2304, 768), (513, 768, 3072)]
 
 
@@ -484,9 +504,14 @@ def test_linear_forward_per_tensor(ctx):
     lin.close()
 
 
+DECODE_SHAPES = [(m, n, k) for m in (1, 4, 16, 32)
+                 for (n, k) in ((2304, 768), (3072, 768), (768, 3072))]
+
+
 def test_linear_forward_per_token(ctx):
+    """Config 5 decode shapes (skinny kernel, M <= 32) plus M = 33 (tiled)."""
     say("linear per-token (decode shapes)")
-    for m, n, k in [(1, 2304, 768), (4, 3072, 768), (32, 768, 3072)]:
+    for m, n, k in DECODE_SHAPES + [(33, 768, 768)]:
         x = _x(m * k, 11, 1.0)
         w = _x(n * k, 12, 0.02)
         b = _x(n, 13, 0.01)

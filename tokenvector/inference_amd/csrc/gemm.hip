@@ -443,6 +443,72 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restric
     }
 }
 
+// Skinny INT8 GEMM for decode batches (M <= 32): the weight is streamed
+// from HBM once and every activation row is reused from L2.  Workgroup b owns
+// output columns [32 b, 32 b + 32); its KW waves split the K steps (wave w
+// takes steps w, w + KW, ...), each wave loads all of its A and W fragments
+// before its MFMAs (v_mfma_i32_32x32x32_i8, A rows past M repeat row M - 1
+// and are never stored), the partial INT32 tiles are summed exactly with LDS
+// atomics, and wave 0 runs the same epilogue as the tiled kernels on the
+// 32 x 32 tile.
+struct CfgGemv {
+    static constexpr int BM = 32, BN = 32, WM = 1, WN = 1, WTM = 32, WTN = 32, TM = 1, TN = 1;
+};
+constexpr int kGemvMaxM = 32;
+constexpr int kGemvUnroll = 8;
+
+template <int KW, class E>
+__global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__ A,
+                                                     const uint8_t* __restrict__ W, int M, int N,
+                                                     int ldk, E ep, void* __restrict__ Y) {
+    __shared__ int32_t red[16 * 64];
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int n0 = blockIdx.x * 32;
+    const int r = lane & 31, kh = lane >> 5;
+    for (int i = threadIdx.x; i < 16 * 64; i += KW * 64) red[i] = 0;
+    const auto eo = ep.template load<CfgGemv>(0, n0, M, N);
+    const uint8_t* arow = A + (int64_t)(r < M ? r : M - 1) * ldk + kh * 16;
+    const uint8_t* wrow = W + (int64_t)(n0 + r < N ? n0 + r : N - 1) * ldk + kh * 16;
+    const int nks = ldk / 32;
+    v16i acc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0;
+    int ks = wave;
+    for (; ks + (kGemvUnroll - 1) * KW < nks; ks += kGemvUnroll * KW) {
+        v4i af[kGemvUnroll], wf[kGemvUnroll];
+#pragma unroll
+        for (int u = 0; u < kGemvUnroll; u++) {
+            af[u] = *reinterpret_cast<const v4i*>(arow + (ks + u * KW) * 32);
+            wf[u] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(wrow + (ks + u * KW) * 32));
+        }
+#pragma unroll
+        for (int u = 0; u < kGemvUnroll; u++)
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[u], wf[u], acc, 0, 0, 0);
+    }
+    for (; ks < nks; ks += KW) {
+        const v4i af = *reinterpret_cast<const v4i*>(arow + ks * 32);
+        const v4i wf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + ks * 32));
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, acc, 0, 0, 0);
+    }
+    __syncthreads();  // red[] zeroed
+    if (KW == 1) {
+        typename PolicyI8::Acc one[1][1];
+        one[0][0] = acc;
+        ep.template store<CfgGemv, PolicyI8>(one, eo, 0, n0, M, N, Y);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) atomicAdd(&red[i * 64 + lane], acc[i]);
+    __syncthreads();
+    if (wave == 0) {
+        typename PolicyI8::Acc sum[1][1];
+#pragma unroll
+        for (int i = 0; i < 16; i++) sum[0][0][i] = red[i * 64 + lane];
+        ep.template store<CfgGemv, PolicyI8>(sum, eo, 0, n0, M, N, Y);
+    }
+}
+
 // ---- tile configurations ---------------------------------------------------
 // K slices are 128 bytes: one full L2 line per row per DMA (64-byte slices
 // fetch every line twice and halve the DMA throughput).
@@ -468,11 +534,12 @@ static int64_t tiles_of(int64_t m, int64_t n) {
 
 // Tile choice: the largest tile that still gives every CU work.  The
 // environment variable TKV_GEMM_CFG (0..9; 2.. are the warp-specialised
-// configurations) forces one (tuning sweeps).
+// configurations; 10 the skinny kernel, INT8 with M <= 32) forces one
+// (tuning sweeps).  INT8 products with M <= 32 take the skinny kernel.
 static int pick_cfg(Ctx* c, int64_t m, int64_t n) {
     if (const char* v = getenv("TKV_GEMM_CFG")) {
         int f = atoi(v);
-        if (f >= 0 && f <= 9) return f;
+        if (f >= 0 && f <= 10) return f;
     }
     // Warp-specialised 128x192 tiles with deferred stores measured best on all
     // four GPT-2 shapes at M = 8192; 64x128 tiles keep every CU busy when M
@@ -508,10 +575,40 @@ static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int6
     return TKV_HIP_OK;
 }
 
+// Waves per workgroup of the skinny kernel: enough workgroups x waves for
+// the weight stream to fill the machine, but never more waves than K steps.
+template <class E>
+static int launch_gemv(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
+                       int64_t ldk, const E& ep, void* y) {
+    const int64_t wgs = ceil_div(n, (int64_t)32);
+    const int64_t nks = ldk / 32;
+    int64_t kw = ceil_div((int64_t)c->num_cus * 8, wgs);
+    if (kw > nks) kw = nks;
+    if (kw >= 16)
+        hipLaunchKernelGGL((k_gemv_i8<16, E>), dim3((unsigned)wgs), dim3(16 * 64), 0, c->stream,
+                           a, w, (int)m, (int)n, (int)ldk, ep, y);
+    else if (kw >= 8)
+        hipLaunchKernelGGL((k_gemv_i8<8, E>), dim3((unsigned)wgs), dim3(8 * 64), 0, c->stream, a,
+                           w, (int)m, (int)n, (int)ldk, ep, y);
+    else if (kw >= 4)
+        hipLaunchKernelGGL((k_gemv_i8<4, E>), dim3((unsigned)wgs), dim3(4 * 64), 0, c->stream, a,
+                           w, (int)m, (int)n, (int)ldk, ep, y);
+    else
+        hipLaunchKernelGGL((k_gemv_i8<1, E>), dim3((unsigned)wgs), dim3(64), 0, c->stream, a, w,
+                           (int)m, (int)n, (int)ldk, ep, y);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
 template <class P, class E>
 static int launch_any(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                       int64_t ldk, const E& ep, void* y) {
-    switch (pick_cfg(c, m, n)) {
+    const int cfg = pick_cfg(c, m, n);
+    if constexpr (std::is_same_v<P, PolicyI8>) {
+        if (m <= kGemvMaxM && (cfg == 10 || !getenv("TKV_GEMM_CFG")))
+            return launch_gemv(c, a, w, m, n, ldk, ep, y);
+    }
+    switch (cfg) {
         case 0: return launch_cfg<Cfg0, P>(c, a, w, m, n, ldk, ep, y);
         case 1: return launch_cfg<Cfg1, P>(c, a, w, m, n, ldk, ep, y);
         case 2: return launch_ws<Cfg2, P>(c, a, w, m, n, ldk, ep, y);
@@ -521,7 +618,8 @@ static int launch_any(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
         case 6: return launch_ws<Cfg6, P>(c, a, w, m, n, ldk, ep, y);
         case 7: return launch_ws<Cfg7, P>(c, a, w, m, n, ldk, ep, y);
         case 8: return launch_ws<Cfg8, P>(c, a, w, m, n, ldk, ep, y);
-        default: return launch_ws<Cfg9, P>(c, a, w, m, n, ldk, ep, y);
+        case 9: return launch_ws<Cfg9, P>(c, a, w, m, n, ldk, ep, y);
+        default: return launch_cfg<Cfg0, P>(c, a, w, m, n, ldk, ep, y);
     }
 }
 

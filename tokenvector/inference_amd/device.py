@@ -190,6 +190,12 @@ def quantize_fp8_e4m3_scaled(ctx, x, n, params, q) -> None:
                                                                _vp(params), _vp(q)))
 
 
+def quantize_fp8_e4m3_dynamic_tensor(ctx, x, n, q, params) -> None:
+    """Per-tensor FP8 activation quantize (extension): scale = max|x| / 240."""
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_fp8_e4m3_dynamic_tensor(ctx.handle, _vp(x), int(n),
+                                                                       _vp(q), _vp(params)))
+
+
 def dequantize_fp8_e4m3(ctx, q, n, y) -> None:
     _lib.check(_lib.lib().tkv_hip_dev_dequantize_fp8_e4m3(ctx.handle, _vp(q), int(n), _vp(y)))
 
