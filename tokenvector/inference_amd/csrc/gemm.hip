@@ -42,13 +42,13 @@ __device__ __forceinline__ T pin(T v) {
 }
 
 // Writes part of the calling wave's TM x TN blocks of 32 x 32 outputs of the
-// tile at (m0, n0): parts P0 .. P0 + NP - 1, part p being accumulator
-// registers 4 * (p % 4) .. 4 * (p % 4) + 3 of row block p / 4 (four output
-// rows per lane) across all TN column blocks; C::TM * 4 parts make the tile.
-// value(i, j, r) is the output held in accumulator register r of block
-// (i, j).  Row bases are wave-uniform (scalar registers); the lane part is one
-// 32-bit element offset (launchers keep N < 2^28).  Tiles fully inside
-// [M, N] (all but the edges) store without any checks.
+// tile at (m0, n0): parts P0 .. P0 + NP - 1, part p being accumulator register
+// p % 16 of row block p / 16 (one output row per lane) across all TN column
+// blocks; C::TM * 16 parts make the tile.  value(i, j, r) is the output held
+// in accumulator register r of block (i, j).  Row bases are wave-uniform
+// (scalar registers); the lane part is one 32-bit element offset (launchers
+// keep N < 2^28).  Tiles fully inside [M, N] (all but the edges) store
+// without any checks.
 template <class C, int P0, int NP, class T, class F>
 __device__ __forceinline__ void write_tile(T* __restrict__ Y, int m0, int n0, int M, int N,
                                            F&& value) {
@@ -59,18 +59,15 @@ __device__ __forceinline__ void write_tile(T* __restrict__ Y, int m0, int n0, in
     auto body = [&](auto check) {
 #pragma unroll
         for (int p = P0; p < P0 + NP; p++) {
-            const int i = p / 4;
+            const int i = p / 16, r = p % 16;
+            const int rrow = i * 32 + (r >> 2) * 8 + (r & 3);
+            T* rowp = Y + (int64_t)(rbase + rrow) * N + cbase;
 #pragma unroll
-            for (int r = (p % 4) * 4; r < (p % 4) * 4 + 4; r++) {
-                const int rrow = i * 32 + (r >> 2) * 8 + (r & 3);
-                T* rowp = Y + (int64_t)(rbase + rrow) * N + cbase;
-#pragma unroll
-                for (int j = 0; j < C::TN; j++) {
-                    const T v = value(i, j, r);
-                    if (!decltype(check)::value ||
-                        (rbase + rrow + khalf * 4 < M && cbase + j * 32 + lc < N))
-                        put(rowp + loff + j * 32, v);
-                }
+            for (int j = 0; j < C::TN; j++) {
+                const T v = value(i, j, r);
+                if (!decltype(check)::value ||
+                    (rbase + rrow + khalf * 4 < M && cbase + j * 32 + lc < N))
+                    put(rowp + loff + j * 32, v);
             }
         }
     };
@@ -158,7 +155,7 @@ struct EpiI8 {
         return o;
     }
 
-    template <class C, class P, int P0 = 0, int NP = C::TM * 4>
+    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
     __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
                                           const Operands<C>& o, int m0, int n0, int M, int N,
                                           void* __restrict__ Y) const {
@@ -226,7 +223,7 @@ struct EpiF8 {
         return o;
     }
 
-    template <class C, class P, int P0 = 0, int NP = C::TM * 4>
+    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
     __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
                                           const Operands<C>& o, int m0, int n0, int M, int N,
                                           void* __restrict__ Y) const {
@@ -285,16 +282,27 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm(const uint8_t* __restrict__
     }
 }
 
-// ep.store of part `part` (wave-uniform, run time) of a tile: a chain of
-// scalar compares selecting the compile-time part.
-template <class C, class P, class E, int... I>
+// ep.store of part `part` (wave-uniform, run time, < C::TM * 16 <= 64) of a
+// tile: one scalar jump to the compile-time part.
+template <class C, class P, class E>
 __device__ __forceinline__ void store_part_dyn(const E& ep, int part,
                                                const typename P::Acc (&acc)[C::TM][C::TN],
                                                const typename E::template Operands<C>& o,
-                                               int m0, int n0, int M,
-                                               int N, void* __restrict__ Y,
-                                               std::integer_sequence<int, I...>) {
-    ((part == I ? ep.template store<C, P, I, 1>(acc, o, m0, n0, M, N, Y) : void()), ...);
+                                               int m0, int n0, int M, int N, void* __restrict__ Y) {
+    static_assert(C::TM * 16 <= 64, "parts");
+    switch (part) {
+#define TKV_PART(i)                                                              \
+    case i:                                                                      \
+        if constexpr (i < C::TM * 16) ep.template store<C, P, i, 1>(acc, o, m0, n0, M, N, Y); \
+        break;
+#define TKV_PART8(i) TKV_PART(i) TKV_PART(i + 1) TKV_PART(i + 2) TKV_PART(i + 3) \
+    TKV_PART(i + 4) TKV_PART(i + 5) TKV_PART(i + 6) TKV_PART(i + 7)
+        TKV_PART8(0) TKV_PART8(8) TKV_PART8(16) TKV_PART8(24)
+        TKV_PART8(32) TKV_PART8(40) TKV_PART8(48) TKV_PART8(56)
+#undef TKV_PART8
+#undef TKV_PART
+        default: break;
+    }
 }
 
 // Warp-specialised persistent GEMM (CfgWS).  Workgroup b owns tiles b, b + G,
@@ -402,14 +410,17 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restric
     } else {
         // The previous tile's accumulators (pacc) are stored one part per K
         // slice of the current tile, after that slice's MFMAs are issued.
-        constexpr int NPART = C::TM * 4;
+        // DEFER == 1: four-register parts in the first slices; DEFER == 2:
+        // single-register parts spread evenly over all of the tile's slices.
+        constexpr int NPART = C::TM * 16;
+        constexpr int GRAIN = C::DEFER == 1 ? 4 : 1;
         typename P::Acc pacc[C::TM][C::TN];
         typename E::template Operands<C> peo;
         int pm0 = 0, pn0 = 0;
         bool have = false;
-        auto store_part = [&](int part) {
-            store_part_dyn<C, P>(ep, part, pacc, peo, pm0, pn0, M, N, Y,
-                                 std::make_integer_sequence<int, NPART>{});
+        auto store_parts = [&](int lo, int hi) {
+            for (int part = lo; part < hi; part++)
+                store_part_dyn<C, P>(ep, part, pacc, peo, pm0, pn0, M, N, Y);
         };
         for (int ti = 0; ti < my_tiles; ti++) {
             const int t = xcd_tile(b + ti * G, tiles);
@@ -425,11 +436,15 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restric
             for (int kt = 0; kt < nk; kt++, s++) {
                 const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
                 P::template slice<C>(sa, sa + C::A_BYTES, a_row, w_row, khalf, acc);
-                if (have && kt < NPART) store_part(kt);
+                if (have) {
+                    if constexpr (GRAIN == 1)
+                        store_parts(kt * NPART / nk, (kt + 1) * NPART / nk);
+                    else if (kt < NPART / GRAIN)
+                        store_parts(kt * GRAIN, kt * GRAIN + GRAIN);
+                }
                 barrier();
             }
-            if (have)
-                for (int p = nk; p < NPART; p++) store_part(p);
+            if (have && GRAIN > 1 && nk < NPART / GRAIN) store_parts(nk * GRAIN, NPART);
 #pragma unroll
             for (int i = 0; i < C::TM; i++)
 #pragma unroll
@@ -521,9 +536,9 @@ typedef CfgWS<128, 192, 2, 2, 128, 3, 4> Cfg3;     // 120 KB, 4 consumers (64x96
 typedef CfgWS<128, 128, 2, 2, 128, 3, 4> Cfg4;     //  96 KB, 4 consumers (64x64) + 4 producers
 typedef CfgWS<64, 128, 2, 2, 128, 3, 4> Cfg5;      //  72 KB, 4 consumers (32x64) + 4 producers
 typedef CfgWS<128, 192, 4, 2, 128, 4, 4> Cfg6;     // 160 KB, 3 slices in flight
-typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 1> Cfg7;  // Cfg2 + stores deferred into next tile
+typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 2> Cfg7;  // Cfg2 + stores spread over the next tile
 typedef CfgWS<128, 128, 2, 2, 128, 3, 4, 1> Cfg8;  // Cfg4 + deferred stores
-typedef CfgWS<128, 192, 4, 2, 128, 4, 4, 1> Cfg9;  // Cfg6 + deferred stores
+typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 1> Cfg9;  // Cfg2 + stores in the next tile's first slices
 
 constexpr int kBK = 128;
 
@@ -541,10 +556,10 @@ static int pick_cfg(Ctx* c, int64_t m, int64_t n) {
         int f = atoi(v);
         if (f >= 0 && f <= 10) return f;
     }
-    // Warp-specialised 128x192 tiles with deferred stores measured best on all
-    // four GPT-2 shapes at M = 8192; 64x128 tiles keep every CU busy when M
-    // is small.
-    return tiles_of<Cfg7>(m, n) >= c->num_cus ? 7 : 0;
+    // Warp-specialised 128x192 tiles (cfg 2) measured best over the four
+    // GPT-2 shapes at M = 8192 (warmed-up, interleaved medians); 64x128 tiles
+    // keep every CU busy when M is small.
+    return tiles_of<Cfg2>(m, n) >= c->num_cus ? 2 : 0;
 }
 
 template <class C, class P, class E>

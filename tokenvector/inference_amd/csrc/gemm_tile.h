@@ -83,9 +83,11 @@ struct CfgWS {
     static constexpr int A_BYTES = BM * BK, W_BYTES = BN * BK;
     static constexpr int STAGE_BYTES = A_BYTES + W_BYTES;
     static constexpr int LDS_BYTES = STAGE_BYTES * STAGES;
-    // DEFER: a tile's output stores are spread over the next tile's K slices
+    // DEFER: a tile's output stores are issued during the next tile's K slices
     // (the consumer keeps the finished accumulators), so HBM writes proceed
-    // during the MFMA work instead of in bursts between tiles.  The extra
+    // during the MFMA work instead of in bursts between tiles: 1 = in the
+    // first slices, four registers per slice; 2 = one register at a time,
+    // spread evenly over all slices.  The extra
     // accumulator set is paid for by reading fragments only two k-steps ahead.
     // FD (fragment depth, k-steps read ahead; 0 = automatic) trades registers
     // for LDS latency hiding, e.g. to fit four waves per SIMD.
