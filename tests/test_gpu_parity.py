@@ -149,7 +149,8 @@ def test_quantize_per_channel_and_dequantize(hip, rows, cols):
         Q.quantize_int8_per_channel(w, q, rows, cols, sc[:-1] if rows > 1 else [])
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 768), (32, 3072), (5, 37), (3, 4)])
+@pytest.mark.parametrize("rows,cols", [(1, 768), (32, 3072), (5, 37), (3, 4), (9000, 3072),
+                                       (3000, 1536)])
 def test_dynamic_rowwise_shapes(hip, rows, cols):
     say(f"dynamic rowwise {rows}x{cols}")
     x = _x(rows * cols, 5, 1.0)
@@ -191,7 +192,40 @@ def test_fp8_encode_bit_patterns(ctx):
     assert np.array_equal(qb.download(), O.fp8_encode_bits(bits))
 
 
-@pytest.mark.parametrize("n", [1, 1000, 8192 * 768])
+# Per-tensor sizes: tiny and ragged (n % 4 tails), one float4 per thread of a
+# 256 x 512 grid and just past it, the GPT-2 activation sizes, and one past
+# the largest; every call runs calibrate + quantize back to back.
+GRID_CHUNK = 256 * 512 * 4
+DYN_SIZES = [1, 3, 4, 1000, 1023, GRID_CHUNK, GRID_CHUNK + 1, 5 * GRID_CHUNK + 7,
+             8192 * 768, 8192 * 3072, 8192 * 3072 + 4]
+
+
+@pytest.mark.parametrize("n", DYN_SIZES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_int8_dynamic_tensor(ctx, n, offset):
+    """calibrate_minmax(x, 1) + quantize_int8_symmetric on the device in one
+    call (engine.tkv:13-36, 216-226): QuantParams and codes bit-exact."""
+    if offset and n not in (1000, 8192 * 768):
+        pytest.skip("misaligned x: two sizes suffice")
+    say(f"int8 dynamic tensor n={n} offset={offset}")
+    x = _x(n, 17 + n % 1000, 1.0)
+    if n > 100:
+        x = O.add_outliers(x, 0.001, 3, 4, 20.0)
+    dx = D.DeviceBuffer.from_host(ctx, np.concatenate([np.zeros(offset, np.float32), x]))
+    dq = D.DeviceBuffer.empty(ctx, n, np.int8)
+    p = D.params_buffer(ctx)
+    for _ in range(2):  # twice: the second call reuses the context's partials
+        D.quantize_int8_dynamic_tensor(ctx, dx.ptr + 4 * offset, n, dq, p)
+        want_p = O.calibrate_minmax(x, 1)
+        got_p = D.read_params(p)
+        assert _same_f32([got_p.scale, got_p.min_val, got_p.max_val],
+                         [want_p.scale, want_p.min_val, want_p.max_val])
+        assert np.array_equal(dq.download().astype(np.int32),
+                              O.quantize_int8_symmetric(x, want_p.scale))
+
+
+@pytest.mark.parametrize("n", [1, 1000, 5 * GRID_CHUNK + 7, 8192 * 768, 32 * GRID_CHUNK,
+                               8192 * 3072])
 def test_fp8_dynamic_tensor(ctx, n):
     """Per-tensor FP8 activation quantize (extension used by the FP8 linear):
     scale = fl32(max|x| / 240), codes = encode(fl32(x * fl32(1 / scale)))."""

@@ -536,8 +536,7 @@ int32_t tkv_hip_dev_quantize_fp8_e4m3_dynamic_tensor(int64_t ctx, const float* x
     if (n <= 0 || !params) return set_error(TKV_HIP_BAD_ARG, "empty input or NULL params");
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
-    TKV_RC_TRY(launch_minmax_tensor(c, x, n, MM_FP8, TKV_HIP_RECIPE_PRIMARY, params));
-    return launch_fp8_encode(c, x, n, params, q, false);
+    return launch_quant_fp8_dynamic(c, x, n, params, q, false);
 }
 
 int32_t tkv_hip_dev_dequantize_fp8_e4m3(int64_t ctx, const uint8_t* q, int64_t n, float* y) {

@@ -219,8 +219,7 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
     }
     if (act_mode != TKV_HIP_ACT_PER_TENSOR)
         return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: FP8 weights take per-tensor activations");
-    TKV_RC_TRY(launch_minmax_tensor(c, x, m * k, MM_FP8, TKV_HIP_RECIPE_PRIMARY, ap));
-    TKV_RC_TRY(launch_fp8_encode(c, x, m * k, ap, qa, false));
+    TKV_RC_TRY(launch_quant_fp8_dynamic(c, x, m * k, ap, qa, false));
     return launch_gemm_f8(c, static_cast<uint8_t*>(qa), static_cast<uint8_t*>(wt->codes), m, wt->n,
                           k, &ap->scale, 0, wt->scales, wt->bias, y,
                           wt->format == TKV_HIP_WEIGHT_FP8_FAST);

@@ -5,10 +5,18 @@
 //
 // Layout: f32 inputs are read as 16-byte float4 loads, four per thread per
 // loop trip for memory-level parallelism; int8 / e4m3 outputs leave as one
-// 32-bit store per float4.  Reductions use wave64 shuffles, then LDS, then
-// one partial per block; the consumer of the partials (a one-block finalize,
-// or every block of the quantize kernel) reduces them after the kernel
-// boundary, which orders them across XCDs without device-scope fences.
+// 32-bit store per float4.  The streaming grids are two 256-thread blocks
+// per CU, the shape that measured highest on MI355X HBM (about 6.8 TB/s
+// read-only with nontemporal loads, 6.5 TB/s for the 16 B in / 4 B out
+// quantize stream, against 5.3 TB/s from 16 blocks per CU).  Loads are
+// nontemporal for tensors beyond kCacheableBytes, which no cache level
+// holds; smaller ones load through the caches, so the quantize pass that
+// follows calibration finds x in the 256 MB Infinity Cache.  Codes are
+// stored through the caches too: the GEMM reads them next.  Reductions use
+// wave64 shuffles, then
+// LDS, then one partial per block; the consumer of the partials (a one-block
+// finalize, or every block of the quantize kernel) reduces them after the
+// kernel boundary, which orders them across XCDs without device-scope fences.
 //
 // Numerics restate tv/quantization/engine.tkv and types.tkv exactly: f64
 // products and reciprocals where the reference computes in f64, round half to
@@ -21,8 +29,23 @@
 namespace tkv {
 
 constexpr int kBlock = 256;
-constexpr int kRedBlock = 1024;  // calibration partial blocks: one per CU
+constexpr int kRedBlock = 256;   // calibration partial blocks
+constexpr int kBlocksPerCu = 2;  // streaming grids: blocks per CU
 constexpr int kUnroll = 4;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int64_t kCacheableBytes = 128ll << 20;
+
+template <bool NT = true>
+__device__ __forceinline__ float4 ld4(const float4* p) {
+    if constexpr (NT) {
+        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+        return make_float4(v.x, v.y, v.z, v.w);
+    } else {
+        return *p;
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Calibration finalize (engine.tkv:13-36 and session.tkv:2853-2876).
@@ -99,7 +122,7 @@ __device__ __forceinline__ void mm_acc(float v, int64_t idx, bool track_zero, fl
 // one-block finalize kernel.  The kernel boundary orders the partial stores
 // before the finalize reads, across XCDs and their separate L2s, without
 // device-scope fences in the streaming kernel.
-template <bool TRACK_ZERO>
+template <bool TRACK_ZERO, bool NT>
 __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __restrict__ x,
                                                                int64_t n, int vec,
                                                                RedPartial* __restrict__ partials) {
@@ -113,7 +136,7 @@ __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __re
     for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
         float4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) v[u] = x4[i + u * stride];
+        for (int u = 0; u < kUnroll; u++) v[u] = ld4<NT>(x4 + i + u * stride);
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             int64_t b = (i + u * stride) * 4;
@@ -124,7 +147,7 @@ __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __re
         }
     }
     for (; i < n4; i += stride) {
-        float4 v = x4[i];
+        float4 v = ld4<NT>(x4 + i);
         mm_acc(v.x, i * 4 + 0, TRACK_ZERO, mn, mx, zi);
         mm_acc(v.y, i * 4 + 1, TRACK_ZERO, mn, mx, zi);
         mm_acc(v.z, i * 4 + 2, TRACK_ZERO, mn, mx, zi);
@@ -213,24 +236,31 @@ __global__ __launch_bounds__(kBlock) void k_minmax_finalize(const float* __restr
     if (threadIdx.x == 0) finalize_minmax(dmn, dmx, mode, recipe, out);
 }
 
-// One partial per CU (kRedBlock threads each, for enough loads in flight):
-// few enough that every block of a consumer kernel can reduce them itself.
-static int64_t partial_blocks(Ctx* c, int64_t work) {
+// kBlocksPerCu partials per CU: few enough that every block of a consumer
+// kernel can reduce them itself.
+static int64_t partial_blocks(Ctx* c, int64_t work, int vec) {
     int64_t blocks = ceil_div(work, (int64_t)kRedBlock * kUnroll);
-    const int64_t cap = c->num_cus < kMaxReduceBlocks ? c->num_cus : kMaxReduceBlocks;
+    const int64_t want = (int64_t)c->num_cus * (vec ? kBlocksPerCu : 8);
+    const int64_t cap = want < kMaxReduceBlocks ? want : kMaxReduceBlocks;
     if (blocks > cap) blocks = cap;
     return blocks < 1 ? 1 : blocks;
 }
 
 static int launch_partials(Ctx* c, const float* x, int64_t n, int track_zero, int64_t* nparts) {
     const int vec = aligned(x, 16) ? 1 : 0;
-    const int64_t blocks = partial_blocks(c, vec ? n / 4 : n);
-    if (track_zero)
-        hipLaunchKernelGGL(k_minmax_partials<true>, dim3((unsigned)blocks), dim3(kRedBlock), 0,
-                           c->stream, x, n, vec, c->partials);
-    else
-        hipLaunchKernelGGL(k_minmax_partials<false>, dim3((unsigned)blocks), dim3(kRedBlock), 0,
-                           c->stream, x, n, vec, c->partials);
+    const int64_t blocks = partial_blocks(c, vec ? n / 4 : n, vec);
+    const bool nt = n * 4 > kCacheableBytes;
+#define TKV_PARTIALS(TZ, NT)                                                                     \
+    hipLaunchKernelGGL((k_minmax_partials<TZ, NT>), dim3((unsigned)blocks), dim3(kRedBlock), 0, \
+                       c->stream, x, n, vec, c->partials)
+    if (track_zero) {
+        if (nt) TKV_PARTIALS(true, true);
+        else TKV_PARTIALS(true, false);
+    } else {
+        if (nt) TKV_PARTIALS(false, true);
+        else TKV_PARTIALS(false, false);
+    }
+#undef TKV_PARTIALS
     TKV_LAUNCH_CHECK();
     *nparts = blocks;
     return TKV_HIP_OK;
@@ -277,7 +307,7 @@ __device__ __forceinline__ void store1(void* q, int64_t i, int a) {
 // FUSED: the scale is computed here from the calibration partials (every
 // block reduces them itself, so no finalize kernel runs in between); block 0
 // also publishes the QuantParams to *p.  Otherwise *p is read.
-template <bool OUT_I32, bool FUSED>
+template <bool OUT_I32, bool FUSED, bool NT>
 __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restrict__ x,
                                                             int64_t n, int vec,
                                                             tkv_hip_qparams_dev* __restrict__ p,
@@ -303,7 +333,7 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restr
     for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
         float4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) v[u] = x4[i + u * stride];
+        for (int u = 0; u < kUnroll; u++) v[u] = ld4<NT>(x4 + i + u * stride);
 #pragma unroll
         for (int u = 0; u < kUnroll; u++)
             store4<OUT_I32>(q, i + u * stride, rne_clamp((double)v[u].x * inv, -127.0, 127.0),
@@ -312,7 +342,7 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restr
                             rne_clamp((double)v[u].w * inv, -127.0, 127.0));
     }
     for (; i < n4; i += stride) {
-        float4 v = x4[i];
+        float4 v = ld4<NT>(x4 + i);
         store4<OUT_I32>(q, i, rne_clamp((double)v.x * inv, -127.0, 127.0),
                         rne_clamp((double)v.y * inv, -127.0, 127.0),
                         rne_clamp((double)v.z * inv, -127.0, 127.0),
@@ -322,25 +352,48 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restr
         store1<OUT_I32>(q, j, rne_clamp((double)x[j] * inv, -127.0, 127.0));
 }
 
-static int64_t stream_blocks(Ctx* c, int64_t work) {
+// Grid of the float4 streaming kernels; `vec` 0 (misaligned input, one
+// element per trip) takes the scalar kernels' wider grid.
+static int64_t stream_blocks(Ctx* c, int64_t work, int vec) {
+    int64_t blocks = ceil_div(work, (int64_t)kBlock * kUnroll);
+    int64_t cap = (int64_t)c->num_cus * (vec ? kBlocksPerCu : 16);
+    if (blocks > cap) blocks = cap;
+    return blocks < 1 ? 1 : blocks;
+}
+
+// Grid for the one-element-per-trip kernels (dequantize, decode, layout
+// conversions): enough resident waves to cover the load latency.
+static int64_t scalar_blocks(Ctx* c, int64_t work) {
     int64_t blocks = ceil_div(work, (int64_t)kBlock * kUnroll);
     int64_t cap = (int64_t)c->num_cus * 16;
     if (blocks > cap) blocks = cap;
     return blocks < 1 ? 1 : blocks;
 }
 
+template <bool FUSED>
+static void launch_quant_kernel(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_dev* p,
+                                void* q, bool out_i32, int nparts, int recipe) {
+    const int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
+    const dim3 grid((unsigned)stream_blocks(c, vec ? n / 4 : n, vec)), block(kBlock);
+    const bool nt = n * 4 > kCacheableBytes;
+#define TKV_QUANT(OI, NT)                                                                        \
+    hipLaunchKernelGGL((k_quant_i8_tensor<OI, FUSED, NT>), grid, block, 0, c->stream, x, n, vec, \
+                       p, q, nparts, recipe, c->partials)
+    if (out_i32) {
+        if (nt) TKV_QUANT(true, true);
+        else TKV_QUANT(true, false);
+    } else {
+        if (nt) TKV_QUANT(false, true);
+        else TKV_QUANT(false, false);
+    }
+#undef TKV_QUANT
+}
+
 int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* p,
                            void* q, bool out_i32) {
     if (n <= 0) return TKV_HIP_OK;
-    int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
-    int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
     auto* pp = const_cast<tkv_hip_qparams_dev*>(p);  // read only when not fused
-    if (out_i32)
-        hipLaunchKernelGGL((k_quant_i8_tensor<true, false>), dim3((unsigned)blocks), dim3(kBlock),
-                           0, c->stream, x, n, vec, pp, q, 0, 0, c->partials);
-    else
-        hipLaunchKernelGGL((k_quant_i8_tensor<false, false>), dim3((unsigned)blocks), dim3(kBlock),
-                           0, c->stream, x, n, vec, pp, q, 0, 0, c->partials);
+    launch_quant_kernel<false>(c, x, n, pp, q, out_i32, 0, 0);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
@@ -353,14 +406,7 @@ int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
     if (n <= 0) return launch_minmax_tensor(c, x, n, MM_SYMMETRIC, recipe, p);
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
-    int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
-    int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
-    if (out_i32)
-        hipLaunchKernelGGL((k_quant_i8_tensor<true, true>), dim3((unsigned)blocks), dim3(kBlock),
-                           0, c->stream, x, n, vec, p, q, (int)nparts, recipe, c->partials);
-    else
-        hipLaunchKernelGGL((k_quant_i8_tensor<false, true>), dim3((unsigned)blocks), dim3(kBlock),
-                           0, c->stream, x, n, vec, p, q, (int)nparts, recipe, c->partials);
+    launch_quant_kernel<true>(c, x, n, p, q, out_i32, (int)nparts, recipe);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
@@ -449,6 +495,98 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float* __restrict__ x, in
     }
 }
 
+// quantize_dynamic_int8_rowwise (engine.tkv:266-285) with the row held in
+// registers: each wave64 walks rows r, r + waves, ... with C4 float4 per
+// lane (lane + 64 c), so every row is read from HBM once; with PIPE the next
+// row's loads are issued before the current row is reduced and quantized.
+// Same numerics as k_rows' RM_DYNAMIC branch.
+template <int C4>
+__device__ __forceinline__ void load_row(const float* __restrict__ x, int64_t r, int64_t cols,
+                                         int lane, float4 (&v)[C4]) {
+    const float4* __restrict__ xr = reinterpret_cast<const float4*>(x + r * cols);
+#pragma unroll
+    for (int c = 0; c < C4; c++)
+        if (lane + 64 * c < cols / 4) v[c] = ld4<true>(xr + lane + 64 * c);
+}
+
+template <int C4, bool OUT_I32>
+__device__ __forceinline__ void quant_row(const float4 (&v)[C4], int64_t r, int64_t cols, int lane,
+                                          void* __restrict__ q, float* __restrict__ scales_out) {
+    const int64_t cols4 = cols / 4;
+    float mn = FLT_MAX * 2.0f, mx = -FLT_MAX * 2.0f;
+#pragma unroll
+    for (int c = 0; c < C4; c++)
+        if (lane + 64 * c < cols4) {
+            mn = fminf(fminf(mn, v[c].x), fminf(v[c].y, fminf(v[c].z, v[c].w)));
+            mx = fmaxf(fmaxf(mx, v[c].x), fmaxf(v[c].y, fmaxf(v[c].z, v[c].w)));
+        }
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    double am = fabs((double)mx);
+    if (fabs((double)mn) > am) am = fabs((double)mn);
+    if (am < 0.00000001) am = 0.00000001;
+    const double sc = am / 127.0;
+    if (lane == 0) scales_out[r] = (float)sc;
+    const double inv = 1.0 / sc;
+    const int64_t base4 = r * cols4;
+#pragma unroll
+    for (int c = 0; c < C4; c++)
+        if (lane + 64 * c < cols4)
+            store4<OUT_I32>(q, base4 + lane + 64 * c, rne_clamp((double)v[c].x * inv, -127.0, 127.0),
+                            rne_clamp((double)v[c].y * inv, -127.0, 127.0),
+                            rne_clamp((double)v[c].z * inv, -127.0, 127.0),
+                            rne_clamp((double)v[c].w * inv, -127.0, 127.0));
+}
+
+template <int C4, bool OUT_I32, bool PIPE>
+__global__ __launch_bounds__(kBlock) void k_rows_dynamic(const float* __restrict__ x, int64_t rows,
+                                                         int64_t cols, void* __restrict__ q,
+                                                         float* __restrict__ scales_out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * (kBlock / 64);
+    int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    float4 cur[C4];
+    load_row<C4>(x, r, cols, lane, cur);
+    for (; r < rows; r += nw) {
+        if constexpr (PIPE) {
+            float4 nxt[C4];
+            if (r + nw < rows) load_row<C4>(x, r + nw, cols, lane, nxt);
+            quant_row<C4, OUT_I32>(cur, r, cols, lane, q, scales_out);
+#pragma unroll
+            for (int c = 0; c < C4; c++) cur[c] = nxt[c];
+        } else {
+            if (r != (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6))
+                load_row<C4>(x, r, cols, lane, cur);
+            quant_row<C4, OUT_I32>(cur, r, cols, lane, q, scales_out);
+        }
+    }
+}
+
+template <bool OUT_I32>
+static bool launch_rows_dynamic(Ctx* c, const float* x, int64_t rows, int64_t cols, void* q,
+                                float* scales_out) {
+    const int64_t per_lane = ceil_div(cols / 4, 64);
+    int64_t blocks = ceil_div(rows, kBlock / 64);
+    const int64_t cap = (int64_t)c->num_cus * 8;
+    if (blocks > cap) blocks = cap;
+    const dim3 grid((unsigned)blocks), block(kBlock);
+#define TKV_ROWS_DYN(C4, PIPE)                                                               \
+    hipLaunchKernelGGL((k_rows_dynamic<C4, OUT_I32, PIPE>), grid, block, 0, c->stream, x, rows, \
+                       cols, q, scales_out)
+    if (per_lane <= 1) TKV_ROWS_DYN(1, true);
+    else if (per_lane <= 2) TKV_ROWS_DYN(2, true);
+    else if (per_lane <= 3) TKV_ROWS_DYN(3, true);
+    else if (per_lane <= 4) TKV_ROWS_DYN(4, true);
+    else if (per_lane <= 6) TKV_ROWS_DYN(6, true);
+    else if (per_lane <= 8) TKV_ROWS_DYN(8, false);
+    else if (per_lane <= 12) TKV_ROWS_DYN(12, false);
+    else if (per_lane <= 16) TKV_ROWS_DYN(16, false);
+    else return false;
+#undef TKV_ROWS_DYN
+    return true;
+}
+
 int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mode,
                       const float* scales_in, void* q, bool out_i32, float* scales_out,
                       tkv_hip_qparams_dev* row_params, int symmetric) {
@@ -456,6 +594,14 @@ int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mo
     bool q_ok = (mode == RM_CALIBRATE || mode == RM_CALIBRATE_FULL) ? true
                                                                      : aligned(q, out_i32 ? 16 : 4);
     int vec = (cols % 4 == 0 && aligned(x, 16) && q_ok) ? 1 : 0;
+    if (mode == RM_DYNAMIC && vec) {
+        const bool done = out_i32 ? launch_rows_dynamic<true>(c, x, rows, cols, q, scales_out)
+                                  : launch_rows_dynamic<false>(c, x, rows, cols, q, scales_out);
+        if (done) {
+            TKV_LAUNCH_CHECK();
+            return TKV_HIP_OK;
+        }
+    }
     int64_t blocks = ceil_div(rows, kBlock / 64);
     if (out_i32)
         hipLaunchKernelGGL(k_rows<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, x,
@@ -489,7 +635,7 @@ int launch_dequant_i8(Ctx* c, const void* q, bool in_i32, int64_t rows, int64_t 
                       float scale, const float* scales, float* y) {
     int64_t n = rows * cols;
     if (n <= 0) return TKV_HIP_OK;
-    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    int64_t blocks = scalar_blocks(c, n / 4 + 1);
     if (in_i32)
         hipLaunchKernelGGL(k_dequant_i8<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
                            q, rows, cols, scale, scales, y);
@@ -530,7 +676,7 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
     for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
         float4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) v[u] = x4[i + u * stride];
+        for (int u = 0; u < kUnroll; u++) v[u] = ld4(x4 + i + u * stride);
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             if (scaled) {
@@ -544,7 +690,7 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
         }
     }
     for (; i < n4; i += stride) {
-        float4 v = x4[i];
+        float4 v = ld4(x4 + i);
         if (scaled) {
             v.x *= mul;
             v.y *= mul;
@@ -569,7 +715,7 @@ int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_d
                       void* q, bool out_i32) {
     if (n <= 0) return TKV_HIP_OK;
     int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
-    int64_t blocks = stream_blocks(c, vec ? n / 4 : n);
+    int64_t blocks = stream_blocks(c, vec ? n / 4 : n, vec);
     if (out_i32)
         hipLaunchKernelGGL(k_fp8_encode<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
                            x, n, vec, scaled, q);
@@ -578,6 +724,14 @@ int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_d
                            c->stream, x, n, vec, scaled, q);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
+}
+
+// Per-tensor FP8 activation quantize: the MM_FP8 scale, then the scaled
+// encode reading it from *p.
+int launch_quant_fp8_dynamic(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_dev* p, void* q,
+                             bool out_i32) {
+    TKV_RC_TRY(launch_minmax_tensor(c, x, n, MM_FP8, TKV_HIP_RECIPE_PRIMARY, p));
+    return launch_fp8_encode(c, x, n, p, q, out_i32);
 }
 
 template <bool IN_I32>
@@ -593,7 +747,7 @@ __global__ __launch_bounds__(kBlock) void k_fp8_decode(const void* __restrict__ 
 
 int launch_fp8_decode(Ctx* c, const void* q, bool in_i32, int64_t n, float* y) {
     if (n <= 0) return TKV_HIP_OK;
-    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    int64_t blocks = scalar_blocks(c, n / 4 + 1);
     if (in_i32)
         hipLaunchKernelGGL(k_fp8_decode<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
                            q, n, y);
@@ -626,7 +780,7 @@ int launch_i32_to_i8(Ctx* c, const int32_t* src, int64_t rows, int64_t cols, int
                      int8_t* dst, int64_t ld_dst, int code_bias) {
     int64_t n = rows * ld_dst;
     if (n <= 0) return TKV_HIP_OK;
-    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    int64_t blocks = scalar_blocks(c, n / 4 + 1);
     hipLaunchKernelGGL(k_i32_to_i8, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, src, rows,
                        cols, ld_src, dst, ld_dst, code_bias);
     TKV_LAUNCH_CHECK();
@@ -642,7 +796,7 @@ __global__ __launch_bounds__(kBlock) void k_i8_to_i32(const int8_t* __restrict__
 
 int launch_i8_to_i32(Ctx* c, const int8_t* src, int64_t n, int32_t* dst, int code_bias) {
     if (n <= 0) return TKV_HIP_OK;
-    int64_t blocks = stream_blocks(c, n / 4 + 1);
+    int64_t blocks = scalar_blocks(c, n / 4 + 1);
     hipLaunchKernelGGL(k_i8_to_i32, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream, src, n,
                        dst, code_bias);
     TKV_LAUNCH_CHECK();

@@ -22,16 +22,6 @@ __device__ __forceinline__ int rne_clamp(double p, double lo, double hi) {
     return (int)r;
 }
 
-// Round v >= 0 right by s bits, ties to even (types.tkv:71-93).  Callers pass
-// v < 2^24, so every shift >= 25 yields 0, as the reference's does.
-__device__ __forceinline__ uint32_t rne_rshift(uint32_t v, int s) {
-    if (s >= 25) return 0;
-    uint32_t q = v >> s;
-    uint32_t rem = v & ((1u << s) - 1u);
-    uint32_t half = 1u << (s - 1);
-    return q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
-}
-
 // e4m3 encode of the reference (types.tkv:154-191 with bias 7, 3 mantissa
 // bits, emax field 15, no inf, saturation code 0x7E) on the binary32 bits.
 // Its three departures from OCP e4m3fn are kept: |x| >= 248 -> 0x7E,
@@ -39,30 +29,23 @@ __device__ __forceinline__ uint32_t rne_rshift(uint32_t v, int s) {
 // NaN gives 0x38: f64_to_f32_bits(NaN) falls through both exponent loops and
 // returns the bits of 1.0.  +-inf gives 0x7F|sign (the reference's loop never
 // ends there).
+//
+// Branch-free form (checked against the scalar restatement on all 2^32
+// inputs).  Normal range (|x| >= 2^-6): rounding the f32 magnitude bits to
+// 3 mantissa bits, ties to even, carries into the exponent by itself, and
+// rebiasing 127 -> 7 subtracts 120 << 3.  Subnormal range: the code is
+// rne(|x| * 2^9) (exact scaling), clamped to 7 as the reference does.
 __device__ __forceinline__ uint32_t e4m3_encode(float x) {
-    uint32_t b = __float_as_uint(x);
-    uint32_t mag = b & 0x7fffffffu;
-    if (mag == 0) return 0;
-    if (mag > 0x7f800000u) return 0x38;
-    uint32_t sign = (b >> 24) & 0x80u;
-    if (mag == 0x7f800000u) return sign | 0x7fu;
-    uint32_t ex = mag >> 23;
-    uint32_t man = mag & 0x7fffffu;
-    int e = ex ? (int)ex - 127 : -126;
-    uint32_t full = ex ? (man | 0x800000u) : man;
-    int e8 = e + 7;
-    if (e8 >= 15) return sign | 0x7eu;
-    if (e8 <= 0) {
-        uint32_t m = rne_rshift(full, 21 - e8);
-        return sign | (m > 7u ? 7u : m);
-    }
-    uint32_t r = rne_rshift(full, 20);
-    if (r >= 16u) {
-        r = 8u;
-        e8 += 1;
-        if (e8 >= 15) return sign | 0x7eu;
-    }
-    return sign | ((uint32_t)e8 << 3) | (r - 8u);
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t mag = b & 0x7fffffffu, sign = (b >> 24) & 0x80u;
+    uint32_t nc = ((mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20) - 960u;
+    nc = mag >= 0x43780000u ? 0x7eu : nc;  // >= 248: rounds to exponent field 15
+    const float s = __builtin_rintf(__uint_as_float(mag) * 512.0f);
+    const uint32_t sc = s > 7.0f ? 7u : (uint32_t)s;
+    uint32_t code = sign | (mag >= 0x3c800000u ? nc : sc);
+    code = mag == 0u ? 0u : code;
+    code = mag == 0x7f800000u ? (sign | 0x7fu) : code;
+    return mag > 0x7f800000u ? 0x38u : code;
 }
 
 // e4m3 decode of the reference (types.tkv:193-226 through f32_bits_to_f64,

@@ -90,6 +90,9 @@ int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qpar
 // calibrate_minmax(x, 1) + quantize_int8_symmetric in two kernels; *p = QuantParams.
 int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
                             tkv_hip_qparams_dev* p, void* q, bool out_i32);
+// Per-tensor FP8 scale (MM_FP8) + scaled e4m3 encode; *p = QuantParams.
+int launch_quant_fp8_dynamic(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_dev* p,
+                             void* q, bool out_i32);
 int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mode,
                       const float* scales_in, void* q, bool out_i32, float* scales_out,
                       tkv_hip_qparams_dev* row_params, int symmetric);
