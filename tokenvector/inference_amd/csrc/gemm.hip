@@ -155,50 +155,71 @@ struct EpiI8 {
         return o;
     }
 
-    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
-    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
-                                          const Operands<C>& o, int m0, int n0, int M, int N,
-                                          void* __restrict__ Y) const {
-        if (MODE == EPI_ACCUM_I32) {
-            write_tile<C, P0, NP>(static_cast<int32_t*>(Y), m0, n0, M, N,
-                          [&](int i, int j, int r) { return pin(acc[i][j][r]); });
-            return;
-        }
-        float* Yf = static_cast<float*>(Y);
-        if (MODE == EPI_PER_CHANNEL && RECIPE == TKV_HIP_RECIPE_PRIMARY) {
+    // Calls f(value) once, value(i, j, r) being the 32 output bits of
+    // accumulator register r of block (i, j): f32 bits, or the INT32 itself.
+    template <class C, class P, class F>
+    __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
+                                               const Operands<C>& o, F&& f) const {
+        if constexpr (MODE == EPI_ACCUM_I32) {
+            f([&](int i, int j, int r) { return (uint32_t)pin(acc[i][j][r]); });
+        } else if constexpr (MODE == EPI_PER_CHANNEL && RECIPE == TKV_HIP_RECIPE_PRIMARY) {
             if (fold) {
                 double c[C::TN];
 #pragma unroll
                 for (int j = 0; j < C::TN; j++) c[j] = (double)o.sa(0, 0) * (double)o.sw[j];
-                write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+                f([&](int i, int j, int r) {
                     double v = (double)pin(acc[i][j][r]) * c[j];
                     v = v + (double)o.b[j];
-                    return (float)v;
+                    return __float_as_uint((float)v);
                 });
             } else {
-                write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+                f([&](int i, int j, int r) {
                     double v = (double)pin(acc[i][j][r]) * (double)o.sa(i, r);
                     v = v * (double)o.sw[j];
                     v = v + (double)o.b[j];
-                    return (float)v;
+                    return __float_as_uint((float)v);
                 });
             }
-        } else if (MODE == EPI_PER_CHANNEL) {
-            write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+        } else if constexpr (MODE == EPI_PER_CHANNEL) {
+            f([&](int i, int j, int r) {
                 float t = (float)pin(acc[i][j][r]) * o.sa(i, r);
                 t = t * o.sw[j];
-                return t + o.b[j];
+                return __float_as_uint(t + o.b[j]);
             });
         } else {
-            write_tile<C, P0, NP>(Yf, m0, n0, M, N, [&](int i, int j, int r) {
+            f([&](int i, int j, int r) {
                 const double s = RECIPE == TKV_HIP_RECIPE_PRIMARY
                                      ? (double)(o.sa(i, r) * scale_w)
                                      : (double)o.sa(i, r) * (double)scale_w;
                 double v = (double)pin(acc[i][j][r]) * s;
                 v = v + (double)o.b[j];
-                return (float)v;
+                return __float_as_uint((float)v);
             });
         }
+    }
+
+    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
+    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
+                                          const Operands<C>& o, int m0, int n0, int M, int N,
+                                          void* __restrict__ Y) const {
+        with_value<C, P>(acc, o, [&](auto&& value) {
+            write_tile<C, P0, NP>(static_cast<uint32_t*>(Y), m0, n0, M, N, value);
+        });
+    }
+
+    // The tile's outputs into registers (stored later with write_tile).
+    template <class C, class P>
+    __device__ __forceinline__ void values(const typename P::Acc (&acc)[C::TM][C::TN],
+                                           const Operands<C>& o,
+                                           uint32_t (&out)[C::TM][C::TN][16]) const {
+        with_value<C, P>(acc, o, [&](auto&& value) {
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) out[i][j][r] = value(i, j, r);
+        });
     }
 };
 
@@ -223,18 +244,40 @@ struct EpiF8 {
         return o;
     }
 
-    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
-    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
-                                          const Operands<C>& o, int m0, int n0, int M, int N,
-                                          void* __restrict__ Y) const {
-        write_tile<C, P0, NP>(static_cast<float*>(Y), m0, n0, M, N, [&](int i, int j, int r) {
+    template <class C, class P, class F>
+    __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
+                                               const Operands<C>& o, F&& f) const {
+        f([&](int i, int j, int r) {
             double v = (double)(pin(acc[i][j][r]) * P::kAccScale);
             if (SCALED) {
                 v = v * (double)o.sa(i, r);
                 v = v * (double)o.sw[j];
             }
             v = v + (double)o.b[j];
-            return (float)v;
+            return __float_as_uint((float)v);
+        });
+    }
+
+    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
+    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
+                                          const Operands<C>& o, int m0, int n0, int M, int N,
+                                          void* __restrict__ Y) const {
+        with_value<C, P>(acc, o, [&](auto&& value) {
+            write_tile<C, P0, NP>(static_cast<uint32_t*>(Y), m0, n0, M, N, value);
+        });
+    }
+
+    template <class C, class P>
+    __device__ __forceinline__ void values(const typename P::Acc (&acc)[C::TM][C::TN],
+                                           const Operands<C>& o,
+                                           uint32_t (&out)[C::TM][C::TN][16]) const {
+        with_value<C, P>(acc, o, [&](auto&& value) {
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) out[i][j][r] = value(i, j, r);
         });
     }
 };
@@ -282,21 +325,26 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm(const uint8_t* __restrict__
     }
 }
 
-// ep.store of part `part` (wave-uniform, run time, < C::TM * 16 <= 64) of a
-// tile: one scalar jump to the compile-time part.
-template <class C, class P, class E>
-__device__ __forceinline__ void store_part_dyn(const E& ep, int part,
-                                               const typename P::Acc (&acc)[C::TM][C::TN],
-                                               const typename E::template Operands<C>& o,
-                                               int m0, int n0, int M, int N, void* __restrict__ Y) {
+// Stores part `part` (wave-uniform, run time, < C::TM * 16 <= 64) of a
+// wave's finished output values, the wave's tile lying inside [M, N]: yw is
+// the wave tile's first output, loff the lane's offset from it.  One scalar
+// jump to the compile-time part, no bounds checks.
+template <class C>
+__device__ __forceinline__ void store_part_dyn(int part, const uint32_t (&v)[C::TM][C::TN][16],
+                                               uint32_t* __restrict__ yw, int N, uint32_t loff) {
     static_assert(C::TM * 16 <= 64, "parts");
     switch (part) {
-#define TKV_PART(i)                                                              \
-    case i:                                                                      \
-        if constexpr (i < C::TM * 16) ep.template store<C, P, i, 1>(acc, o, m0, n0, M, N, Y); \
+#define TKV_PART(p)                                                                      \
+    case p:                                                                              \
+        if constexpr (p < C::TM * 16) {                                                  \
+            constexpr int i = p / 16 < C::TM ? p / 16 : 0, r = p % 16;                  \
+            uint32_t* rowp = yw + (int64_t)(i * 32 + (r >> 2) * 8 + (r & 3)) * N;        \
+            _Pragma("unroll") for (int j = 0; j < C::TN; j++)                            \
+                put(rowp + loff + j * 32, v[i][j][r]);                                   \
+        }                                                                                \
         break;
-#define TKV_PART8(i) TKV_PART(i) TKV_PART(i + 1) TKV_PART(i + 2) TKV_PART(i + 3) \
-    TKV_PART(i + 4) TKV_PART(i + 5) TKV_PART(i + 6) TKV_PART(i + 7)
+#define TKV_PART8(p) TKV_PART(p) TKV_PART(p + 1) TKV_PART(p + 2) TKV_PART(p + 3) \
+    TKV_PART(p + 4) TKV_PART(p + 5) TKV_PART(p + 6) TKV_PART(p + 7)
         TKV_PART8(0) TKV_PART8(8) TKV_PART8(16) TKV_PART8(24)
         TKV_PART8(32) TKV_PART8(40) TKV_PART8(48) TKV_PART8(56)
 #undef TKV_PART8
@@ -317,7 +365,7 @@ __device__ __forceinline__ void store_part_dyn(const E& ep, int part,
 // The barrier after slice s both publishes slice s + 1 to the consumers and
 // tells the producers that slice s's slot is free again.
 template <class C, class P, class E>
-__global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restrict__ A,
+__global__ __launch_bounds__(C::THREADS, C::MIN_WAVES_EU) void k_gemm_ws(const uint8_t* __restrict__ A,
                                                         const uint8_t* __restrict__ W, int M,
                                                         int N, int ldk, E ep,
                                                         void* __restrict__ Y) {
@@ -408,20 +456,19 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restric
             ep.template store<C, P>(acc, eo, m0, n0, M, N, Y);
         }
     } else {
-        // The previous tile's accumulators (pacc) are stored one part per K
-        // slice of the current tile, after that slice's MFMAs are issued.
-        // DEFER == 1: four-register parts in the first slices; DEFER == 2:
-        // single-register parts spread evenly over all of the tile's slices.
+        // Deferred stores: a finished tile is turned into its output values
+        // (the epilogue arithmetic runs once, at the tile's end) and those are
+        // stored during the next tile's K slices, one even share of the
+        // C::TM * 16 parts after each slice's MFMAs, so the HBM writes drain
+        // while the matrix cores work instead of stalling the consumers
+        // between tiles.  Wave tiles crossing the M / N edge are stored at
+        // once (with bounds checks); the last tile's values at the end.
         constexpr int NPART = C::TM * 16;
-        constexpr int GRAIN = C::DEFER == 1 ? 4 : 1;
-        typename P::Acc pacc[C::TM][C::TN];
-        typename E::template Operands<C> peo;
-        int pm0 = 0, pn0 = 0;
+        uint32_t pv[C::TM][C::TN][16];
+        uint32_t* Y32 = static_cast<uint32_t*>(Y);
+        const uint32_t loff = (uint32_t)(khalf * 4) * (uint32_t)N + (uint32_t)(lane & 31);
+        uint32_t* yw = Y32;
         bool have = false;
-        auto store_parts = [&](int lo, int hi) {
-            for (int part = lo; part < hi; part++)
-                store_part_dyn<C, P>(ep, part, pacc, peo, pm0, pn0, M, N, Y);
-        };
         for (int ti = 0; ti < my_tiles; ti++) {
             const int t = xcd_tile(b + ti * G, tiles);
             const int m0 = (t / tiles_n) * C::BM, n0 = (t % tiles_n) * C::BN;
@@ -436,25 +483,23 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_ws(const uint8_t* __restric
             for (int kt = 0; kt < nk; kt++, s++) {
                 const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
                 P::template slice<C>(sa, sa + C::A_BYTES, a_row, w_row, khalf, acc);
-                if (have) {
-                    if constexpr (GRAIN == 1)
-                        store_parts(kt * NPART / nk, (kt + 1) * NPART / nk);
-                    else if (kt < NPART / GRAIN)
-                        store_parts(kt * GRAIN, kt * GRAIN + GRAIN);
-                }
+                if (have)
+                    for (int part = kt * NPART / nk; part < (kt + 1) * NPART / nk; part++)
+                        store_part_dyn<C>(part, pv, yw, N, loff);
                 barrier();
             }
-            if (have && GRAIN > 1 && nk < NPART / GRAIN) store_parts(nk * GRAIN, NPART);
-#pragma unroll
-            for (int i = 0; i < C::TM; i++)
-#pragma unroll
-                for (int j = 0; j < C::TN; j++) pacc[i][j] = acc[i][j];
-            peo = eo;
-            pm0 = m0;
-            pn0 = n0;
-            have = true;
+            const int rbase = m0 + wm * C::WTM, cbase = n0 + wn * C::WTN;
+            if (rbase + C::WTM <= M && cbase + C::WTN <= N) {
+                ep.template values<C, P>(acc, eo, pv);
+                yw = Y32 + (int64_t)rbase * N + cbase;
+                have = true;
+            } else {
+                ep.template store<C, P>(acc, eo, m0, n0, M, N, Y);
+                have = false;
+            }
         }
-        if (have) ep.template store<C, P>(pacc, peo, pm0, pn0, M, N, Y);
+        if (have)
+            for (int part = 0; part < NPART; part++) store_part_dyn<C>(part, pv, yw, N, loff);
     }
 }
 
@@ -530,15 +575,19 @@ __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__
 //            BM   BN  WM WN   BK  STAGES
 typedef Cfg<64, 128, 2, 2, 128, 3> Cfg0;   //  72 KB, small M (tiles < CUs)
 typedef Cfg<128, 192, 4, 2, 128, 3> Cfg1;  // 120 KB, 8 waves, 32x96 wave tiles
-// warp-specialised:  BM   BN  WM WN   BK  STAGES PW DEFER
+// warp-specialised:  BM   BN  WM WN   BK  STAGES PW DEFER FD
+// (cfg 7 and 9 defer each tile's stores into the next tile's K slices; at
+// M = 8192 they win on the N = 768 shapes by a few percent and lose on the
+// wide ones, where the extra values cost fragment read-ahead: cfg 2 stays
+// the default)
 typedef CfgWS<128, 192, 4, 2, 128, 3, 4> Cfg2;     // 120 KB, 8 consumers (32x96) + 4 producers
 typedef CfgWS<128, 192, 2, 2, 128, 3, 4> Cfg3;     // 120 KB, 4 consumers (64x96) + 4 producers
 typedef CfgWS<128, 128, 2, 2, 128, 3, 4> Cfg4;     //  96 KB, 4 consumers (64x64) + 4 producers
 typedef CfgWS<64, 128, 2, 2, 128, 3, 4> Cfg5;      //  72 KB, 4 consumers (32x64) + 4 producers
 typedef CfgWS<128, 192, 4, 2, 128, 4, 4> Cfg6;     // 160 KB, 3 slices in flight
-typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 2> Cfg7;  // Cfg2 + stores spread over the next tile
-typedef CfgWS<128, 128, 2, 2, 128, 3, 4, 1> Cfg8;  // Cfg4 + deferred stores
-typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 1> Cfg9;  // Cfg2 + stores in the next tile's first slices
+typedef CfgWS<128, 192, 4, 2, 128, 3, 4, 1, 1> Cfg7;  // Cfg2 + stores spread over the next tile
+typedef CfgWS<128, 192, 4, 3, 128, 3, 4> Cfg8;     // 120 KB, 12 consumers (32x64) + 4 producers
+typedef CfgWS<128, 192, 4, 3, 128, 3, 4, 1, 1> Cfg9;  // Cfg8 + stores spread over the next tile
 
 constexpr int kBK = 128;
 

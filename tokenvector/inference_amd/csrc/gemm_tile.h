@@ -68,7 +68,7 @@ struct Cfg {
 // drain while the producers keep the ring full, and no consumer ever waits on
 // vmcnt for operand data.
 template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int PW_, int DEFER_ = 0,
-          int FD_ = 0>
+          int FD_ = 0, int OCC_ = 1>
 struct CfgWS {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_, STAGES = STAGES_;
     static constexpr int CW = WM * WN, PW = PW_;
@@ -83,16 +83,19 @@ struct CfgWS {
     static constexpr int A_BYTES = BM * BK, W_BYTES = BN * BK;
     static constexpr int STAGE_BYTES = A_BYTES + W_BYTES;
     static constexpr int LDS_BYTES = STAGE_BYTES * STAGES;
-    // DEFER: a tile's output stores are issued during the next tile's K slices
-    // (the consumer keeps the finished accumulators), so HBM writes proceed
-    // during the MFMA work instead of in bursts between tiles: 1 = in the
-    // first slices, four registers per slice; 2 = one register at a time,
-    // spread evenly over all slices.  The extra
-    // accumulator set is paid for by reading fragments only two k-steps ahead.
+    // DEFER: a tile's output values are stored during the next tile's K
+    // slices (spread evenly over them) instead of between tiles; the values
+    // wait in registers, paid for by reading fragments fewer k-steps ahead.
     // FD (fragment depth, k-steps read ahead; 0 = automatic) trades registers
-    // for LDS latency hiding, e.g. to fit four waves per SIMD.
+    // for LDS latency hiding.
     static constexpr int DEFER = DEFER_;
     static constexpr int FRAG_DEPTH = FD_ ? FD_ : (DEFER ? 2 : BK / 32);
+    // OCC workgroups resident per CU: the register budget is set for
+    // OCC * WAVES waves over the 4 SIMDs, so that while one workgroup's
+    // consumers wait on their output stores the other's run MFMAs.
+    static constexpr int OCC = OCC_;
+    static constexpr int MIN_WAVES_EU = (OCC * WAVES + 3) / 4;
+    static_assert(OCC * LDS_BYTES <= 163840, "OCC workgroups must fit the CU's LDS");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32x32 blocks");
     static_assert(BM % ROWS_PER_DMA == 0 && BN % ROWS_PER_DMA == 0, "rows per DMA block");
     static_assert((A_BLK + W_BLK) % PW == 0, "DMA blocks must split evenly over producers");
