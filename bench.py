@@ -138,6 +138,7 @@ def run_gpu(steps, warmup):
     quant = bench_quant(ctx, D, O)
     fp8 = bench_fp8(ctx, D, O)
     decode = bench_decode(ctx, D, O)
+    qlinear = bench_qlinear(ctx, D)
     ctx.close()
     return {
         "ms_per_step": ms_per_step,
@@ -148,6 +149,7 @@ def run_gpu(steps, warmup):
         "quant": quant,
         "fp8": fp8,
         "decode": decode,
+        "qlinear": qlinear,
         "ops_per_step": ops_step,
     }
 
@@ -203,6 +205,35 @@ def bench_fp8(ctx, D, O, ms=(2048, 8192, 32768), reps=10):
         lin.close()
     out["note"] = ("fast: v_mfma_scale_f32_32x32x64_f8f6f4, peak 5000 TFLOP/s; reference_products: "
                    "reference-decoded operands on v_mfma_f32_32x32x16_f16, peak 2500 TFLOP/s")
+    return out
+
+
+def bench_qlinear(ctx, D, m=M, reps=20):
+    """QLinearMatMul (session.tkv:1992-2071) on the four GPT-2 shapes: int8
+    codes in, zero-point corrections and requantization fused into the INT8
+    GEMM's epilogue, int8 out.  Algorithmic bytes M*K + N*K + M*N; with the
+    small output the shapes are MFMA-bound.  Two input sets are cycled."""
+    rng = np.random.default_rng(7)
+    out = {}
+    for (name, n, k) in SHAPES:
+        sets = [(D.DeviceBuffer.from_host(ctx, rng.integers(-128, 128, m * k).astype(np.int8)),
+                 D.DeviceBuffer.empty(ctx, (m, n), np.int8)) for _ in range(2)]
+        w = D.DeviceBuffer.from_host(ctx, rng.integers(-128, 128, n * k).astype(np.int8))
+        sy = float(np.float32(np.sqrt(k) * 128 * 128 * 0.02 * 0.003 / 90.0))
+        us = _time_us(ctx, D, lambda i: D.qlinear_matmul(
+            ctx, sets[i % 2][0], 0.02, -3, w, 0.003, 5, sy, 7, sets[i % 2][1], m, n, k), reps)
+        ops = 2.0 * m * n * k
+        nbytes = m * k + n * k + m * n
+        ceil = min(PEAK_INT8_TOPS, ops / nbytes * PEAK_HBM_GBPS * 1e9 / 1e12)
+        tops = ops / (us * 1e-6) / 1e12
+        out[f"{name}_m{m}"] = {"us": round(us, 2), "tops": round(tops, 1),
+                               "ceiling_tops": round(ceil, 1),
+                               "frac_of_ceiling": round(tops / ceil, 3)}
+        for t in sets:
+            for buf in t:
+                buf.close()
+        w.close()
+    out["note"] = "int8 in / int8 out, zero points and requantization fused in the epilogue"
     return out
 
 
@@ -410,6 +441,7 @@ def main():
         "quantize": r["quant"],
         "fp8": r["fp8"],
         "decode": r["decode"],
+        "qlinear": r["qlinear"],
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_rows)

@@ -176,6 +176,18 @@ int32_t tkv_hip_quantized_gemm(const int32_t* aq, const int32_t* wq, const float
  * with B row-major [K,N]; reads past na/nb are 0, writes past ny dropped. */
 int32_t tkv_hip_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, int64_t nb,
                                int64_t* y, int64_t ny, int64_t m, int64_t n, int64_t k);
+/* QLinearMatMul node (session.tkv:1992-2071, OperatorType_QLinearMatMul = 65):
+ * y = clamp(round(acc * mult) + zpy, -128, 127) with
+ * acc = sum_p (a[i,p] - zpa) (b[p,j] - zpw) and mult = sa * sw / sy (sy == 0
+ * reads as 1).  B is row-major [K,N] as in the node.  recipe PRIMARY: sa, sw,
+ * sy are f64 locals holding the f32 inputs (mult = fl64(sa*sw/sy)); ALTERNATE:
+ * the f32 chain fl32(fl32(sa*sw)/sy).  Reads past na / nb contribute 0 as in
+ * the node (TKV_HIP_UNSUPPORTED when a zero point outside [-128, 127] would be
+ * needed to express that); writes past ny are dropped. */
+int32_t tkv_hip_qlinear_matmul(const int32_t* a, int64_t na, float sa, int64_t zpa,
+                               const int32_t* b, int64_t nb, float sw, int64_t zpw, float sy,
+                               int64_t zpy, int32_t* y, int64_t ny, int64_t m, int64_t n,
+                               int64_t k, int32_t recipe);
 /* QuantizeLinear node (session.tkv:1896-1953): n_scales == 1 per-tensor, else
  * per-axis over the [outer, dim, inner] view of x. */
 int32_t tkv_hip_quantize_linear(const float* x, int64_t nx, const float* scales,
@@ -249,6 +261,13 @@ int32_t tkv_hip_dev_matmul_int8(int64_t ctx, const int8_t* a, const int8_t* w, i
                                 int64_t scale_a_stride, float scale_w,
                                 const float* scales_w, const float* bias, float* y,
                                 int32_t recipe);
+/* QLinearMatMul on device codes (session.tkv:1992-2071): a int8 [M,K], w int8
+ * [N,K] (the node's B transposed: K-major, like every weight here), y int8
+ * [M,N]; one GEMM with the zero-point corrections and the requantization
+ * fused into its epilogue.  Same numerics and recipe switch as the mirror. */
+int32_t tkv_hip_dev_qlinear_matmul(int64_t ctx, const int8_t* a, float sa, int32_t zpa,
+                                   const int8_t* w, float sw, int32_t zpw, float sy, int32_t zpy,
+                                   int8_t* y, int64_t m, int64_t n, int64_t k, int32_t recipe);
 /* INT32 accumulators only (MatMulInteger core; exactness checks). */
 int32_t tkv_hip_dev_matmul_int8_accum(int64_t ctx, const int8_t* a, const int8_t* w,
                                       int64_t m, int64_t n, int64_t k, int32_t* acc);

@@ -94,6 +94,8 @@ def _declare(L: C.CDLL) -> None:
         "tkvo_matmul_fp8_e4m3": (I32, [P, P, P, I64, P, I64, I64, I64]),
         "tkvo_matmul_fp8_e4m3_exact": (I32, [P, P, P, P, I64, I64, I64]),
         "tkvo_matmul_integer": (I32, [P, I64, P, I64, P, I64, I64, I64, I64]),
+        "tkvo_qlinear_matmul": (I32, [P, I64, F32, I64, P, I64, F32, I64, F32, I64, P, I64,
+                                      I64, I64, I64, I32]),
         "tkvo_quantize_linear": (I32, [P, I64, P, I64, I64, I64, I64, I64, P]),
         "tkvo_dequantize_linear": (I32, [P, I64, P, I64, I64, I64, I64, I64, P]),
         "tkvo_dynamic_quantize_linear": (I32, [P, I64, P, P, P]),
@@ -333,6 +335,16 @@ def matmul_integer(a, b, y_len, m, n, k) -> np.ndarray:
     y = np.zeros(max(int(y_len), 1), dtype=np.int64)
     lib().tkvo_matmul_integer(_p(A), A.size, _p(B), B.size, _p(y), int(y_len),
                               int(m), int(n), int(k))
+    return y[: int(y_len)]
+
+
+def qlinear_matmul(a, sa, zpa, b, sw, zpw, sy, zpy, y_len, m, n, k,
+                   recipe: int = PRIMARY) -> np.ndarray:
+    A, B = _i32(a), _i32(b)
+    y = np.zeros(max(int(y_len), 1), dtype=np.int32)
+    lib().tkvo_qlinear_matmul(_p(A), A.size, float(np.float32(sa)), int(zpa), _p(B), B.size,
+                              float(np.float32(sw)), int(zpw), float(np.float32(sy)), int(zpy),
+                              _p(y), int(y_len), int(m), int(n), int(k), int(recipe))
     return y[: int(y_len)]
 
 

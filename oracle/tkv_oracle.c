@@ -520,6 +520,47 @@ int32_t tkvo_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, int6
     return 0;
 }
 
+/* session.tkv:1992-2058.  The locals sa, sw, sy hold _span0's f32 values;
+ * unannotated float locals are f64 in the generated IL, so mult is one f64
+ * division of the exact f64 product (primary).  The integer sum is the
+ * runtime's overflow-free integer; acc * mult widens acc to f64 (exact for
+ * |acc| < 2^53). */
+int32_t tkvo_qlinear_matmul(const int32_t* a, int64_t na, float sa, int64_t zpa,
+                            const int32_t* b, int64_t nb, float sw, int64_t zpw, float sy,
+                            int64_t zpy, int32_t* y, int64_t ny, int64_t m, int64_t n,
+                            int64_t k, int32_t recipe) {
+    double mult;
+    if (recipe == TKVO_RECIPE_PRIMARY) {
+        double dsy = (double)sy;
+        if (dsy == 0.0) dsy = 1.0;
+        mult = (double)sa * (double)sw / dsy;
+    } else {
+        float fsy = sy == 0.0f ? 1.0f : sy;
+        float fm = sa * sw;
+        fm = fm / fsy;
+        mult = (double)fm;
+    }
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t j = 0; j < n; j++) {
+            int64_t acc = 0;
+            for (int64_t p = 0; p < k; p++) {
+                int64_t ai = i * k + p;
+                int64_t bi = p * n + j;
+                int64_t av = (ai >= 0 && ai < na) ? (int64_t)a[ai] - zpa : 0;
+                int64_t bv = (bi >= 0 && bi < nb) ? (int64_t)b[bi] - zpw : 0;
+                acc = acc + av * bv;
+            }
+            double r = net_round((double)acc * mult);
+            if (r != r) r = 0.0;
+            if (r > 0x1p62) r = 0x1p62;
+            if (r < -0x1p62) r = -0x1p62;
+            int64_t v = clamp_i64((int64_t)r + zpy, -128, 127);
+            int64_t yi = i * n + j;
+            if (yi >= 0 && yi < ny) y[yi] = (int32_t)v;
+        }
+    return 0;
+}
+
 /* session.tkv:1896-1953: q = clamp(round(x / s) + zp, -128, 127) with
  * s = max(sc, 1e-12) as an f64 local: a true f64 division, not a reciprocal
  * multiply.  Integer arithmetic is the runtime's overflow-free integer, so

@@ -27,7 +27,9 @@
  *   - tkvo_quantize_int8_symmetric: whether 1.0/scale (engine.tkv:219-222)
  *     is evaluated in f32 (primary) or f64 (TKVO_RECIPE_ALTERNATE);
  *   - tkvo_matmul_int8_per_channel / _symmetric: whether the i64 * f32
- *     epilogue chains (matmul.tkv:5,14 and :29) run in f64 (primary) or f32.
+ *     epilogue chains (matmul.tkv:5,14 and :29) run in f64 (primary) or f32;
+ *   - tkvo_qlinear_matmul: whether mult = sa * sw / sy (session.tkv:2027)
+ *     runs on f64 locals (primary) or as an f32 chain.
  * No reference test reaches a rounding tie that separates the readings, and
  * the reference compiler (tkvc, .NET) is not available to run.
  */
@@ -119,6 +121,16 @@ int32_t tkvo_matmul_fp8_e4m3_exact(const int32_t* a, const int32_t* w, int64_t* 
  * na/nb are zero and writes outside ny are dropped, as in the reference. */
 int32_t tkvo_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, int64_t nb,
                             int64_t* y, int64_t ny, int64_t m, int64_t n, int64_t k);
+/* QLinearMatMul (session.tkv:1992-2071): y = clamp(round(acc * mult) + zpy,
+ * -128, 127), acc = sum_p (a - zpa)(b - zpw) over in-range reads (others 0),
+ * mult = sa * sw / sy with sy == 0 read as 1; B row-major [K,N]; writes
+ * outside ny dropped.  recipe: TKVO_RECIPE_PRIMARY (f64 locals) or
+ * TKVO_RECIPE_ALTERNATE (f32 chain for mult).  Parity unpinned for the
+ * recipe choice (no reference test runs the node). */
+int32_t tkvo_qlinear_matmul(const int32_t* a, int64_t na, float sa, int64_t zpa,
+                            const int32_t* b, int64_t nb, float sw, int64_t zpw, float sy,
+                            int64_t zpy, int32_t* y, int64_t ny, int64_t m, int64_t n,
+                            int64_t k, int32_t recipe);
 /* QuantizeLinear (session.tkv:1896-1953).  nscale == 1: per-tensor; else
  * per-axis with the tensor viewed as [outer, dim, inner]. */
 int32_t tkvo_quantize_linear(const float* x, int64_t nx, const float* scales,

@@ -381,6 +381,43 @@ def test_matmul_integer_node(hip):
     assert np.array_equal(y, O.matmul_integer(a, b, m * n - 2, m, n, k))
 
 
+def test_qlinear_matmul_node(hip):
+    """QLinearMatMul node mirror (session.tkv:1992-2071) against the oracle,
+    bit-exact: the ONNX-style 2x2 case, random zero points and scales at tile
+    edges, short A / B / Y, sy == 0, K == 0, both recipes."""
+    say("QLinearMatMul node")
+    node = S.new_node("ql", S.OperatorType_QLinearMatMul)
+    one = lambda v: (np.array([v], np.float32), [1])
+    (y,) = node.execute([([1, 2, 3, 4], [2, 2]), one(0.5), one(0), ([1, 1, 1, 1], [2, 2]),
+                         one(0.5), one(0), one(0.25), one(0)], [[2, 2]])
+    assert list(y) == [3, 3, 7, 7]
+    cases = [(1, 1, 1), (2, 3, 5), (33, 17, 45), (129, 200, 300), (300, 500, 384), (5, 7, 0)]
+    for ci, (m, n, k) in enumerate(cases):
+        a = RNG.integers(-128, 128, m * k).astype(np.int32)
+        b = RNG.integers(-128, 128, k * n).astype(np.int32)
+        if ci == 2:
+            a, b = a[:-5], b[:-7]
+        zpa, zpw, zpy = (int(v) for v in RNG.integers(-30, 31, 3))
+        sa, sw = (float(np.float32(v)) for v in RNG.uniform(0.001, 0.05, 2))
+        if ci == 1:
+            sy = 0.0
+        else:  # map the sums' range onto about +-100 codes
+            av = np.zeros(m * k, np.int64)
+            av[:a.size] = a.astype(np.int64) - zpa
+            bv = np.zeros(k * n, np.int64)
+            bv[:b.size] = b.astype(np.int64) - zpw
+            span = max(1, int(np.abs(av.reshape(m, k) @ bv.reshape(k, n)).max())) if k else 1
+            sy = float(np.float32(sa * sw * span / 100.0))
+        ny = m * n - (3 if ci == 3 else 0)
+        for recipe in (0, 1):
+            (y,) = [node._qlinear_matmul([(a, [m, k]), one(sa), one(zpa), (b, [k, n]), one(sw),
+                                          one(zpw), one(sy), one(zpy)], [ny], recipe)]
+            want = O.qlinear_matmul(a, sa, zpa, b, sw, zpw, sy, zpy, ny, m, n, k, recipe)
+            assert np.array_equal(y, want), (m, n, k, recipe)
+            if ci >= 3 and k > 0:
+                assert np.unique(y).size > 50, "requantized codes should spread over the range"
+
+
 def test_qdq_nodes(hip):
     say("Q/DQ nodes")
     x = _x(2 * 3 * 40, 8, 3.0).reshape(2, 3, 40)
@@ -561,3 +598,30 @@ def test_linear_forward_per_token(ctx):
                 + b.astype(np.float64)[None, :]).astype(np.float32)
         assert _same_f32(dy.download(), want), (m, n, k)
         lin.close()
+
+
+@pytest.mark.parametrize("cfg", GEMM_CFGS)
+def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
+    """Device QLinearMatMul (fused requantizing epilogue, int8 out) on every
+    GEMM configuration, including the skinny kernel (M <= 32), bit-exact."""
+    gemm_cfg(cfg)
+    for (m, n, k) in [(37, 100, 200), (1024, 768, 768), (16, 2304, 768)]:
+        say(f"dev qlinear cfg={cfg} {m}x{n}x{k}")
+        a = RNG.integers(-128, 128, m * k).astype(np.int8)
+        w = RNG.integers(-128, 128, n * k).astype(np.int8)   # [N, K] = B transposed
+        zpa, zpw, zpy = -3, 5, 7
+        sa, sw = np.float32(0.02), np.float32(0.003)
+        sy = np.float32(np.sqrt(k) * 128 * 128 * sa * sw / 90.0)
+        da, dw = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, w)
+        dy = D.DeviceBuffer.empty(ctx, (m, n), np.int8)
+        _lib_check(D, "tkv_hip_dev_qlinear_matmul", ctx.handle, da.ptr, float(sa), zpa, dw.ptr,
+                   float(sw), zpw, float(sy), zpy, dy.ptr, m, n, k, 0)
+        b = np.ascontiguousarray(w.reshape(n, k).T).reshape(-1).astype(np.int32)
+        want = O.qlinear_matmul(a.astype(np.int32), sa, zpa, b, sw, zpw, sy, zpy, m * n, m, n, k)
+        got = dy.download().astype(np.int32).reshape(-1)
+        assert np.array_equal(got, want), (cfg, m, n, k, int(np.sum(got != want)))
+
+
+def _lib_check(D, name, *args):
+    from tokenvector.inference_amd import _lib
+    _lib.check(getattr(_lib.lib(), name)(*args))

@@ -332,6 +332,57 @@ def test_matmul_integer_bounds_semantics():
     assert np.array_equal(y, want[: m * n - 3])
 
 
+def _qlinear_numpy(a, sa, zpa, b, sw, zpw, sy, zpy, ny, m, n, k, recipe):
+    """Independent restatement with numpy: in-range reads as (code - zp),
+    out-of-range as 0, int64 matmul, f64 multiply, numpy rint (half even)."""
+    a, b = np.asarray(a, np.int64), np.asarray(b, np.int64)
+    av = np.zeros((m, k), np.int64)
+    bv = np.zeros((k, n), np.int64)
+    ia = np.arange(m * k).reshape(m, k)
+    ib = np.arange(k * n).reshape(k, n)
+    av[ia < a.size] = a[ia[ia < a.size]] - zpa
+    bv[ib < b.size] = b[ib[ib < b.size]] - zpw
+    acc = av @ bv
+    if recipe == O.PRIMARY:
+        mult = np.float64(np.float32(sa)) * np.float64(np.float32(sw)) / (
+            np.float64(np.float32(sy)) if np.float32(sy) != 0 else 1.0)
+    else:
+        fsy = np.float32(sy) if np.float32(sy) != 0 else np.float32(1.0)
+        mult = np.float64((np.float32(sa) * np.float32(sw)) / fsy)
+    v = np.clip(np.rint(acc.astype(np.float64) * mult) + zpy, -128, 127).astype(np.int32)
+    return v.reshape(-1)[:ny]
+
+
+@pytest.mark.parametrize("recipe", [0, 1])
+def test_qlinear_matmul_bruteforce(recipe):
+    """QLinearMatMul (session.tkv:1992-2071) against numpy: random codes and
+    zero points, exact half-way products (mult = 1/2 with odd sums), short
+    A / B (reads past the end are 0, not (0 - zp)), short Y, sy == 0, k == 0."""
+    for case in range(40):
+        m, n, k = (int(v) for v in RNG.integers(1, 9, 3))
+        if case == 0:
+            k = 0
+        a = RNG.integers(-128, 128, m * k).astype(np.int32)
+        b = RNG.integers(-128, 128, k * n).astype(np.int32)
+        if case % 5 == 1 and a.size > 1:
+            a = a[:-2]
+        if case % 7 == 2 and b.size > 1:
+            b = b[:-3]
+        zpa, zpw, zpy = (int(v) for v in RNG.integers(-20, 21, 3))
+        if case % 3 == 0:
+            sa, sw, sy = 0.5, 1.0, 1.0           # every odd sum is a tie
+        else:
+            sa, sw = (float(np.float32(v)) for v in RNG.uniform(0.001, 0.05, 2))
+            sy = 0.0 if case % 11 == 4 else float(np.float32(RNG.uniform(0.05, 2.0)))
+        ny = m * n - (1 if case % 4 == 3 else 0)
+        got = O.qlinear_matmul(a, sa, zpa, b, sw, zpw, sy, zpy, ny, m, n, k, recipe)
+        want = _qlinear_numpy(a, sa, zpa, b, sw, zpw, sy, zpy, ny, m, n, k, recipe)
+        assert np.array_equal(got, want), case
+    # a planted rounding mistake (half away from zero) is caught by the ties
+    acc = np.array([1, 3, 5, -1, -3], np.int64)
+    assert not np.array_equal(np.rint(acc * 0.5), np.floor(acc * 0.5 + 0.5))
+
+
 def test_quantize_linear_per_tensor_and_axis():
     x = RNG.normal(0, 3, (2, 3, 4)).astype(np.float32)
     y = O.quantize_linear(x, [0.05], zero_point=3)

@@ -3,6 +3,7 @@
 // functions raise ValueError (returning TKV_HIP_BAD_ARG), move the
 // reference's int32-per-code lists to and from packed device codes, and run
 // the same kernels as the device-pointer variants.
+#include <climits>
 #include <cstring>
 #include <vector>
 
@@ -103,6 +104,17 @@ int host_gemm_i8(const int32_t* pa, const int32_t* pw, const float* pbias, int64
     TKV_RC_TRY(launch_gemm_i8(c, static_cast<int8_t*>(da), static_cast<int8_t*>(dw), m, n, ldk,
                               ep, dy));
     return download(c, py, dy, ybytes);
+}
+
+// mult = sa * sw / sy of the QLinearMatMul node (session.tkv:2024-2027).
+double qlinear_mult(float sa, float sw, float sy, int32_t recipe) {
+    if (recipe == TKV_HIP_RECIPE_PRIMARY) {
+        double dsy = (double)sy;
+        if (dsy == 0.0) dsy = 1.0;
+        return (double)sa * (double)sw / dsy;
+    }
+    const float fsy = sy == 0.0f ? 1.0f : sy;
+    return (double)((sa * sw) / fsy);
 }
 
 }  // namespace
@@ -392,6 +404,62 @@ int32_t tkv_hip_matmul_integer(const int32_t* a, int64_t na, const int32_t* b, i
     return TKV_HIP_OK;
 }
 
+int32_t tkv_hip_qlinear_matmul(const int32_t* a, int64_t na, float sa, int64_t zpa,
+                               const int32_t* b, int64_t nb, float sw, int64_t zpw, float sy,
+                               int64_t zpy, int32_t* y, int64_t ny, int64_t m, int64_t n,
+                               int64_t k, int32_t recipe) {
+    if (m < 0 || n < 0 || k < 0 || na < 0 || nb < 0 || ny < 0)
+        return set_error(TKV_HIP_BAD_ARG, "negative size");
+    TKV_RC_TRY(check_recipe(recipe));
+    if (m == 0 || n == 0 || ny == 0) return TKV_HIP_OK;
+    auto fits8 = [](int64_t v) { return v >= -128 && v <= 127; };
+    auto fits32 = [](int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; };
+    if (!fits32(zpa) || !fits32(zpw) || !fits32(zpy))
+        return set_error(TKV_HIP_UNSUPPORTED, "QLinearMatMul: zero point beyond int32");
+    // A value read past the end contributes 0 to the node's sum, which a code
+    // equal to the zero point reproduces (k == 0: one such term, acc = 0).
+    const bool pad_a = m * k > na || k == 0, pad_b = k * n > nb || k == 0;
+    if ((pad_a && !fits8(zpa)) || (pad_b && !fits8(zpw)))
+        return set_error(TKV_HIP_UNSUPPORTED, "QLinearMatMul: padding needs an int8 zero point");
+    const int64_t kk = k > 0 ? k : 1;  // k == 0: one zero term (a = zpa) gives acc = 0
+    std::vector<int8_t> A((size_t)(m * kk), (int8_t)(pad_a ? zpa : 0)),
+        Wt((size_t)(n * kk), (int8_t)(pad_b ? zpw : 0));
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t p = 0; p < k; p++) {
+            const int64_t ai = i * k + p;
+            if (ai < na) {
+                if (!fits8(a[ai])) return set_error(TKV_HIP_BAD_ARG, "A code outside int8");
+                A[(size_t)(i * kk + p)] = (int8_t)a[ai];
+            }
+        }
+    for (int64_t p = 0; p < k; p++)
+        for (int64_t j = 0; j < n; j++) {
+            const int64_t bi = p * n + j;
+            if (bi < nb) {
+                if (!fits8(b[bi])) return set_error(TKV_HIP_BAD_ARG, "B code outside int8");
+                Wt[(size_t)(j * kk + p)] = (int8_t)b[bi];
+            }
+        }
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    void *da, *dw, *dy;
+    TKV_RC_TRY(upload(c, WS_A, A.data(), A.size(), &da));
+    TKV_RC_TRY(upload(c, WS_W, Wt.data(), Wt.size(), &dw));
+    TKV_RC_TRY(ctx_workspace(c, WS_Y, (size_t)(m * n), &dy));
+    QLinearParams q;
+    q.zpa = (int32_t)zpa;
+    q.zpw = (int32_t)zpw;
+    q.zpy = (int32_t)zpy;
+    q.mult = qlinear_mult(sa, sw, sy, recipe);
+    TKV_RC_TRY(launch_gemm_qlinear(c, static_cast<int8_t*>(da), static_cast<int8_t*>(dw), m, n,
+                                   kk, q, static_cast<int8_t*>(dy)));
+    std::vector<int8_t> out((size_t)(m * n));
+    TKV_RC_TRY(download(c, out.data(), dy, out.size()));
+    const int64_t lim = m * n < ny ? m * n : ny;
+    for (int64_t i = 0; i < lim; i++) y[i] = out[(size_t)i];
+    return TKV_HIP_OK;
+}
+
 int32_t tkv_hip_quantize_linear(const float* x, int64_t nx, const float* scales, int64_t n_scales,
                                 int64_t zero_point, int64_t outer, int64_t dim, int64_t inner,
                                 int32_t* y) {
@@ -564,6 +632,21 @@ int32_t tkv_hip_dev_matmul_int8(int64_t ctx, const int8_t* a, const int8_t* w, i
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
     return launch_gemm_i8(c, a, w, m, n, k, ep, y);
+}
+
+int32_t tkv_hip_dev_qlinear_matmul(int64_t ctx, const int8_t* a, float sa, int32_t zpa,
+                                   const int8_t* w, float sw, int32_t zpw, float sy, int32_t zpy,
+                                   int8_t* y, int64_t m, int64_t n, int64_t k, int32_t recipe) {
+    TKV_RC_TRY(check_recipe(recipe));
+    if (m < 0 || n < 0 || k <= 0) return set_error(TKV_HIP_BAD_ARG, "bad QLinearMatMul sizes");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    QLinearParams q;
+    q.zpa = zpa;
+    q.zpw = zpw;
+    q.zpy = zpy;
+    q.mult = qlinear_mult(sa, sw, sy, recipe);
+    return launch_gemm_qlinear(c, a, w, m, n, k, q, y);
 }
 
 int32_t tkv_hip_dev_matmul_int8_accum(int64_t ctx, const int8_t* a, const int8_t* w, int64_t m,

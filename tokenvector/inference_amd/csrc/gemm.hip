@@ -135,6 +135,7 @@ __device__ __forceinline__ void load_operands(const float* __restrict__ sa_ptr, 
 
 template <int MODE, int RECIPE, bool ROWS>
 struct EpiI8 {
+    static constexpr bool kOut32 = true;  // 32-bit outputs (deferrable stores)
     const float* scale_a;
     int64_t scale_a_stride;
     float scale_w;
@@ -228,6 +229,7 @@ struct EpiI8 {
 // exact (a power of two undoing the operand pre-scale).
 template <bool SCALED, bool ROWS>
 struct EpiF8 {
+    static constexpr bool kOut32 = true;
     const float* scale_a;  // used when SCALED (extension epilogue)
     int64_t scale_a_stride;
     const float* scales_w;
@@ -280,6 +282,80 @@ struct EpiF8 {
                     for (int r = 0; r < 16; r++) out[i][j][r] = value(i, j, r);
         });
     }
+};
+
+// QLinearMatMul requantizing epilogue (session.tkv:2016-2058), int8 out:
+//   acc = sum_k (a - zpa)(w - zpw)
+//       = sum_k a w - zpw * ra[m] - zpa * cw[n] + K * zpa * zpw   (exact, int64)
+//   y   = clamp(rne(fl64(acc * mult)) + zpy, -128, 127)
+// with ra / cw the row sums of A and W (the node's B transposed) and mult
+// the host-computed multiplier.  The launcher keeps |zp| <= 2^15 and K < 2^17,
+// so every term and partial sum is an integer below 2^53: the correction is
+// exact in f64 (cheaper than int64 products), and the product with mult
+// rounds once, as the reference's acc * mult does.
+struct EpiQL {
+    static constexpr bool kOut32 = false;  // int8 outputs: stored at the tile's end
+    const int32_t* row_sums;  // [M]
+    const int32_t* col_sums;  // [N]
+    int32_t zpa, zpw, zpy;
+    int64_t kzz;              // K * zpa * zpw
+    double mult;
+
+    template <class C>
+    struct Operands {
+        int32_t ra[C::TM][16];
+        int32_t cw[C::TN];
+    };
+
+    // Rows past M read row M - 1 and columns past N column N - 1 (never stored).
+    template <class C>
+    __device__ __forceinline__ Operands<C> load(int m0, int n0, int M, int N) const {
+        Operands<C> o;
+        const int lane = threadIdx.x & 63, wave = wave_id();
+        const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * C::WTM + i * 32 + acc_row(r, khalf);
+                o.ra[i][r] = row_sums[row < M ? row : M - 1];
+            }
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int col = n0 + wn * C::WTN + j * 32 + (lane & 31);
+            o.cw[j] = col_sums[col < N ? col : N - 1];
+        }
+        return o;
+    }
+
+    template <class C, class P, class F>
+    __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
+                                               const Operands<C>& o, F&& f) const {
+        const double kzz_d = (double)kzz, zpw_d = (double)zpw, zpa_d = (double)zpa;
+        f([&](int i, int j, int r) {
+            const double row = kzz_d - zpw_d * (double)o.ra[i][r];
+            const double a = ((double)pin(acc[i][j][r]) + row) - zpa_d * (double)o.cw[j];
+            double v = __builtin_rint(a * mult);
+            if (v != v) v = 0.0;
+            v = v + (double)zpy;
+            v = v < -128.0 ? -128.0 : (v > 127.0 ? 127.0 : v);
+            return (uint32_t)(int32_t)v;
+        });
+    }
+
+    template <class C, class P, int P0 = 0, int NP = C::TM * 16>
+    __device__ __forceinline__ void store(const typename P::Acc (&acc)[C::TM][C::TN],
+                                          const Operands<C>& o, int m0, int n0, int M, int N,
+                                          void* __restrict__ Y) const {
+        with_value<C, P>(acc, o, [&](auto&& value) {
+            write_tile<C, P0, NP>(static_cast<int8_t*>(Y), m0, n0, M, N, value);
+        });
+    }
+
+    template <class C, class P>
+    __device__ __forceinline__ void values(const typename P::Acc (&)[C::TM][C::TN],
+                                           const Operands<C>&,
+                                           uint32_t (&)[C::TM][C::TN][16]) const {}
 };
 
 // Persistent workgroups: workgroup b owns tiles b, b + G, b + 2G, ... (G =
@@ -436,7 +512,7 @@ __global__ __launch_bounds__(C::THREADS, C::MIN_WAVES_EU) void k_gemm_ws(const u
     for (int j = 0; j < C::TN; j++) w_row[j] = wn * C::WTN + j * 32 + (lane & 31);
     barrier();
     int s = 0;
-    if constexpr (!C::DEFER) {
+    if constexpr (!C::DEFER || !E::kOut32) {
         for (int ti = 0; ti < my_tiles; ti++) {
             const int t = xcd_tile(b + ti * G, tiles);
             const int m0 = (t / tiles_n) * C::BM, n0 = (t % tiles_n) * C::BN;
@@ -719,6 +795,27 @@ static int check_sizes(int64_t m, int64_t n, int64_t k, const char* what) {
 }  // namespace gemm
 
 int64_t gemm_k_align() { return gemm::kBK; }
+
+// QLinearMatMul: row sums of A and W first (zero padding past k adds
+// nothing), then the GEMM with the requantizing epilogue.
+int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n,
+                        int64_t k, const QLinearParams& q, int8_t* y) {
+    if (m <= 0 || n <= 0) return TKV_HIP_OK;
+    TKV_RC_TRY(gemm::check_sizes(m, n, k, "QLinearMatMul"));
+    auto small = [](int32_t v) { return v >= -32768 && v <= 32767; };
+    if (!small(q.zpa) || !small(q.zpw))
+        return set_error(TKV_HIP_UNSUPPORTED, "QLinearMatMul: input zero points beyond +-2^15");
+    void* sums;
+    TKV_RC_TRY(ctx_workspace(c, 8, (size_t)(m + n) * 4, &sums));
+    int32_t* ra = static_cast<int32_t*>(sums);
+    TKV_RC_TRY(launch_row_sums_i8(c, a, m, w, n, k, ra));
+    const void *pa = a, *pw = w;
+    int64_t ldk;
+    TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));
+    gemm::EpiQL e{ra, ra + m, q.zpa, q.zpw, q.zpy, k * (int64_t)q.zpa * (int64_t)q.zpw, q.mult};
+    return gemm::launch_any<gemm::PolicyI8>(c, static_cast<const uint8_t*>(pa),
+                                            static_cast<const uint8_t*>(pw), m, n, ldk, e, y);
+}
 
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
                    const I8Epilogue& e, void* y) {

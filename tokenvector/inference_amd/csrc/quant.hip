@@ -759,6 +759,54 @@ int launch_fp8_decode(Ctx* c, const void* q, bool in_i32, int64_t n, float* y) {
 }
 
 // ---------------------------------------------------------------------------
+// Row sums of int8 codes (the zero-point corrections of QLinearMatMul): rows
+// [0, rows_a) of A, then rows [0, rows_w) of W, in one launch; one wave64 per
+// row, four 32-bit loads (16 codes) per lane in flight where the rows allow.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int sum4(uint32_t v) {
+    return (int)(int8_t)(v & 0xff) + (int)(int8_t)((v >> 8) & 0xff) +
+           (int)(int8_t)((v >> 16) & 0xff) + (int)(int8_t)(v >> 24);
+}
+
+__global__ __launch_bounds__(kBlock) void k_row_sums_i8(const int8_t* __restrict__ a,
+                                                        int64_t rows_a,
+                                                        const int8_t* __restrict__ w,
+                                                        int64_t rows_w, int64_t cols, int vec,
+                                                        int32_t* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    if (r >= rows_a + rows_w) return;
+    const int8_t* __restrict__ row = r < rows_a ? a + r * cols : w + (r - rows_a) * cols;
+    int sum = 0;
+    if (vec) {
+        const uint32_t* __restrict__ r4 = reinterpret_cast<const uint32_t*>(row);
+        const int64_t n4 = cols / 4;
+        int64_t c4 = lane;
+        for (; c4 + 3 * 64 < n4; c4 += 4 * 64) {
+            const uint32_t v0 = r4[c4], v1 = r4[c4 + 64], v2 = r4[c4 + 128], v3 = r4[c4 + 192];
+            sum += sum4(v0) + sum4(v1) + sum4(v2) + sum4(v3);
+        }
+        for (; c4 < n4; c4 += 64) sum += sum4(r4[c4]);
+    } else {
+        for (int64_t c = lane; c < cols; c += 64) sum += row[c];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) out[r] = sum;
+}
+
+int launch_row_sums_i8(Ctx* c, const int8_t* a, int64_t rows_a, const int8_t* w, int64_t rows_w,
+                       int64_t cols, int32_t* out) {
+    const int64_t rows = rows_a + rows_w;
+    if (rows <= 0) return TKV_HIP_OK;
+    const int vec = (cols % 4 == 0 && aligned(a, 4) && aligned(w, 4)) ? 1 : 0;
+    hipLaunchKernelGGL(k_row_sums_i8, dim3((unsigned)ceil_div(rows, kBlock / 64)), dim3(kBlock),
+                       0, c->stream, a, rows_a, w, rows_w, cols, vec, out);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Code layout conversions for the host mirrors: int32 codes (List<int>) to
 // packed int8 rows with a padded leading dimension, and back.  code_bias
 // +128 maps the reference's FP8 codes to raw e4m3 bytes.

@@ -55,7 +55,7 @@ struct Ctx {
     RedPartial* partials = nullptr;
     tkv_hip_qparams_dev* params = nullptr;  // 64 slots of per-call params
     // grow-only workspaces
-    static constexpr int kSlots = 8;
+    static constexpr int kSlots = 10;
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
 };
@@ -134,6 +134,18 @@ int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t 
 int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                    int64_t k, const float* scale_a, int64_t scale_a_stride,
                    const float* scales_w, const float* bias, float* y, bool fast);
+// QLinearMatMul (session.tkv:1992-2071) on packed codes: A [m,k], W [n,k]
+// (the node's B transposed), both with row stride k; y int8 [m,n].
+struct QLinearParams {
+    int32_t zpa, zpw, zpy;
+    double mult;  // fl64(sa * sw / sy) (primary) or the f32 chain widened
+};
+int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n,
+                        int64_t k, const QLinearParams& q, int8_t* y);
+// out[r] = sum of row r's `cols` int8 codes: rows of A [rows_a, cols], then
+// rows of W [rows_w, cols] (both compact).
+int launch_row_sums_i8(Ctx* c, const int8_t* a, int64_t rows_a, const int8_t* w, int64_t rows_w,
+                       int64_t cols, int32_t* out);
 // K granularity of the GEMM main loop: operands whose row stride is a
 // multiple of it (and 16-byte aligned) run without repacking.
 int64_t gemm_k_align();

@@ -208,6 +208,13 @@ def matmul_int8(ctx, a, w, m, n, k, scale_a, scale_a_stride, scale_w, scales_w, 
                                                   _vp(y), int(recipe)))
 
 
+def qlinear_matmul(ctx, a, sa, zpa, w, sw, zpw, sy, zpy, y, m, n, k, recipe: int = 0) -> None:
+    """QLinearMatMul on int8 codes: a [m,k], w [n,k] (B transposed), y int8 [m,n]."""
+    _lib.check(_lib.lib().tkv_hip_dev_qlinear_matmul(
+        ctx.handle, _vp(a), float(sa), int(zpa), _vp(w), float(sw), int(zpw), float(sy),
+        int(zpy), _vp(y), int(m), int(n), int(k), int(recipe)))
+
+
 def matmul_int8_accum(ctx, a, w, m, n, k, acc) -> None:
     _lib.check(_lib.lib().tkv_hip_dev_matmul_int8_accum(ctx.handle, _vp(a), _vp(w), int(m), int(n),
                                                         int(k), _vp(acc)))

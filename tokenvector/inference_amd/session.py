@@ -7,6 +7,7 @@ and dispatches exactly as ``ExecutionNode.execute`` does for:
     OperatorType_QuantizedGemm (21)          session.tkv:678-697
     OperatorType_QuantizeLinear (63)         session.tkv:1896-1953
     OperatorType_DequantizeLinear (64)       session.tkv:1955-1990
+    OperatorType_QLinearMatMul (65)          session.tkv:1992-2071
     OperatorType_MatMulInteger (78)          session.tkv:2789-2851
     OperatorType_DynamicQuantizeLinear (79)  session.tkv:2853-2901
 
@@ -26,6 +27,7 @@ from . import _lib
 OperatorType_QuantizedGemm = 21
 OperatorType_QuantizeLinear = 63
 OperatorType_DequantizeLinear = 64
+OperatorType_QLinearMatMul = 65
 OperatorType_MatMulInteger = 78
 OperatorType_DynamicQuantizeLinear = 79
 
@@ -85,6 +87,8 @@ class QuantNode:
             return [self._dequantize_linear(inputs)]
         if op == OperatorType_MatMulInteger:
             return [self._matmul_integer(inputs, out_shapes[0])]
+        if op == OperatorType_QLinearMatMul:
+            return [self._qlinear_matmul(inputs, out_shapes[0])]
         if op == OperatorType_DynamicQuantizeLinear:
             return list(self._dynamic_quantize_linear(inputs))
         raise NotImplementedError(f"op {op} is not a quantized node")
@@ -151,6 +155,28 @@ class QuantNode:
         y = np.zeros(max(ny, 1), np.int64)
         _lib.check(_lib.lib().tkv_hip_matmul_integer(_p(a), a.size, _p(b), b.size, _p(y), ny,
                                                      m, n, k))
+        return y[:ny]
+
+    def _qlinear_matmul(self, inputs, y_shape, recipe: int = 0) -> np.ndarray:
+        """Inputs a, a_scale, a_zero_point, b, b_scale, b_zero_point, y_scale,
+        y_zero_point (session.tkv:1994-2014): scalars are the first element of
+        a float tensor, zero points truncated to integers by int()."""
+        (a, a_shape), (b, b_shape) = inputs[0], inputs[3]
+        a, b = _i32(a), _i32(b)
+
+        def scalar(t):
+            return np.float32(np.asarray(t[0], dtype=np.float32).reshape(-1)[0])
+
+        sa, sw, sy = scalar(inputs[1]), scalar(inputs[4]), scalar(inputs[6])
+        zpa, zpw, zpy = int(scalar(inputs[2])), int(scalar(inputs[5])), int(scalar(inputs[7]))
+        m = int(a_shape[0]) if len(a_shape) > 1 else 1
+        k = int(a_shape[1]) if len(a_shape) > 1 else _count(a_shape)
+        n = int(b_shape[1]) if len(b_shape) > 1 else _count(b_shape)
+        ny = _count(y_shape)
+        y = np.zeros(max(ny, 1), np.int32)
+        _lib.check(_lib.lib().tkv_hip_qlinear_matmul(
+            _p(a), a.size, float(sa), zpa, _p(b), b.size, float(sw), zpw, float(sy), zpy, _p(y),
+            ny, m, n, k, int(recipe)))
         return y[:ny]
 
     def _dynamic_quantize_linear(self, inputs):
