@@ -416,6 +416,18 @@ def test_qlinear_matmul_node(hip):
             assert np.array_equal(y, want), (m, n, k, recipe)
             if ci >= 3 and k > 0:
                 assert np.unique(y).size > 50, "requantized codes should spread over the range"
+    # zero points too large for the int32 fast path (exact f64 correction), and
+    # an f32-chain multiplier that overflows to inf (alternate recipe)
+    m, n, k = 40, 70, 300
+    a = RNG.integers(-128, 128, m * k).astype(np.int32)
+    b = RNG.integers(-128, 128, k * n).astype(np.int32)
+    for (sa, zpa, sw, zpw, sy, zpy) in [(0.01, 20000, 0.02, -15000, 2.0e6, 3),
+                                         (1e30, 2, 1e30, -1, 1.0, -5)]:
+        for recipe in (0, 1):
+            (y,) = [node._qlinear_matmul([(a, [m, k]), one(sa), one(zpa), (b, [k, n]), one(sw),
+                                          one(zpw), one(sy), one(zpy)], [m * n], recipe)]
+            want = O.qlinear_matmul(a, sa, zpa, b, sw, zpw, sy, zpy, m * n, m, n, k, recipe)
+            assert np.array_equal(y, want), (zpa, zpw, sa, recipe)
 
 
 def test_qdq_nodes(hip):

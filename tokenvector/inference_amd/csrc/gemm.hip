@@ -13,6 +13,7 @@
 //
 // Data movement and tiling live in gemm_tile.h.  All arithmetic here is
 // compiled with -ffp-contract=off.
+#include <cmath>
 #include <cstdlib>
 #include <type_traits>
 #include <utility>
@@ -286,13 +287,21 @@ struct EpiF8 {
 
 // QLinearMatMul requantizing epilogue (session.tkv:2016-2058), int8 out:
 //   acc = sum_k (a - zpa)(w - zpw)
-//       = sum_k a w - zpw * ra[m] - zpa * cw[n] + K * zpa * zpw   (exact, int64)
+//       = sum_k a w - zpw * ra[m] - zpa * cw[n] + K * zpa * zpw
 //   y   = clamp(rne(fl64(acc * mult)) + zpy, -128, 127)
 // with ra / cw the row sums of A and W (the node's B transposed) and mult
-// the host-computed multiplier.  The launcher keeps |zp| <= 2^15 and K < 2^17,
-// so every term and partial sum is an integer below 2^53: the correction is
-// exact in f64 (cheaper than int64 products), and the product with mult
-// rounds once, as the reference's acc * mult does.
+// the host-computed multiplier; fl64(acc) is exact, so the product rounds
+// once, as the reference's acc * mult does.
+//   I32: the launcher has checked K (128 + |zpa|)(128 + |zpw|) < 2^31, so the
+//        true acc fits int32 and two's-complement int32 arithmetic yields it
+//        exactly whatever the intermediate wraps; the per-row term
+//        K zpa zpw - zpw ra and the per-column term zpa cw are formed once per
+//        tile.  The rounded product converts with saturation (NaN -> 0, as the
+//        reference's saturating int()) before zpy is added and the result
+//        clamped.
+//   else: the same correction in f64, exact because the launcher keeps
+//        |zp| <= 2^15 and K < 2^17 (every term below 2^53).
+template <bool I32>
 struct EpiQL {
     static constexpr bool kOut32 = false;  // int8 outputs: stored at the tile's end
     const int32_t* row_sums;  // [M]
@@ -303,8 +312,8 @@ struct EpiQL {
 
     template <class C>
     struct Operands {
-        int32_t ra[C::TM][16];
-        int32_t cw[C::TN];
+        int32_t rt[C::TM][16];  // I32: K zpa zpw - zpw ra; else ra
+        int32_t ct[C::TN];      // I32: zpa cw; else cw
     };
 
     // Rows past M read row M - 1 and columns past N column N - 1 (never stored).
@@ -318,12 +327,14 @@ struct EpiQL {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * C::WTM + i * 32 + acc_row(r, khalf);
-                o.ra[i][r] = row_sums[row < M ? row : M - 1];
+                const int32_t ra = row_sums[row < M ? row : M - 1];
+                o.rt[i][r] = I32 ? (int32_t)((uint32_t)kzz - (uint32_t)zpw * (uint32_t)ra) : ra;
             }
 #pragma unroll
         for (int j = 0; j < C::TN; j++) {
             const int col = n0 + wn * C::WTN + j * 32 + (lane & 31);
-            o.cw[j] = col_sums[col < N ? col : N - 1];
+            const int32_t cw = col_sums[col < N ? col : N - 1];
+            o.ct[j] = I32 ? (int32_t)((uint32_t)zpa * (uint32_t)cw) : cw;
         }
         return o;
     }
@@ -331,16 +342,30 @@ struct EpiQL {
     template <class C, class P, class F>
     __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
                                                const Operands<C>& o, F&& f) const {
-        const double kzz_d = (double)kzz, zpw_d = (double)zpw, zpa_d = (double)zpa;
-        f([&](int i, int j, int r) {
-            const double row = kzz_d - zpw_d * (double)o.ra[i][r];
-            const double a = ((double)pin(acc[i][j][r]) + row) - zpa_d * (double)o.cw[j];
-            double v = __builtin_rint(a * mult);
-            if (v != v) v = 0.0;
-            v = v + (double)zpy;
-            v = v < -128.0 ? -128.0 : (v > 127.0 ? 127.0 : v);
-            return (uint32_t)(int32_t)v;
-        });
+        if constexpr (I32) {
+            // clamp(rint(p) + zpy) == clamp(rint(p), -128 - zpy, 127 - zpy) + zpy for an
+            // integer zpy; the launcher takes this path only for a finite mult, so p
+            // is never NaN
+            const double lo = -128.0 - (double)zpy, hi = 127.0 - (double)zpy;
+            f([&](int i, int j, int r) {
+                const int32_t a = (int32_t)((uint32_t)pin(acc[i][j][r]) + (uint32_t)o.rt[i][r] -
+                                            (uint32_t)o.ct[j]);
+                double v = __builtin_rint((double)a * mult);
+                v = v < lo ? lo : (v > hi ? hi : v);
+                return (uint32_t)((int32_t)v + zpy);
+            });
+        } else {
+            const double kzz_d = (double)kzz, zpw_d = (double)zpw, zpa_d = (double)zpa;
+            f([&](int i, int j, int r) {
+                const double row = kzz_d - zpw_d * (double)o.rt[i][r];
+                const double a = ((double)pin(acc[i][j][r]) + row) - zpa_d * (double)o.ct[j];
+                double v = __builtin_rint(a * mult);
+                if (v != v) v = 0.0;
+                v = v + (double)zpy;
+                v = v < -128.0 ? -128.0 : (v > 127.0 ? 127.0 : v);
+                return (uint32_t)(int32_t)v;
+            });
+        }
     }
 
     template <class C, class P, int P0 = 0, int NP = C::TM * 16>
@@ -812,9 +837,16 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
     const void *pa = a, *pw = w;
     int64_t ldk;
     TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));
-    gemm::EpiQL e{ra, ra + m, q.zpa, q.zpw, q.zpy, k * (int64_t)q.zpa * (int64_t)q.zpw, q.mult};
-    return gemm::launch_any<gemm::PolicyI8>(c, static_cast<const uint8_t*>(pa),
-                                            static_cast<const uint8_t*>(pw), m, n, ldk, e, y);
+    const int64_t kzz = k * (int64_t)q.zpa * (int64_t)q.zpw;
+    const int64_t bound = k * (128 + (int64_t)std::abs(q.zpa)) * (128 + (int64_t)std::abs(q.zpw));
+    const auto* ua = static_cast<const uint8_t*>(pa);
+    const auto* uw = static_cast<const uint8_t*>(pw);
+    if (bound < (1ll << 31) && std::isfinite(q.mult))
+        return gemm::launch_any<gemm::PolicyI8>(
+            c, ua, uw, m, n, ldk, gemm::EpiQL<true>{ra, ra + m, q.zpa, q.zpw, q.zpy, kzz, q.mult},
+            y);
+    return gemm::launch_any<gemm::PolicyI8>(
+        c, ua, uw, m, n, ldk, gemm::EpiQL<false>{ra, ra + m, q.zpa, q.zpw, q.zpy, kzz, q.mult}, y);
 }
 
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
