@@ -108,6 +108,22 @@ int32_t tkv_hip_event_elapsed_ms(int64_t ev_start, int64_t ev_end, float* ms_out
 int32_t tkv_hip_calibrate_minmax(const float* data, int64_t n, int32_t symmetric,
                                  float* scale, int64_t* zero_point, float* min_val,
                                  float* max_val);
+/* calibrate_kl(data, num_bins, target_bins) -> QuantParams   engine.tkv:42-123
+ * (TensorRT-style KL over a num_bins histogram of |x|; num_bins <= 4096). */
+int32_t tkv_hip_calibrate_kl(const float* data, int64_t n, int64_t num_bins,
+                             int64_t target_bins, float* scale, int64_t* zero_point,
+                             float* min_val, float* max_val);
+/* calibrate_percentile(data, percentile, symmetric) -> QuantParams
+ * engine.tkv:126-162; TKV_HIP_BAD_ARG where the reference raises
+ * ValueError (percentile outside (0, 100]). */
+int32_t tkv_hip_calibrate_percentile(const float* data, int64_t n, float percentile,
+                                     int32_t symmetric, float* scale, int64_t* zero_point,
+                                     float* min_val, float* max_val);
+/* calibrate_mse(data, num_candidates) -> QuantParams   engine.tkv:165-197
+ * (num_candidates <= 4096; below 4 reads as 4, as in the reference). */
+int32_t tkv_hip_calibrate_mse(const float* data, int64_t n, int64_t num_candidates,
+                              float* scale, int64_t* zero_point, float* min_val,
+                              float* max_val);
 /* calibrate_per_channel_minmax(data, rows, cols, symmetric) engine.tkv:202-213;
  * outputs one QuantParams per row as four arrays (zero_points/min/max may be
  * NULL).  BAD_ARG where the .tkv raises (rows/cols <= 0, short data). */
@@ -210,6 +226,15 @@ int32_t tkv_hip_dynamic_quantize_linear(const float* x, int64_t nx, int32_t* y,
  * engine.tkv:13-36 */
 int32_t tkv_hip_dev_calibrate_minmax(int64_t ctx, const float* x, int64_t n,
                                      int32_t symmetric, tkv_hip_qparams_dev* params);
+/* The heavier calibrators on device data (engine.tkv:42-197), one
+ * tkv_hip_qparams_dev each, no host sync; n > 0. */
+int32_t tkv_hip_dev_calibrate_kl(int64_t ctx, const float* x, int64_t n, int64_t num_bins,
+                                 int64_t target_bins, tkv_hip_qparams_dev* params);
+int32_t tkv_hip_dev_calibrate_percentile(int64_t ctx, const float* x, int64_t n,
+                                         float percentile, int32_t symmetric,
+                                         tkv_hip_qparams_dev* params);
+int32_t tkv_hip_dev_calibrate_mse(int64_t ctx, const float* x, int64_t n,
+                                  int64_t num_candidates, tkv_hip_qparams_dev* params);
 /* Per-row absmax scales (symmetric calibrate_per_channel_minmax, engine.tkv:202-213):
  * scales[r] = fl32(max(|x[r,:]|, 1e-8) / 127). */
 int32_t tkv_hip_dev_calibrate_rows(int64_t ctx, const float* x, int64_t rows, int64_t cols,

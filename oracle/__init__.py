@@ -78,6 +78,9 @@ def _declare(L: C.CDLL) -> None:
         "tkvo_fp8_e5m2_decode": (F32, [I64]),
         "tkvo_quant_identity": (_QP, []),
         "tkvo_calibrate_minmax": (_QP, [P, I64, I32]),
+        "tkvo_calibrate_kl": (_QP, [P, I64, I64, I64]),
+        "tkvo_calibrate_percentile": (_QP, [P, I64, F32, I32, P]),
+        "tkvo_calibrate_mse": (_QP, [P, I64, I64]),
         "tkvo_calibrate_per_channel_minmax": (I32, [P, I64, I64, I64, I32, P]),
         "tkvo_quantize_int8_symmetric": (I32, [P, I64, P, F32, I32]),
         "tkvo_dequantize_int8_symmetric": (I32, [P, I64, P, F32]),
@@ -203,6 +206,27 @@ def quant_identity() -> QuantParams:
 def calibrate_minmax(data, symmetric: int = 1) -> QuantParams:
     x = _f32(data)
     return QuantParams._from(lib().tkvo_calibrate_minmax(_p(x), x.size, int(symmetric)))
+
+
+def calibrate_kl(data, num_bins: int = 2048, target_bins: int = 128) -> QuantParams:
+    x = _f32(data)
+    return QuantParams._from(lib().tkvo_calibrate_kl(_p(x), x.size, int(num_bins),
+                                                     int(target_bins)))
+
+
+def calibrate_percentile(data, percentile: float = 99.99, symmetric: int = 1) -> QuantParams:
+    x = _f32(data)
+    err = C.c_int32(0)
+    r = lib().tkvo_calibrate_percentile(_p(x), x.size, float(np.float32(percentile)),
+                                        int(symmetric), C.byref(err))
+    if err.value:
+        raise ValueError("percentile must be in (0, 100]")
+    return QuantParams._from(r)
+
+
+def calibrate_mse(data, num_candidates: int = 50) -> QuantParams:
+    x = _f32(data)
+    return QuantParams._from(lib().tkvo_calibrate_mse(_p(x), x.size, int(num_candidates)))
 
 
 def calibrate_per_channel_minmax(data, rows: int, cols: int, symmetric: int = 1):

@@ -275,6 +275,172 @@ tkvo_qparams tkvo_calibrate_minmax(const float* data, int64_t n, int32_t symmetr
     return p;
 }
 
+/* |x| maximum as the reference's loops keep it (f64 local from 0.0; NaN
+ * never compares greater). */
+static double absmax_f64(const float* data, int64_t n) {
+    double am = 0.0;
+    for (int64_t i = 0; i < n; i++) {
+        double a = fabs((double)data[i]);
+        if (a > am) am = a;
+    }
+    return am;
+}
+
+static tkvo_qparams sym_params(double thr) {
+    tkvo_qparams p;
+    p.scale = (float)(thr / 127.0);
+    p.zero_point = 0;
+    p.min_val = (float)(-thr);
+    p.max_val = (float)thr;
+    return p;
+}
+
+/* engine.tkv:42-123.  Locals without annotation are f64; hist[] holds
+ * integers; p / q are f64 lists; `log` is the runtime's natural log (libm).
+ * bin = int(|x| / bw): truncation with the saturating conversion (NaN -> 0). */
+tkvo_qparams tkvo_calibrate_kl(const float* data, int64_t n, int64_t num_bins,
+                               int64_t target_bins) {
+    if (n == 0) return tkvo_quant_identity();
+    double am = absmax_f64(data, n);
+    if (am < 0.00000001) return tkvo_calibrate_minmax(data, n, 1);
+    int64_t* hist = (int64_t*)calloc((size_t)num_bins, sizeof(int64_t));
+    double* p = (double*)calloc((size_t)num_bins, sizeof(double));
+    double* q = (double*)calloc((size_t)num_bins, sizeof(double));
+    double bw = am / (double)num_bins;
+    for (int64_t i = 0; i < n; i++) {
+        int64_t b = net_to_i64(fabs((double)data[i]) / bw);
+        if (b >= num_bins) b = num_bins - 1;
+        hist[b] = hist[b] + 1;
+    }
+    double total = 0.0;
+    for (int64_t i = 0; i < num_bins; i++) total = total + (double)hist[i];
+    if (total == 0) {
+        free(hist); free(p); free(q);
+        return tkvo_calibrate_minmax(data, n, 1);
+    }
+    int64_t best_bin = num_bins;
+    double best_kl = 1e45;
+    for (int64_t th = target_bins; th <= num_bins; th += 16) {
+        double s = 0.0;
+        for (int64_t i = 0; i < th; i++) {
+            p[i] = (double)hist[i];
+            s = s + (double)hist[i];
+        }
+        for (int64_t i = th; i < num_bins; i++) {
+            p[th - 1] = p[th - 1] + (double)hist[i];
+            s = s + (double)hist[i];
+        }
+        if (s != 0) {
+            for (int64_t i = 0; i < th; i++) p[i] = p[i] / s;
+            int64_t per = th / target_bins;
+            if (per >= 1) {
+                for (int64_t i = 0; i < th; i++) q[i] = 0.0;
+                for (int64_t b = 0; b < target_bins; b++) {
+                    int64_t start = b * per;
+                    int64_t end = (b == target_bins - 1) ? th : start + per;
+                    double mass = 0.0;
+                    for (int64_t i = start; i < end; i++) mass = mass + p[i];
+                    int64_t span = end - start;
+                    if (span < 1) span = 1;
+                    double share = mass / (double)span;
+                    for (int64_t i = start; i < end; i++) q[i] = share;
+                }
+                double kl = 0.0;
+                for (int64_t i = 0; i < th; i++)
+                    if (p[i] > 0.000000000001 && q[i] > 0.000000000001)
+                        kl = kl + p[i] * log(p[i] / q[i]);
+                if (kl < best_kl) {
+                    best_kl = kl;
+                    best_bin = th;
+                }
+            }
+        }
+    }
+    free(hist); free(p); free(q);
+    return sym_params((double)best_bin * bw);
+}
+
+static int cmp_f32(const void* a, const void* b) {
+    float x = *(const float*)a, y = *(const float*)b;
+    return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+/* engine.tkv:126-162.  percentile is an f32 parameter, _p100 an f64 local:
+ * idx = int(min(n - 1, (f64)percentile / 100.0 * n)). */
+tkvo_qparams tkvo_calibrate_percentile(const float* data, int64_t n, float percentile,
+                                       int32_t symmetric, int32_t* err) {
+    *err = 0;
+    if (n == 0) return tkvo_quant_identity();
+    if (percentile <= 0.0f || percentile > 100.0f) {
+        *err = 1;
+        return tkvo_quant_identity();
+    }
+    float* ab = (float*)malloc((size_t)n * sizeof(float));
+    for (int64_t i = 0; i < n; i++) ab[i] = fabsf(data[i]);
+    qsort(ab, (size_t)n, sizeof(float), cmp_f32);
+    int64_t nab = n - 1;
+    if (nab < 0) nab = 0;
+    double t = (double)percentile / 100.0 * (double)n;
+    double lim = (double)nab < t ? (double)nab : t;
+    int64_t idx = net_to_i64(lim);
+    double clip = ab[idx];
+    free(ab);
+    if (clip <= 0.00000001) clip = 0.00000001;
+    if (symmetric) return sym_params(clip);
+    double mn = data[0], mx = data[0];
+    for (int64_t i = 1; i < n; i++) {
+        double v = data[i];
+        if (v < -clip) v = -clip;
+        if (v > clip) v = clip;
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+    }
+    if (fabs(mx - mn) < 0.00000001) mx = mn + 0.00000001;
+    double scale = (mx - mn) / 255.0;
+    double z = net_round(-mn / scale);
+    if (z != z) z = 0.0;
+    z = z - 128.0;
+    tkvo_qparams p;
+    p.scale = (float)scale;
+    p.zero_point = z < -128.0 ? -128 : (z > 127.0 ? 127 : (int64_t)z);
+    p.min_val = (float)mn;
+    p.max_val = (float)mx;
+    return p;
+}
+
+/* engine.tkv:165-197.  thr = am * c / num_candidates, scale = thr / 127,
+ * inv = 1 / scale, dq = clamp(int(round(cl * inv)), -127, 127) * scale, the
+ * squared errors summed in index order in f64. */
+tkvo_qparams tkvo_calibrate_mse(const float* data, int64_t n, int64_t num_candidates) {
+    if (n == 0) return tkvo_quant_identity();
+    if (num_candidates < 4) num_candidates = 4;
+    double am = absmax_f64(data, n);
+    if (am < 0.00000001) return tkvo_calibrate_minmax(data, n, 1);
+    double best_thr = am, best_mse = 1e45;
+    for (int64_t c = 1; c <= num_candidates; c++) {
+        double thr = am * (double)c / (double)num_candidates;
+        double scale = thr / 127.0;
+        double inv = 1.0 / scale;
+        double mse = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            double cl = data[i];
+            if (cl < -thr) cl = -thr;
+            if (cl > thr) cl = thr;
+            int64_t qv = net_to_i64(net_round(cl * inv));
+            qv = clamp_i64(qv, -127, 127);
+            double dq = (double)qv * scale;
+            double d = (double)data[i] - dq;
+            mse = mse + d * d;
+        }
+        mse = mse / (double)n;
+        if (mse < best_mse) {
+            best_mse = mse;
+            best_thr = thr;
+        }
+    }
+    return sym_params(best_thr);
+}
+
 /* engine.tkv:202-213: A1 on a copy of each row. */
 int32_t tkvo_calibrate_per_channel_minmax(const float* data, int64_t len, int64_t rows,
                                           int64_t cols, int32_t symmetric,

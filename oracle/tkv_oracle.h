@@ -29,7 +29,9 @@
  *   - tkvo_matmul_int8_per_channel / _symmetric: whether the i64 * f32
  *     epilogue chains (matmul.tkv:5,14 and :29) run in f64 (primary) or f32;
  *   - tkvo_qlinear_matmul: whether mult = sa * sw / sy (session.tkv:2027)
- *     runs on f64 locals (primary) or as an f32 chain.
+ *     runs on f64 locals (primary) or as an f32 chain;
+ *   - tkvo_calibrate_kl: the natural log is the host libm's (the runtime's
+ *     Math.Log), pinned only through the selected threshold.
  * No reference test reaches a rounding tie that separates the readings, and
  * the reference compiler (tkvc, .NET) is not available to run.
  */
@@ -74,6 +76,16 @@ float tkvo_fp8_e5m2_decode(int64_t v);
 /* ---- engine.tkv ------------------------------------------------------ */
 tkvo_qparams tkvo_quant_identity(void);
 tkvo_qparams tkvo_calibrate_minmax(const float* data, int64_t n, int32_t symmetric);
+/* engine.tkv:42-123: TensorRT-style KL calibration over a num_bins histogram
+ * of |x|, thresholds target_bins, target_bins + 16, ..., num_bins. */
+tkvo_qparams tkvo_calibrate_kl(const float* data, int64_t n, int64_t num_bins,
+                               int64_t target_bins);
+/* engine.tkv:126-162: clip at the percentile of |x| (sorted); *err = 1 where
+ * the reference raises ValueError (percentile outside (0, 100]). */
+tkvo_qparams tkvo_calibrate_percentile(const float* data, int64_t n, float percentile,
+                                       int32_t symmetric, int32_t* err);
+/* engine.tkv:165-197: MSE grid search over num_candidates thresholds. */
+tkvo_qparams tkvo_calibrate_mse(const float* data, int64_t n, int64_t num_candidates);
 /* returns 0, or -4 for the ValueError cases of engine.tkv:203-206 */
 int32_t tkvo_calibrate_per_channel_minmax(const float* data, int64_t len, int64_t rows,
                                           int64_t cols, int32_t symmetric,

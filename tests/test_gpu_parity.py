@@ -88,6 +88,59 @@ def test_calibrate_per_channel(hip, rows, cols, sym):
         Q.calibrate_per_channel_minmax(w, rows + 1, cols)
 
 
+# heavier calibrators (engine.tkv:42-197): equal QuantParams fields.  KL and
+# percentile reproduce the reference's arithmetic bit for bit; the MSE search
+# sums per-block partials (another order than the reference's loop), so its
+# parity is the chosen threshold, exact away from candidates within rounding.
+CAL_SIZES = [1, 7, 1000, 65539, 786432, 8192 * 768]
+
+
+def _same_qp(a, b):
+    return a.zero_point == b.zero_point and _same_f32([a.scale, a.min_val, a.max_val],
+                                                     [b.scale, b.min_val, b.max_val])
+
+
+@pytest.mark.parametrize("n", CAL_SIZES)
+def test_calibrate_kl(hip, n):
+    say(f"calibrate_kl n={n}")
+    x = _x(n, 41 + n % 97, 1.0)
+    if n > 100:
+        x = O.add_outliers(x, 0.001, 3, 4, 20.0)
+    for bins, target in [(2048, 128), (512, 32), (64, 8), (4096, 4000)]:
+        g, o = Q.calibrate_kl(x, bins, target), O.calibrate_kl(x, bins, target)
+        assert _same_qp(g, o), (bins, target, g, o)
+    z = np.zeros(max(n, 2), np.float32)
+    assert _same_qp(Q.calibrate_kl(z), O.calibrate_kl(z))
+
+
+@pytest.mark.parametrize("n", CAL_SIZES)
+def test_calibrate_percentile(hip, n):
+    say(f"calibrate_percentile n={n}")
+    x = _x(n, 43 + n % 89, 1.0)
+    if n > 100:
+        x = O.add_outliers(x, 0.001, 3, 4, 20.0)
+    x[0] = np.float32(-30.0) if n > 1 else x[0]  # data[0] stays unclipped in the reference
+    for pct in (99.99, 50.0, 100.0, 0.5):
+        for sym in (1, 0):
+            g, o = Q.calibrate_percentile(x, pct, sym), O.calibrate_percentile(x, pct, sym)
+            assert _same_qp(g, o), (pct, sym, g, o)
+    with pytest.raises(ValueError):
+        Q.calibrate_percentile(x, 0.0)
+
+
+@pytest.mark.parametrize("n", [1, 7, 1000, 65539, 786432])
+def test_calibrate_mse(hip, n):
+    say(f"calibrate_mse n={n}")
+    x = _x(n, 47 + n % 83, 1.0)
+    if n > 100:
+        x = O.add_outliers(x, 0.001, 3, 4, 20.0)
+    for nc in (50, 4, 130):
+        g, o = Q.calibrate_mse(x, nc), O.calibrate_mse(x, nc)
+        assert _same_qp(g, o), (nc, g, o)
+    z = np.zeros(max(n, 2), np.float32)
+    assert _same_qp(Q.calibrate_mse(z), O.calibrate_mse(z))
+
+
 # ---------------------------------------------------------------------------
 # quantize / dequantize (config 2 shapes)
 # ---------------------------------------------------------------------------

@@ -383,6 +383,77 @@ def test_qlinear_matmul_bruteforce(recipe):
     assert not np.array_equal(np.rint(acc * 0.5), np.floor(acc * 0.5 + 0.5))
 
 
+# ---------------------------------------------------------------------------
+# heavier calibrators (engine.tkv:42-197)
+# ---------------------------------------------------------------------------
+
+def _calib_data(n, seed):
+    x = O.gi_noise(n, seed, 1.0)
+    return O.add_outliers(x, 0.01, seed + 1, seed + 2, 20.0) if n > 100 else x
+
+
+@pytest.mark.parametrize("n,bins,target", [(5000, 2048, 128), (20000, 512, 32), (3000, 64, 8)])
+def test_calibrate_kl_closed_form(n, bins, target):
+    """At th = target_bins every q equals p (per = 1 and the last block is the
+    merged tail itself), so KL = 0 exactly and no later candidate can beat it
+    on data whose tail bins differ: thr = target * max|x| / num_bins."""
+    x = _calib_data(n, 17)
+    am = float(np.max(np.abs(x.astype(np.float64))))
+    thr = target * (am / bins)
+    p = O.calibrate_kl(x, bins, target)
+    assert p.zero_point == 0
+    assert p.scale == np.float32(thr / 127.0)
+    assert p.min_val == np.float32(-thr) and p.max_val == np.float32(thr)
+    assert O.calibrate_kl(np.zeros(7, np.float32)) == O.calibrate_minmax(np.zeros(7, np.float32), 1)
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 1000, 50001])
+@pytest.mark.parametrize("pct", [99.99, 50.0, 100.0, 0.5])
+def test_calibrate_percentile_vs_numpy(n, pct):
+    """Clip = sorted |x| at int(min(n - 1, f64(pct) / 100 * n)) (numpy sort);
+    asymmetric min / max: data[0] unclipped, the rest clipped (numpy)."""
+    x = _calib_data(n, 23)
+    ab = np.sort(np.abs(x))
+    idx = int(min(n - 1, float(np.float32(pct)) / 100.0 * n))
+    clip = max(float(ab[idx]), 1e-8)
+    p = O.calibrate_percentile(x, pct, 1)
+    assert p.scale == np.float32(clip / 127.0) and p.max_val == np.float32(clip)
+    q = O.calibrate_percentile(x, pct, 0)
+    c = np.clip(x[1:].astype(np.float64), -clip, clip)
+    mn = min(float(x[0]), float(c.min())) if n > 1 else float(x[0])
+    mx = max(float(x[0]), float(c.max())) if n > 1 else float(x[0])
+    if abs(mx - mn) < 1e-8:
+        mx = mn + 1e-8
+    assert q.min_val == np.float32(mn) and q.max_val == np.float32(mx)
+    assert q.scale == np.float32((mx - mn) / 255.0)
+    assert q.zero_point == int(np.clip(np.rint(-mn / ((mx - mn) / 255.0)) - 128, -128, 127))
+    for bad in (0.0, -1.0, 100.5):
+        with pytest.raises(ValueError):
+            O.calibrate_percentile(x, bad)
+
+
+@pytest.mark.parametrize("n,cands", [(3000, 50), (800, 4), (20000, 17)])
+def test_calibrate_mse_argmin_vs_numpy(n, cands):
+    """The chosen threshold minimizes the quantization MSE among the
+    candidates, recomputed with numpy's vectorized arithmetic (a different
+    summation order: agreement holds away from near-ties)."""
+    x = _calib_data(n, 31).astype(np.float64)
+    am = float(np.max(np.abs(x)))
+    mses = []
+    for c in range(1, cands + 1):
+        thr = am * c / cands
+        scale = thr / 127.0
+        inv = 1.0 / scale
+        q = np.clip(np.rint(np.clip(x, -thr, thr) * inv), -127, 127)
+        mses.append(float(np.mean((x - q * scale) ** 2)))
+    best = int(np.argmin(mses)) + 1
+    srt = sorted(mses)
+    assert srt[1] - srt[0] > 1e-9 * srt[0], "test data must not produce a near-tie"
+    thr = am * best / cands
+    p = O.calibrate_mse(x.astype(np.float32), cands)
+    assert p.scale == np.float32(thr / 127.0) and p.max_val == np.float32(thr)
+
+
 def test_quantize_linear_per_tensor_and_axis():
     x = RNG.normal(0, 3, (2, 3, 4)).astype(np.float32)
     y = O.quantize_linear(x, [0.05], zero_point=3)

@@ -125,6 +125,71 @@ extern "C" {
 // Host-pointer mirrors
 // ===========================================================================
 
+}  // extern "C"
+
+namespace {
+
+// Host mirror of a heavier calibrator: n == 0 gives _quant_identity()
+// (engine.tkv:9-10), as each of them returns first.
+template <class F>
+int32_t host_calibrate(const float* data, int64_t n, float* scale, int64_t* zero_point,
+                       float* min_val, float* max_val, F&& launch) {
+    if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative length");
+    tkv_hip_qparams_dev p;
+    if (n == 0) {
+        p.scale = 1.0f;
+        p.zero_point = 0;
+        p.min_val = -3.4028234663852886e38f;
+        p.max_val = 3.4028234663852886e38f;
+    } else {
+        void* dx;
+        Ctx* c;
+        TKV_RC_TRY(begin_host(&c));
+        TKV_RC_TRY(upload(c, WS_IN, data, (size_t)n * 4, &dx));
+        TKV_RC_TRY(launch(c, static_cast<const float*>(dx), c->params));
+        TKV_RC_TRY(download(c, &p, c->params, sizeof(p)));
+    }
+    if (scale) *scale = p.scale;
+    if (zero_point) *zero_point = p.zero_point;
+    if (min_val) *min_val = p.min_val;
+    if (max_val) *max_val = p.max_val;
+    return TKV_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tkv_hip_calibrate_kl(const float* data, int64_t n, int64_t num_bins,
+                             int64_t target_bins, float* scale, int64_t* zero_point,
+                             float* min_val, float* max_val) {
+    return host_calibrate(data, n, scale, zero_point, min_val, max_val,
+                          [&](Ctx* c, const float* x, tkv_hip_qparams_dev* o) {
+                              return launch_calibrate_kl(c, x, n, num_bins, target_bins, o);
+                          });
+}
+
+int32_t tkv_hip_calibrate_percentile(const float* data, int64_t n, float percentile,
+                                     int32_t symmetric, float* scale, int64_t* zero_point,
+                                     float* min_val, float* max_val) {
+    if (n > 0 && !(percentile > 0.0f && percentile <= 100.0f))
+        return set_error(TKV_HIP_BAD_ARG, "percentile must be in (0, 100]");
+    return host_calibrate(data, n, scale, zero_point, min_val, max_val,
+                          [&](Ctx* c, const float* x, tkv_hip_qparams_dev* o) {
+                              return launch_calibrate_percentile(c, x, n, percentile, symmetric,
+                                                                 o);
+                          });
+}
+
+int32_t tkv_hip_calibrate_mse(const float* data, int64_t n, int64_t num_candidates,
+                              float* scale, int64_t* zero_point, float* min_val,
+                              float* max_val) {
+    return host_calibrate(data, n, scale, zero_point, min_val, max_val,
+                          [&](Ctx* c, const float* x, tkv_hip_qparams_dev* o) {
+                              return launch_calibrate_mse(c, x, n, num_candidates, o);
+                          });
+}
+
 int32_t tkv_hip_calibrate_minmax(const float* data, int64_t n, int32_t symmetric, float* scale,
                                  int64_t* zero_point, float* min_val, float* max_val) {
     if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative length");
@@ -548,6 +613,31 @@ int32_t tkv_hip_dev_quantize_int8_tensor(int64_t ctx, const float* x, int64_t n,
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
     return launch_quant_i8_tensor(c, x, n, params, q, false);
+}
+
+int32_t tkv_hip_dev_calibrate_kl(int64_t ctx, const float* x, int64_t n, int64_t num_bins,
+                                 int64_t target_bins, tkv_hip_qparams_dev* params) {
+    if (!params) return set_error(TKV_HIP_BAD_ARG, "NULL params");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_calibrate_kl(c, x, n, num_bins, target_bins, params);
+}
+
+int32_t tkv_hip_dev_calibrate_percentile(int64_t ctx, const float* x, int64_t n,
+                                         float percentile, int32_t symmetric,
+                                         tkv_hip_qparams_dev* params) {
+    if (!params) return set_error(TKV_HIP_BAD_ARG, "NULL params");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_calibrate_percentile(c, x, n, percentile, symmetric, params);
+}
+
+int32_t tkv_hip_dev_calibrate_mse(int64_t ctx, const float* x, int64_t n,
+                                  int64_t num_candidates, tkv_hip_qparams_dev* params) {
+    if (!params) return set_error(TKV_HIP_BAD_ARG, "NULL params");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_calibrate_mse(c, x, n, num_candidates, params);
 }
 
 int32_t tkv_hip_dev_quantize_int8_dynamic_tensor(int64_t ctx, const float* x, int64_t n,

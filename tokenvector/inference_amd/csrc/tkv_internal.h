@@ -81,6 +81,18 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 // quant.hip
 int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe,
                          tkv_hip_qparams_dev* out);
+// calib.hip: calibrate_kl / _percentile / _mse (engine.tkv:42-197) into *out.
+constexpr int64_t kMaxKlBins = 4096;
+constexpr int64_t kMaxMseCandidates = 4096;
+int launch_calibrate_kl(Ctx* c, const float* x, int64_t n, int64_t num_bins, int64_t target_bins,
+                        tkv_hip_qparams_dev* out);
+int launch_calibrate_percentile(Ctx* c, const float* x, int64_t n, float percentile,
+                                int symmetric, tkv_hip_qparams_dev* out);
+int launch_calibrate_mse(Ctx* c, const float* x, int64_t n, int64_t num_candidates,
+                         tkv_hip_qparams_dev* out);
+// Per-block min / max (+ first zero when track_zero) partials of x into
+// c->partials; *nparts = their count (reduced by reduce_partials, tkv_reduce.h).
+int launch_partials(Ctx* c, const float* x, int64_t n, int track_zero, int64_t* nparts);
 enum MinMaxMode { MM_SYMMETRIC = 0, MM_ASYMMETRIC = 1, MM_DYNAMIC_QL = 2, MM_FP8 = 3 };
 // FP8 scaling target: amax maps to 240, the largest e4m3 value the
 // reference encoder reaches without its >= 248 saturation step.

@@ -151,6 +151,21 @@ def calibrate_minmax(ctx, x, n, symmetric, params) -> None:
                                                        _vp(params)))
 
 
+def calibrate_kl(ctx, x, n, params, num_bins: int = 2048, target_bins: int = 128) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_calibrate_kl(ctx.handle, _vp(x), int(n), int(num_bins),
+                                                   int(target_bins), _vp(params)))
+
+
+def calibrate_percentile(ctx, x, n, params, percentile: float = 99.99, symmetric: int = 1) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_calibrate_percentile(
+        ctx.handle, _vp(x), int(n), float(np.float32(percentile)), int(symmetric), _vp(params)))
+
+
+def calibrate_mse(ctx, x, n, params, num_candidates: int = 50) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_calibrate_mse(ctx.handle, _vp(x), int(n),
+                                                    int(num_candidates), _vp(params)))
+
+
 def calibrate_rows(ctx, x, rows, cols, scales) -> None:
     _lib.check(_lib.lib().tkv_hip_dev_calibrate_rows(ctx.handle, _vp(x), int(rows), int(cols),
                                                      _vp(scales)))

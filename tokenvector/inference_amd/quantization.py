@@ -73,6 +73,34 @@ def calibrate_minmax(data, symmetric: int = 1) -> QuantParams:
     return QuantParams(np.float32(s.value), int(zp.value), np.float32(mn.value), np.float32(mx.value))
 
 
+def _calib_call(name, x, *args) -> QuantParams:
+    s, mn, mx = C.c_float(), C.c_float(), C.c_float()
+    zp = C.c_int64()
+    rc = getattr(_lib.lib(), name)(_p(x), x.size, *args, C.byref(s), C.byref(zp), C.byref(mn),
+                                   C.byref(mx))
+    _lib.check(rc)
+    return QuantParams(np.float32(s.value), int(zp.value), np.float32(mn.value), np.float32(mx.value))
+
+
+def calibrate_kl(data, num_bins: int = 2048, target_bins: int = 128) -> QuantParams:
+    """engine.tkv:42-123 -- TensorRT-style KL calibration of |x|'s histogram."""
+    return _calib_call("tkv_hip_calibrate_kl", _f32_in(data), int(num_bins), int(target_bins))
+
+
+def calibrate_percentile(data, percentile: float = 99.99, symmetric: int = 1) -> QuantParams:
+    """engine.tkv:126-162 -- clip at the percentile of |x|; ValueError outside (0, 100]."""
+    x = _f32_in(data)
+    if x.size and not (0.0 < np.float32(percentile) <= 100.0):
+        raise ValueError("percentile must be in (0, 100]")
+    return _calib_call("tkv_hip_calibrate_percentile", x, float(np.float32(percentile)),
+                       int(symmetric))
+
+
+def calibrate_mse(data, num_candidates: int = 50) -> QuantParams:
+    """engine.tkv:165-197 -- grid search of symmetric thresholds minimizing the MSE."""
+    return _calib_call("tkv_hip_calibrate_mse", _f32_in(data), int(num_candidates))
+
+
 def calibrate_per_channel_minmax(data, rows: int, cols: int, symmetric: int = 1) -> List[QuantParams]:
     """engine.tkv:202-213 -- calibrate_minmax per row of a [rows, cols] matrix."""
     x = _f32_in(data)
