@@ -141,6 +141,25 @@ def test_calibrate_mse(hip, n):
     assert _same_qp(Q.calibrate_mse(z), O.calibrate_mse(z))
 
 
+@pytest.mark.parametrize("n", [1003, 65539])
+def test_calibrators_misaligned_device(ctx, n):
+    """The device calibrators on x one float past a 16-byte boundary (the
+    scalar load paths), called twice on one context, against the oracle."""
+    say(f"calibrators misaligned n={n}")
+    x = O.add_outliers(_x(n, 53, 1.0), 0.001, 3, 4, 20.0)
+    dx = D.DeviceBuffer.from_host(ctx, np.concatenate([np.zeros(1, np.float32), x]))
+    p = D.params_buffer(ctx)
+    xp = dx.ptr + 4
+    for _ in range(2):
+        D.calibrate_kl(ctx, xp, n, p, 512, 32)
+        g = D.read_params(p)
+        assert _same_qp(g, O.calibrate_kl(x, 512, 32))
+        D.calibrate_percentile(ctx, xp, n, p, 99.9, 0)
+        assert _same_qp(D.read_params(p), O.calibrate_percentile(x, 99.9, 0))
+        D.calibrate_mse(ctx, xp, n, p, 37)
+        assert _same_qp(D.read_params(p), O.calibrate_mse(x, 37))
+
+
 # ---------------------------------------------------------------------------
 # quantize / dequantize (config 2 shapes)
 # ---------------------------------------------------------------------------

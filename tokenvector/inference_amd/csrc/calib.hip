@@ -4,16 +4,17 @@
 //   calibrate_kl          max|x| from the min / max partials, a num_bins
 //                         histogram of |x| (LDS per block, 64-bit global
 //                         atomics), then the threshold search: one candidate
-//                         threshold per thread, each evaluated in the
+//                         threshold per wave, its kl sum added in the
 //                         reference's sequential order.
 //   calibrate_percentile  the k-th smallest |x| by radix select on its f32 bit
 //                         pattern (non-negative floats order as integers):
 //                         three histogram passes of 11 / 11 / 10 bits, each
 //                         followed by a one-block digit pick; the asymmetric
 //                         form clips the min / max partials.
-//   calibrate_mse         one pass computing every candidate threshold's
-//                         squared quantization error per block (f64), then a
-//                         one-block selection.
+//   calibrate_mse         passes over x of 16 candidate thresholds each,
+//                         summing squared quantization errors per block
+//                         (f64), one block per candidate reducing those
+//                         sums, then the reference's first-minimum pick.
 //
 // Numerics follow the reference's f64 locals.  Sums whose order the
 // reference fixes are reproduced in that order where they decide the result
@@ -21,6 +22,8 @@
 // (a different order than the reference's single loop), which can only
 // matter for candidates within rounding of each other.
 #include <float.h>
+
+#include <utility>
 
 #include "tkv_device.h"
 #include "tkv_internal.h"
@@ -33,7 +36,7 @@ namespace {
 constexpr int kCalBlock = 256;
 constexpr int kRadixBits = 11;
 constexpr int kRadixBins = 1 << kRadixBits;  // 2048
-constexpr int kMseChunk = 52;                // candidates per accumulation pass (50 by default)
+constexpr int kMseChunk = 16;  // most candidates per pass: their scale / inv pairs fit in SGPRs
 
 // Device-side state of one calibration call (in a context workspace).
 struct CalibState {
@@ -141,36 +144,37 @@ __global__ __launch_bounds__(kCalBlock) void k_kl_hist(const float* __restrict__
     }
 }
 
-// Suffix sums of the histogram (exact integers in f64) and its total.
-__global__ void k_kl_suffix(int num_bins, const unsigned long long* __restrict__ hist,
-                            double* __restrict__ suf) {
-    double acc = 0.0;
-    for (int i = num_bins - 1; i >= 0; i--) {
-        acc = acc + (double)hist[i];
-        suf[i] = acc;
-    }
-}
-
 // Candidate th = target + 16 * blockIdx.x, one wave each.  Every candidate's
 // total s equals the histogram total (the tail is merged into p[th - 1]), so
-// p[i] = hist[i] / s for i < th - 1 and p[th - 1] = (exact integer suffix
-// sum) / s, as the reference's own arithmetic gives.  Lanes form the block
-// shares (each block's mass summed in index order) and the kl terms in
-// parallel; lane 0 adds the terms in index order, so kl is the reference's
-// sequential sum bit for bit (terms the reference skips are +0.0).
+// p[i] = hist[i] / s for i < th - 1 and p[th - 1] = (tail sum) / s, as the
+// reference's own arithmetic gives; the total and the tail are integer sums,
+// exact in f64 in any order.  Lanes form the block shares (each block's mass
+// summed in index order) and the kl terms in parallel; lane 0 adds the terms
+// in index order, so kl is the reference's sequential sum bit for bit (terms
+// the reference skips are +0.0).
 __global__ __launch_bounds__(64) void k_kl_candidate(int num_bins, int target_bins,
                                                      const unsigned long long* __restrict__ hist,
-                                                     const double* __restrict__ suf,
                                                      double* __restrict__ kl_out) {
     extern __shared__ double s_dyn[];  // [num_bins] p, then [target_bins] shares
     double* s_p = s_dyn;
     double* s_share = s_dyn + num_bins;
+    __shared__ double s_t[64];
     const int lane = threadIdx.x;
     const int th = target_bins + 16 * (int)blockIdx.x;
-    const double total = suf[0];
-    for (int i = lane; i < th; i += 64) s_p[i] = (double)hist[i] / total;
-    __syncthreads();
-    if (lane == 0) s_p[th - 1] = suf[th - 1] / total;
+    unsigned long long tot = 0, tail = 0;
+    for (int i = lane; i < num_bins; i += 64) {
+        const unsigned long long h = hist[i];
+        tot += h;
+        if (i >= th - 1) tail += h;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        tot += __shfl_xor(tot, o, 64);
+        tail += __shfl_xor(tail, o, 64);
+    }
+    const double total = (double)tot;
+    for (int i = lane; i < th - 1; i += 64) s_p[i] = (double)hist[i] / total;
+    if (lane == 0) s_p[th - 1] = (double)tail / total;
     __syncthreads();
     const int per = th / target_bins;
     for (int b = lane; b < target_bins; b += 64) {
@@ -192,8 +196,13 @@ __global__ __launch_bounds__(64) void k_kl_candidate(int num_bins, int target_bi
             const double pi = s_p[i], sh = s_share[b];
             if (pi > 0.000000000001 && sh > 0.000000000001) t = pi * log(pi / sh);
         }
-        const int cnt = th - i0 < 64 ? th - i0 : 64;
-        for (int l = 0; l < cnt; l++) kl = kl + __shfl(t, l, 64);
+        s_t[lane] = t;
+        __syncthreads();
+        if (lane == 0) {
+            const int cnt = th - i0 < 64 ? th - i0 : 64;
+            for (int l = 0; l < cnt; l++) kl = kl + s_t[l];
+        }
+        __syncthreads();
     }
     if (lane == 0) kl_out[blockIdx.x] = kl;
 }
@@ -273,25 +282,42 @@ __global__ __launch_bounds__(kCalBlock) void k_radix_hist(const float* __restric
     }
 }
 
-// Digit holding the element of rank st->rank; clears the histogram after.
+// Digit holding the element of rank st->rank (block prefix sum over the
+// 2048 digit counts, 8 per thread); clears the histogram after.
 __global__ __launch_bounds__(kCalBlock) void k_radix_pick(int shift, CalibState* st,
                                                           unsigned long long* __restrict__ hist) {
-    __shared__ unsigned long long s_h[kRadixBins];
-    for (int i = threadIdx.x; i < kRadixBins; i += kCalBlock) {
-        s_h[i] = hist[i];
-        hist[i] = 0;
+    constexpr int kPer = kRadixBins / kCalBlock;
+    __shared__ unsigned long long s_scan[kCalBlock];
+    unsigned long long h[kPer], sum = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        h[j] = hist[threadIdx.x * kPer + j];
+        hist[threadIdx.x * kPer + j] = 0;
+        sum += h[j];
     }
+    s_scan[threadIdx.x] = sum;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int64_t rank = st->rank;
+    for (int o = 1; o < kCalBlock; o <<= 1) {  // inclusive scan
+        const unsigned long long v = threadIdx.x >= o ? s_scan[threadIdx.x - o] : 0ull;
+        __syncthreads();
+        s_scan[threadIdx.x] += v;
+        __syncthreads();
+    }
+    const int64_t rank = st->rank;
+    const unsigned long long before = threadIdx.x ? s_scan[threadIdx.x - 1] : 0ull;
+    const unsigned long long upto = s_scan[threadIdx.x];
+    __syncthreads();  // every thread has read st->rank before it is rewritten
+    // a rank past the total lands in the last digit, as a sequential walk ends
+    if ((unsigned long long)rank >= before &&
+        ((unsigned long long)rank < upto || threadIdx.x == kCalBlock - 1)) {
+        int64_t r = rank - (int64_t)before;
         int d = 0;
-        for (; d < kRadixBins - 1; d++) {
-            const int64_t c = (int64_t)s_h[d];
-            if (rank < c) break;
-            rank -= c;
+        for (; d < kPer - 1; d++) {
+            if (r < (int64_t)h[d]) break;
+            r -= (int64_t)h[d];
         }
-        st->rank = rank;
-        st->prefix |= (uint32_t)d << shift;
+        st->rank = r;
+        st->prefix |= (uint32_t)(threadIdx.x * kPer + d) << shift;
     }
 }
 
@@ -324,11 +350,14 @@ __global__ void k_pct_final(const float* __restrict__ x, int symmetric,
 // ---------------------------------------------------------------------------
 
 // Candidate c (1-based) of num_candidates: thr = am * c / nc, scale = thr /
-// 127, inv = 1 / scale (f64, as the reference's locals).
-__global__ __launch_bounds__(kCalBlock) void k_mse_table(int nc, const CalibState* __restrict__ st,
+// 127, inv = 1 / scale (f64, as the reference's locals).  Entries up to npad
+// (whole chunks) past nc repeat the last candidate; their sums are dropped.
+__global__ __launch_bounds__(kCalBlock) void k_mse_table(int nc, int npad,
+                                                         const CalibState* __restrict__ st,
                                                          double* __restrict__ table) {
-    for (int c = threadIdx.x; c < nc; c += kCalBlock) {
-        const double thr = st->am * (double)(c + 1) / (double)nc;
+    for (int c = threadIdx.x; c < npad; c += kCalBlock) {
+        const int cc = c < nc ? c : nc - 1;
+        const double thr = st->am * (double)(cc + 1) / (double)nc;
         const double scale = thr / 127.0;
         table[3 * c + 0] = thr;
         table[3 * c + 1] = scale;
@@ -336,88 +365,113 @@ __global__ __launch_bounds__(kCalBlock) void k_mse_table(int nc, const CalibStat
     }
 }
 
-// Squared error of candidates [c0, c0 + kMseChunk) summed over this block's
-// elements: partial[block * nc + c].  The candidate constants are wave-uniform
-// (scalar loads).  Clamping with max / min instead of the reference's
-// compares only differs for NaN, where every candidate's error is NaN either
-// way; after the clamp |cl * inv| <= 127 (to rounding), so the code needs no
-// second clamp.
+// Squared error of one element against candidate (scale, inv), on a = |x|.
+// The reference clamps x to [-thr, thr], rounds x * inv half to even and
+// clamps the code to [-127, 127].  Since fl(thr * inv) lies within a few ulps
+// of 127, min(rint(|x| * inv), 127) is that code's magnitude for every x, and
+// the error of -x is the negated error of x, so its square is the same.  NaN
+// stays NaN (a - q * scale).  The products are contracted into fmas.
+__device__ __forceinline__ double mse_term(double a, double scale, double inv) {
+    const double q = __builtin_fmin(__builtin_rint(a * inv), 127.0);
+    const double d = a - q * scale;
+    return d * d;
+}
+
+// Squared error of candidates [c0, c0 + CH) summed over this block's
+// elements: partial[block * nc + c] for c < nc.  Each thread sums its
+// elements in index order, four per float4.
+template <int CH>
 __global__ __launch_bounds__(kCalBlock) void k_mse_partials(const float* __restrict__ x, int64_t n,
-                                                            int nc, int c0,
+                                                            int vec, int nc, int c0,
                                                             const double* __restrict__ table,
                                                             double* __restrict__ partial) {
-    __shared__ double s_red[kCalBlock / 64][kMseChunk];
-    const int cn = nc - c0 < kMseChunk ? nc - c0 : kMseChunk;
-    const double* __restrict__ t = table + 3 * c0;
-    double acc[kMseChunk];
+    __shared__ double s_red[kCalBlock / 64][CH];
+    double sc[CH], iv[CH], acc[CH];
 #pragma unroll
-    for (int c = 0; c < kMseChunk; c++) acc[c] = 0.0;
+    for (int c = 0; c < CH; c++) {
+        sc[c] = table[3 * (c0 + c) + 1];
+        iv[c] = table[3 * (c0 + c) + 2];
+        acc[c] = 0.0;
+    }
     const int64_t stride = (int64_t)gridDim.x * kCalBlock;
-    for (int64_t i = (int64_t)blockIdx.x * kCalBlock + threadIdx.x; i < n; i += stride) {
-        const double v = (double)x[i];
+    const int64_t tid = (int64_t)blockIdx.x * kCalBlock + threadIdx.x;
+    const int64_t n4 = vec ? n / 4 : 0;
+    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
+    for (int64_t i = tid; i < n4; i += stride) {
+        const float4 u = x4[i];
+        const double a0 = __builtin_fabs((double)u.x), a1 = __builtin_fabs((double)u.y);
+        const double a2 = __builtin_fabs((double)u.z), a3 = __builtin_fabs((double)u.w);
 #pragma unroll
-        for (int c = 0; c < kMseChunk; c++) {
-            if (c < cn) {
-                const double thr = t[3 * c], scale = t[3 * c + 1], inv = t[3 * c + 2];
-                const double cl = __builtin_fmin(__builtin_fmax(v, -thr), thr);
-                const double q = __builtin_rint(cl * inv);
-                const double d = v - q * scale;
-                acc[c] = acc[c] + d * d;
-            }
+        for (int c = 0; c < CH; c++) {
+            acc[c] = acc[c] + mse_term(a0, sc[c], iv[c]);
+            acc[c] = acc[c] + mse_term(a1, sc[c], iv[c]);
+            acc[c] = acc[c] + mse_term(a2, sc[c], iv[c]);
+            acc[c] = acc[c] + mse_term(a3, sc[c], iv[c]);
         }
+    }
+    for (int64_t i = 4 * n4 + tid; i < n; i += stride) {
+        const double a = __builtin_fabs((double)x[i]);
+#pragma unroll
+        for (int c = 0; c < CH; c++) acc[c] = acc[c] + mse_term(a, sc[c], iv[c]);
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int c = 0; c < kMseChunk; c++) {
+    for (int c = 0; c < CH; c++) {
         double a = acc[c];
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) a = a + __shfl_xor(a, o, 64);
         if (lane == 0) s_red[wave][c] = a;
     }
     __syncthreads();
-    for (int c = threadIdx.x; c < cn; c += kCalBlock) {
+    if (threadIdx.x < CH && c0 + (int)threadIdx.x < nc) {
         double a = 0.0;
-        for (int w = 0; w < kCalBlock / 64; w++) a = a + s_red[w][c];
-        partial[(int64_t)blockIdx.x * nc + c0 + c] = a;
+        for (int w = 0; w < kCalBlock / 64; w++) a = a + s_red[w][threadIdx.x];
+        partial[(int64_t)blockIdx.x * nc + c0 + threadIdx.x] = a;
     }
 }
 
-// mse[c] = (sum over blocks, in block order) / n; the first strict minimum
-// over c ascending wins, as in the reference's loop.
-__global__ __launch_bounds__(kCalBlock) void k_mse_select(int64_t n, int nc, int nblocks,
-                                                          const double* __restrict__ table,
+using MsePartialsFn = void (*)(const float*, int64_t, int, int, int, const double*, double*);
+
+template <int... CH>
+constexpr MsePartialsFn mse_partials_for(int ch, std::integer_sequence<int, CH...>) {
+    constexpr MsePartialsFn fns[] = {k_mse_partials<CH + 1>...};
+    return fns[ch - 1];
+}
+
+// mse[c] = (sum over the per-block partials, a fixed tree order) / n.
+__global__ __launch_bounds__(kCalBlock) void k_mse_reduce(int64_t n, int nc, int nblocks,
                                                           const double* __restrict__ partial,
-                                                          const CalibState* __restrict__ st,
-                                                          tkv_hip_qparams_dev* __restrict__ out) {
-    __shared__ double s_m[kCalBlock];
-    __shared__ int s_c[kCalBlock];
-    double best = 1e45;
-    int bc = -1;
-    for (int c = threadIdx.x; c < nc; c += kCalBlock) {
-        double s = 0.0;
-        for (int b = 0; b < nblocks; b++) s = s + partial[(int64_t)b * nc + c];
-        const double mse = s / (double)n;
-        if (mse < best) {
-            best = mse;
-            bc = c;
-        }
-    }
-    s_m[threadIdx.x] = best;
-    s_c[threadIdx.x] = bc;
+                                                          double* __restrict__ mse) {
+    __shared__ double s_red[kCalBlock / 64];
+    const int c = blockIdx.x;
+    double a = 0.0;
+    for (int b = threadIdx.x; b < nblocks; b += kCalBlock) a = a + partial[(int64_t)b * nc + c];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) a = a + __shfl_xor(a, o, 64);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = a;
     __syncthreads();
     if (threadIdx.x == 0) {
-        double m = s_m[0];
-        int c = s_c[0];
-        for (int t = 1; t < kCalBlock; t++)
-            if (s_c[t] >= 0 && (s_m[t] < m || (s_m[t] == m && (c < 0 || s_c[t] < c)))) {
-                m = s_m[t];
-                c = s_c[t];
-            }
-        if (st->am < 0.00000001)
-            finalize_minmax(st->mn, st->mx, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
-        else
-            write_sym(c >= 0 ? table[3 * c] : st->am, out);
+        double t = 0.0;
+        for (int w = 0; w < kCalBlock / 64; w++) t = t + s_red[w];
+        mse[c] = t / (double)n;
     }
+}
+
+// The first strict minimum over c ascending, as in the reference's loop.
+__global__ void k_mse_select(int nc, const double* __restrict__ table,
+                             const double* __restrict__ mse, const CalibState* __restrict__ st,
+                             tkv_hip_qparams_dev* __restrict__ out) {
+    double best = 1e45;
+    int bc = -1;
+    for (int c = 0; c < nc; c++)
+        if (mse[c] < best) {
+            best = mse[c];
+            bc = c;
+        }
+    if (st->am < 0.00000001)
+        finalize_minmax(st->mn, st->mx, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
+    else
+        write_sym(bc >= 0 ? table[3 * bc] : st->am, out);
 }
 
 int64_t cal_grid(Ctx* c, int64_t n) {
@@ -449,8 +503,7 @@ int launch_calibrate_kl(Ctx* c, const float* x, int64_t n, int64_t num_bins, int
     const int ncand = num_bins >= target_bins ? (int)((num_bins - target_bins) / 16 + 1) : 0;
     TKV_RC_TRY(cal_workspace(c, (size_t)num_bins * 16 + (size_t)ncand * 8 + 8, &st, &rest));
     auto* hist = static_cast<unsigned long long*>(rest);
-    auto* suf = reinterpret_cast<double*>(hist + num_bins);
-    double* kl = suf + num_bins;
+    double* kl = reinterpret_cast<double*>(hist + num_bins);
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
     hipLaunchKernelGGL(k_cal_prep, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts, 0,
@@ -461,12 +514,10 @@ int launch_calibrate_kl(Ctx* c, const float* x, int64_t n, int64_t num_bins, int
                        (size_t)num_bins * 4 * (kCalBlock / 64), c->stream, x, n, vec,
                        (int)num_bins, st, hist);
     TKV_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_kl_suffix, dim3(1), dim3(1), 0, c->stream, (int)num_bins, hist, suf);
-    TKV_LAUNCH_CHECK();
     if (ncand > 0) {
         hipLaunchKernelGGL(k_kl_candidate, dim3((unsigned)ncand), dim3(64),
                            (size_t)(num_bins + target_bins) * 8, c->stream, (int)num_bins,
-                           (int)target_bins, hist, suf, kl);
+                           (int)target_bins, hist, kl);
         TKV_LAUNCH_CHECK();
     }
     hipLaunchKernelGGL(k_kl_select, dim3(1), dim3(1), 0, c->stream, ncand, (int)num_bins,
@@ -518,27 +569,40 @@ int launch_calibrate_mse(Ctx* c, const float* x, int64_t n, int64_t num_candidat
     if (n <= 0 || num_candidates > kMaxMseCandidates)
         return set_error(TKV_HIP_BAD_ARG, "calibrate_mse: needs n > 0, num_candidates <= 4096");
     const int nc = (int)(num_candidates < 4 ? 4 : num_candidates);
-    const int grid = (int)cal_grid(c, n);
+    // passes of ch <= kMseChunk candidates, as even as whole passes allow
+    const int passes = (int)ceil_div((int64_t)nc, (int64_t)kMseChunk);
+    const int ch = (int)ceil_div((int64_t)nc, (int64_t)passes);
+    const int npad = passes * ch;
+    // compute-bound: up to 8 blocks per CU
+    int64_t blocks = ceil_div(n, (int64_t)kCalBlock * 4);
+    if (blocks > (int64_t)c->num_cus * 8) blocks = (int64_t)c->num_cus * 8;
+    const int grid = blocks < 1 ? 1 : (int)blocks;
+    const int vec = aligned(x, 16) ? 1 : 0;
     CalibState* st;
     void* rest;
-    TKV_RC_TRY(cal_workspace(c, (size_t)nc * 24 + (size_t)grid * nc * 8, &st, &rest));
+    TKV_RC_TRY(cal_workspace(c, (size_t)npad * 24 + (size_t)nc * 8 + (size_t)grid * nc * 8, &st,
+                             &rest));
     auto* table = static_cast<double*>(rest);
-    double* partial = table + 3 * nc;
+    double* mse = table + 3 * npad;
+    double* partial = mse + nc;
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
     hipLaunchKernelGGL(k_cal_prep, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts, 0,
                        c->partials, (int64_t)0, st, (unsigned long long*)nullptr, (int64_t)0,
                        (int64_t)0);
     TKV_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_mse_table, dim3(1), dim3(kCalBlock), 0, c->stream, nc, st, table);
+    hipLaunchKernelGGL(k_mse_table, dim3(1), dim3(kCalBlock), 0, c->stream, nc, npad, st, table);
     TKV_LAUNCH_CHECK();
-    for (int c0 = 0; c0 < nc; c0 += kMseChunk) {
-        hipLaunchKernelGGL(k_mse_partials, dim3((unsigned)grid), dim3(kCalBlock), 0, c->stream,
-                           x, n, nc, c0, table, partial);
+    const MsePartialsFn fn = mse_partials_for(ch, std::make_integer_sequence<int, kMseChunk>());
+    for (int c0 = 0; c0 < nc; c0 += ch) {
+        hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kCalBlock), 0, c->stream,
+                           x, n, vec, nc, c0, table, partial);
         TKV_LAUNCH_CHECK();
     }
-    hipLaunchKernelGGL(k_mse_select, dim3(1), dim3(kCalBlock), 0, c->stream, n, nc, grid, table,
-                       partial, st, out);
+    hipLaunchKernelGGL(k_mse_reduce, dim3((unsigned)nc), dim3(kCalBlock), 0, c->stream, n, nc,
+                       grid, partial, mse);
+    TKV_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_mse_select, dim3(1), dim3(1), 0, c->stream, nc, table, mse, st, out);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
