@@ -88,6 +88,8 @@ int32_t tkv_hip_malloc(int64_t ctx, int64_t bytes, void** ptr_out);
 int32_t tkv_hip_free(int64_t ctx, void* ptr);
 int32_t tkv_hip_memcpy_h2d(int64_t ctx, void* dst, const void* src, int64_t bytes);
 int32_t tkv_hip_memcpy_d2h(int64_t ctx, void* dst, const void* src, int64_t bytes);
+/* Byte fill, asynchronous on the context's stream (a kernel, so it can be
+ * captured). */
 int32_t tkv_hip_memset(int64_t ctx, void* dst, int32_t value, int64_t bytes);
 /* Device-to-device copy, asynchronous on the context's stream.  16-byte
  * aligned pointers and sizes run one plain streaming kernel (k_copy16) that
@@ -98,6 +100,20 @@ int32_t tkv_hip_event_create(int64_t* ev_out);
 int32_t tkv_hip_event_destroy(int64_t ev);
 int32_t tkv_hip_event_record(int64_t ctx, int64_t ev);
 int32_t tkv_hip_event_elapsed_ms(int64_t ev_start, int64_t ev_end, float* ms_out);
+/* Stream capture into a replayable HIP graph.  No reference counterpart (the
+ * reference runs this path on the CPU); for callers that repeat a fixed
+ * sequence of device entry points (a layer stack, a decode step) and want
+ * one launch per sequence.  Between begin and end the context's stream
+ * records instead of running; every entry point called in between must
+ * find its workspace already sized by an identical earlier call (it fails
+ * with TKV_HIP_BAD_ARG otherwise), and host-pointer entry points, copies to
+ * or from the host and synchronizations fail.  A graph replays the captured
+ * device pointers and scalars as they were; device-resident QuantParams are
+ * re-read on every replay. */
+int32_t tkv_hip_capture_begin(int64_t ctx);
+int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out);
+int32_t tkv_hip_graph_launch(int64_t ctx, int64_t graph);
+int32_t tkv_hip_graph_destroy(int64_t graph);
 
 /* ======================================================================== */
 /* Host-pointer mirrors (one per .tkv function).  ctx-free: each calling    */

@@ -709,3 +709,78 @@ def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
 def _lib_check(D, name, *args):
     from tokenvector.inference_amd import _lib
     _lib.check(getattr(_lib.lib(), name)(*args))
+
+
+# ---------------------------------------------------------------------------
+# stream capture (tkv_hip_capture_begin / capture_end / graph_launch)
+# ---------------------------------------------------------------------------
+
+def test_graph_capture_replays(hip):
+    """A captured layer (dynamic quantize, an INT8 GEMM whose K needs the
+    zero-padded operand repack, a byte fill) replays to the eager results bit
+    for bit: three replays, each after new input values, other eager work and
+    a synchronization.  A call that would grow a workspace inside a capture is
+    refused on the host, and the stream runs eagerly again afterwards."""
+    say("graph capture replays")
+    ctx = D.Context(0)  # fresh workspaces: the refusal below depends on their sizes
+    m, n, k = 300, 200, 200
+    w = _x(n * k, 63, 0.05)
+    sw = np.array([q.scale for q in O.calibrate_per_channel_minmax(w, n, k)], np.float32)
+    wq = O.quantize_int8_per_channel(w, n, k, sw).astype(np.int8)
+    dw, dsw = D.DeviceBuffer.from_host(ctx, wq), D.DeviceBuffer.from_host(ctx, sw)
+    db = D.DeviceBuffer.from_host(ctx, _x(n, 64, 0.01))
+    dx = D.DeviceBuffer.empty(ctx, (m, k), np.float32)
+    qa = D.DeviceBuffer.empty(ctx, (m, k), np.int8)
+    dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+    fill = D.DeviceBuffer.empty(ctx, 1000, np.uint8)
+    p = D.params_buffer(ctx)
+    other_x = D.DeviceBuffer.from_host(ctx, _x(4099, 65, 1.0))
+    other_q = D.DeviceBuffer.empty(ctx, 4099, np.int8)
+    other_p = D.params_buffer(ctx)
+
+    def layer():
+        D.quantize_int8_dynamic_tensor(ctx, dx, m * k, qa, p)
+        D.matmul_int8(ctx, qa, dw, m, n, k, p.ptr, 0, 0.0, dsw, db, dy)
+        D.memset(ctx, fill.ptr + 3, 0x5A, 990)
+
+    inputs = [_x(m * k, 70 + i, 1.0 + i) for i in range(3)]
+    want = []
+    for x in inputs:
+        dx.upload(x)
+        D.memset(ctx, fill, 0, 1000)
+        layer()
+        ctx.synchronize()
+        want.append((qa.download(), dy.download(), fill.download()))
+    f = np.zeros(1000, np.uint8)
+    f[3:993] = 0x5A
+    assert np.array_equal(want[0][2], f)
+
+    with D.Graph(ctx) as g:
+        layer()
+    for rep in range(2):
+        for x, (wqa, wy, wf) in zip(inputs, want):
+            dx.upload(x)
+            D.quantize_int8_dynamic_tensor(ctx, other_x, 4099, other_q, other_p)
+            D.memset(ctx, fill, 0, 1000)
+            D.memset(ctx, qa, 0, m * k)
+            ctx.synchronize()
+            g.launch()
+            ctx.synchronize()
+            assert np.array_equal(qa.download(), wqa), rep
+            assert np.array_equal(dy.download(), wy), rep
+            assert np.array_equal(fill.download(), wf), rep
+    g.close()
+
+    # K = 300 pads to 384: 4100 x 384 bytes outgrows the 1 MiB repack slot
+    big_a = D.DeviceBuffer.empty(ctx, (4100, 300), np.int8)
+    big_w = D.DeviceBuffer.empty(ctx, (n, 300), np.int8)
+    big_y = D.DeviceBuffer.empty(ctx, (4100, n), np.float32)
+    with pytest.raises((ValueError, RuntimeError), match="stream capture"):
+        with D.Graph(ctx) as bad:
+            D.matmul_int8(ctx, big_a, big_w, 4100, n, 300, p.ptr, 0, 0.0, dsw, db, big_y)
+    bad.close()
+    dx.upload(inputs[1])
+    layer()
+    ctx.synchronize()
+    assert np.array_equal(dy.download(), want[1][1])
+    ctx.close()

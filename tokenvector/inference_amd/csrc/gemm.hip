@@ -788,6 +788,34 @@ static int launch_any(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
     }
 }
 
+// dst[r * ldk + j] = j < k ? src[r * k + j] : 0 for r < rows, j < ldk
+// (ldk a multiple of 16, dst 16-byte aligned): 16 output bytes per lane.
+__global__ void __launch_bounds__(256) k_pad_rows(const uint8_t* __restrict__ src, int64_t k,
+                                                  int64_t rows, int64_t ldk,
+                                                  uint8_t* __restrict__ dst) {
+    typedef unsigned char u8x16 __attribute__((ext_vector_type(16)));
+    const int64_t n16 = rows * (ldk / 16);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+        const int64_t r = i / (ldk / 16), j0 = (i % (ldk / 16)) * 16;
+        const uint8_t* __restrict__ s = src + r * k;
+        u8x16 v;
+#pragma unroll
+        for (int b = 0; b < 16; b++) v[b] = j0 + b < k ? s[j0 + b] : (uint8_t)0;
+        *reinterpret_cast<u8x16*>(dst + 16 * i) = v;
+    }
+}
+
+static int pad_rows(Ctx* c, const void* src, int64_t k, int64_t rows, int64_t ldk, void* dst) {
+    const int64_t n16 = rows * (ldk / 16);
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(n16 > 0 ? n16 : 1, 256),
+                                                      (int64_t)c->num_cus * 8);
+    hipLaunchKernelGGL(k_pad_rows, dim3(grid), dim3(256), 0, c->stream,
+                       static_cast<const uint8_t*>(src), k, rows, ldk, static_cast<uint8_t*>(dst));
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
 // Rows must start on 16-byte boundaries and K must be a multiple of the
 // slice depth: otherwise repack both operands into zero-padded workspace.
 static int prepare_operands(Ctx* c, const void** a, const void** w, int64_t m, int64_t n,
@@ -797,12 +825,8 @@ static int prepare_operands(Ctx* c, const void** a, const void** w, int64_t m, i
         void *pa, *pw;
         TKV_RC_TRY(ctx_workspace(c, 2, (size_t)(m * ldk), &pa));
         TKV_RC_TRY(ctx_workspace(c, 3, (size_t)(n * ldk), &pw));
-        TKV_HIP_TRY(hipMemsetAsync(pa, 0, (size_t)(m * ldk), c->stream));
-        TKV_HIP_TRY(hipMemsetAsync(pw, 0, (size_t)(n * ldk), c->stream));
-        TKV_HIP_TRY(hipMemcpy2DAsync(pa, (size_t)ldk, *a, (size_t)k, (size_t)k, (size_t)m,
-                                     hipMemcpyDeviceToDevice, c->stream));
-        TKV_HIP_TRY(hipMemcpy2DAsync(pw, (size_t)ldk, *w, (size_t)k, (size_t)k, (size_t)n,
-                                     hipMemcpyDeviceToDevice, c->stream));
+        TKV_RC_TRY(pad_rows(c, *a, k, m, ldk, pa));
+        TKV_RC_TRY(pad_rows(c, *w, k, n, ldk, pw));
         *a = pa;
         *w = pw;
     }

@@ -129,6 +129,12 @@ int ctx_get(int64_t handle, Ctx** out) {
 int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out) {
     if (bytes == 0) bytes = 256;
     if (c->ws_bytes[slot] < bytes) {
+        // growing synchronizes the stream and reallocates: not capturable
+        if (c->capturing)
+            return set_error(TKV_HIP_BAD_ARG,
+                             "workspace slot " + std::to_string(slot) +
+                                 " would grow inside a stream capture: make the same calls "
+                                 "once before capturing");
         if (c->ws[slot]) {
             TKV_HIP_TRY(hipStreamSynchronize(c->stream));
             TKV_HIP_TRY(hipFree(c->ws[slot]));
@@ -153,6 +159,38 @@ __global__ void __launch_bounds__(256) k_copy16(const u32x4* __restrict__ src,
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
         __builtin_nontemporal_store(__builtin_nontemporal_load(&src[i]), &dst[i]);
+}
+
+// Byte fill: 16 B per lane over the 16-byte aligned middle, bytes at the
+// ragged ends.  A kernel rather than hipMemsetAsync, so that a captured stream
+// records a kernel node.
+__global__ void __launch_bounds__(256) k_fill(uint8_t* __restrict__ dst, int64_t head,
+                                              int64_t n16, int64_t bytes, uint32_t word) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    u32x4* __restrict__ d16 = reinterpret_cast<u32x4*>(dst + head);
+    const u32x4 v = {word, word, word, word};
+    for (int64_t i = t; i < n16; i += stride) d16[i] = v;
+    const int64_t tail0 = head + 16 * n16;
+    for (int64_t i = t; i < head + (bytes - tail0); i += stride) {
+        const int64_t j = i < head ? i : tail0 + (i - head);
+        dst[j] = (uint8_t)word;
+    }
+}
+
+int launch_fill(Ctx* c, void* dst, int value, int64_t bytes) {
+    if (bytes <= 0) return TKV_HIP_OK;
+    const uintptr_t p = reinterpret_cast<uintptr_t>(dst);
+    int64_t head = (int64_t)((16 - (p & 15)) & 15);
+    if (head > bytes) head = bytes;
+    const int64_t n16 = (bytes - head) / 16;
+    const int64_t work = n16 > 0 ? n16 : 1;
+    const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, (int64_t)c->num_cus * 8);
+    const uint32_t b = (uint8_t)value;
+    k_fill<<<grid, 256, 0, c->stream>>>(static_cast<uint8_t*>(dst), head, n16, bytes,
+                                         b * 0x01010101u);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
 }
 
 }  // namespace tkv
@@ -280,7 +318,47 @@ int32_t tkv_hip_memset(int64_t ctx, void* dst, int32_t value, int64_t bytes) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
     if (bytes <= 0) return TKV_HIP_OK;
-    TKV_HIP_TRY(hipMemsetAsync(dst, value, (size_t)bytes, c->stream));
+    if (!dst) return set_error(TKV_HIP_BAD_ARG, "memset: NULL pointer");
+    return launch_fill(c, dst, value, bytes);
+}
+
+int32_t tkv_hip_capture_begin(int64_t ctx) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (c->capturing) return set_error(TKV_HIP_BAD_ARG, "capture_begin: already capturing");
+    TKV_HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (!graph_out) return set_error(TKV_HIP_BAD_ARG, "capture_end: graph_out is NULL");
+    *graph_out = 0;
+    if (!c->capturing) return set_error(TKV_HIP_BAD_ARG, "capture_end: no capture in progress");
+    c->capturing = false;
+    hipGraph_t g = nullptr;
+    TKV_HIP_TRY(hipStreamEndCapture(c->stream, &g));
+    hipGraphExec_t x = nullptr;
+    const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    *graph_out = reinterpret_cast<int64_t>(x);
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_graph_launch(int64_t ctx, int64_t graph) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (!graph) return set_error(TKV_HIP_BAD_ARG, "graph_launch: NULL graph");
+    if (c->capturing) return set_error(TKV_HIP_BAD_ARG, "graph_launch: context is capturing");
+    TKV_HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), c->stream));
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_graph_destroy(int64_t graph) {
+    if (graph) TKV_HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph)));
     return TKV_HIP_OK;
 }
 

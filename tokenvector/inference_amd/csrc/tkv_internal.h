@@ -58,6 +58,7 @@ struct Ctx {
     static constexpr int kSlots = 10;
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
+    bool capturing = false;  // between capture_begin and capture_end
 };
 
 int ctx_create(int device, Ctx** out);
@@ -66,7 +67,10 @@ int ctx_destroy(Ctx* c);
 // TKV_HIP_DEVICE, default 0).
 int ctx_get(int64_t handle, Ctx** out);
 // Device workspace slot `slot` of at least `bytes` (contents undefined).
+// Refuses to grow while the context's stream is being captured.
 int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out);
+// Byte fill of [dst, dst + bytes) on the context's stream (a kernel).
+int launch_fill(Ctx* c, void* dst, int value, int64_t bytes);
 // Environment gate: TKV_QUANT_HIP=0 turns every host mirror into a
 // TKV_HIP_UNSUPPORTED return so .tkv callers keep their own loops.
 bool hip_path_enabled();

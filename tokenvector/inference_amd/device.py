@@ -144,6 +144,50 @@ class Event:
             pass
 
 
+class Graph:
+    """The device entry points called inside ``with Graph(ctx) as g:``,
+    captured from the context's stream into one replayable HIP graph.
+
+    Every call inside the block must have run once, with the same sizes,
+    before the capture (workspaces are sized then); ``g.launch()`` replays
+    the sequence on the context's stream with the captured pointers."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.handle = 0
+
+    def __enter__(self):
+        _lib.check(_lib.lib().tkv_hip_capture_begin(self.ctx.handle))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = C.c_int64()
+        rc = _lib.lib().tkv_hip_capture_end(self.ctx.handle, C.byref(h))
+        if exc_type is None:
+            _lib.check(rc)
+        self.handle = h.value
+        return False
+
+    def launch(self) -> None:
+        _lib.check(_lib.lib().tkv_hip_graph_launch(self.ctx.handle, self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.check(_lib.lib().tkv_hip_graph_destroy(self.handle))
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def memset(ctx: Context, dst, value: int, nbytes: int) -> None:
+    """Byte fill on the context's stream (a kernel: capturable)."""
+    _lib.check(_lib.lib().tkv_hip_memset(ctx.handle, _vp(dst), int(value), int(nbytes)))
+
+
 # ---- packed-code kernels (device pointers) ---------------------------------
 
 def calibrate_minmax(ctx, x, n, symmetric, params) -> None:
