@@ -615,6 +615,10 @@ def test_gemm_every_config_int8(ctx, gemm_cfg, cfg):
         want = ((acc * sa.astype(np.float64)[:, None]) * sw.astype(np.float64)[None, :]
                 + b.astype(np.float64)[None, :]).astype(np.float32)
         assert _same_f32(dy.download(), want), (cfg, m, n, k)
+        D.matmul_int8(ctx, da, dw, m, n, k, dsa, 0, 0.0, dsw, db, dy)   # per-tensor sa[0]
+        want = ((acc * np.float64(sa[0])) * sw.astype(np.float64)[None, :]
+                + b.astype(np.float64)[None, :]).astype(np.float32)
+        assert _same_f32(dy.download(), want), (cfg, "per-tensor", m, n, k)
 
 
 @pytest.mark.parametrize("cfg", GEMM_CFGS)

@@ -370,7 +370,8 @@ __global__ __launch_bounds__(kCalBlock) void k_mse_table(int nc, int npad,
 // clamps the code to [-127, 127].  Since fl(thr * inv) lies within a few ulps
 // of 127, min(rint(|x| * inv), 127) is that code's magnitude for every x, and
 // the error of -x is the negated error of x, so its square is the same.  NaN
-// stays NaN (a - q * scale).  The products are contracted into fmas.
+// stays NaN (a - q * scale).  Built without contraction, q * scale, the
+// difference, its square and the sum each round once, as in the reference.
 __device__ __forceinline__ double mse_term(double a, double scale, double inv) {
     const double q = __builtin_fmin(__builtin_rint(a * inv), 127.0);
     const double d = a - q * scale;
