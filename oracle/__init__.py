@@ -103,6 +103,14 @@ def _declare(L: C.CDLL) -> None:
         "tkvo_dequantize_linear": (I32, [P, I64, P, I64, I64, I64, I64, I64, P]),
         "tkvo_dynamic_quantize_linear": (I32, [P, I64, P, P, P]),
         "tkvo_quantized_gemm_node": (I32, [P, P, P, I64, P, I64, I64, I64, F32, F32, P, I64, I32]),
+        "tkvo_quantize_int4_grouped": (I32, [P, I64, I64, I64, I64, P, I64, P]),
+        "tkvo_dequantize_int4_grouped": (I32, [P, I64, P, I64, I64, I64, I64, P, I64]),
+        "tkvo_quantize_int4_grouped_asym": (I32, [P, I64, I64, I64, I64, P, I64, P, P]),
+        "tkvo_dequantize_int4_grouped_asym": (I32, [P, I64, P, I64, I64, I64, I64, P, P, I64]),
+        "tkvo_permute_cols": (I32, [P, I64, I64, P, I64, I32, P]),
+        "tkvo_matmul_int4_grouped": (I32, [P, P, P, I64, P, I64, I64, I64, I64, P, I64, P]),
+        "tkvo_f16_to_f32": (F32, [I64]),
+        "tkvo_dequantize_gguf": (I32, [P, I64, I64, I32, P]),
         "tkvo_lcg31": (I64, [I64]),
         "tkvo_gi_noise": (None, [P, I64, I64, F64]),
         "tkvo_add_outliers": (None, [P, I64, I64, I64, I64, F64]),
@@ -411,3 +419,103 @@ def quantized_gemm_node(aq, wq, bias, m, n, k, scale_a, scale_b, scales_w, recip
     if rc != 0:
         raise ValueError("scales_w smaller than N")
     return y
+
+
+# ---- int4.tkv: grouped INT4 -------------------------------------------------
+
+def _i64(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.int64)
+
+
+def _groups(rows: int, cols: int, group_size: int) -> int:
+    return max(int(rows) * (int(cols) // int(group_size)), 1) if int(group_size) > 0 else 1
+
+
+def quantize_int4_grouped(src, rows: int, cols: int, group_size: int, npacked=None):
+    """(packed int32 bytes [rows * cols / 2], scales f32 [rows * cols / group_size])."""
+    x = _f32(src)
+    packed = np.zeros(int(npacked) if npacked is not None else max(int(rows) * (int(cols) // 2), 1),
+                      np.int32)
+    scales = np.zeros(_groups(rows, cols, group_size), np.float32)
+    rc = lib().tkvo_quantize_int4_grouped(_p(x), x.size, int(rows), int(cols), int(group_size),
+                                          _p(packed), packed.size, _p(scales))
+    if rc != 0:
+        raise ValueError("cols must be a multiple of group_size and even; src / packed sizes")
+    return packed, scales
+
+
+def dequantize_int4_grouped(packed, rows: int, cols: int, group_size: int, scales) -> np.ndarray:
+    pk, sc = _i32(packed), _f32(scales)
+    y = np.zeros(max(int(rows) * int(cols), 1), np.float32)
+    rc = lib().tkvo_dequantize_int4_grouped(_p(pk), pk.size, _p(y), y.size, int(rows), int(cols),
+                                            int(group_size), _p(sc), sc.size)
+    if rc != 0:
+        raise ValueError("scales smaller than rows*num_groups / dst too small")
+    return y[: int(rows) * int(cols)]
+
+
+def quantize_int4_grouped_asym(src, rows: int, cols: int, group_size: int):
+    """(packed, scales f32, zero points int64), one scale / zero point per group."""
+    x = _f32(src)
+    packed = np.zeros(max(int(rows) * (int(cols) // 2), 1), np.int32)
+    scales = np.zeros(_groups(rows, cols, group_size), np.float32)
+    zps = np.zeros(scales.size, np.int64)
+    rc = lib().tkvo_quantize_int4_grouped_asym(_p(x), x.size, int(rows), int(cols),
+                                               int(group_size), _p(packed), packed.size,
+                                               _p(scales), _p(zps))
+    if rc != 0:
+        raise ValueError("cols must be a multiple of group_size and even; src / packed sizes")
+    return packed, scales, zps
+
+
+def dequantize_int4_grouped_asym(packed, rows, cols, group_size, scales, zps) -> np.ndarray:
+    pk, sc, zp = _i32(packed), _f32(scales), _i64(zps)
+    y = np.zeros(max(int(rows) * int(cols), 1), np.float32)
+    rc = lib().tkvo_dequantize_int4_grouped_asym(_p(pk), pk.size, _p(y), y.size, int(rows),
+                                                 int(cols), int(group_size), _p(sc), _p(zp),
+                                                 min(sc.size, zp.size))
+    if rc != 0:
+        raise ValueError("scales / zps smaller than rows*num_groups")
+    return y[: int(rows) * int(cols)]
+
+
+def permute_cols(src, rows: int, cols: int, perm, inverse: bool = False) -> np.ndarray:
+    x, pm = _f32(src), _i64(perm)
+    y = np.zeros(max(int(rows) * int(cols), 1), np.float32)
+    rc = lib().tkvo_permute_cols(_p(x), int(rows), int(cols), _p(pm), pm.size, int(bool(inverse)),
+                                 _p(y))
+    if rc != 0:
+        raise ValueError("perm length must equal cols")
+    return y[: int(rows) * int(cols)]
+
+
+def matmul_int4_grouped(a, packed_w, bias, m, n, k, group_size, scales_w, perm=None) -> np.ndarray:
+    A, W, S = _f32(a), _i32(packed_w), _f32(scales_w)
+    b, nb = _bias(bias)
+    y = np.zeros(max(int(m) * int(n), 1), np.float32)
+    pm = _i64(perm) if perm is not None else None
+    rc = lib().tkvo_matmul_int4_grouped(_p(A), _p(W), _p(b), nb, _p(y),
+                                        int(m), int(n), int(k), int(group_size), _p(S), S.size,
+                                        _p(pm) if pm is not None else None)
+    if rc != 0:
+        raise ValueError("scales_w smaller than N*num_groups")
+    return y[: int(m) * int(n)]
+
+
+# ---- gguf.tkv: block formats -------------------------------------------------
+
+GGUF_Q4_0, GGUF_Q4_1, GGUF_Q8_0 = 2, 3, 8
+
+
+def f16_to_f32(h: int) -> np.float32:
+    return np.float32(lib().tkvo_f16_to_f32(int(h)))
+
+
+def dequantize_gguf(raw, n: int, dtype: int) -> np.ndarray:
+    r = np.ascontiguousarray(np.frombuffer(bytes(raw), np.uint8) if not isinstance(raw, np.ndarray)
+                             else raw, dtype=np.uint8)
+    y = np.zeros(max(int(n), 1), np.float32)
+    rc = lib().tkvo_dequantize_gguf(_p(r), r.size, int(n), int(dtype), _p(y))
+    if rc != 0:
+        raise ValueError("unsupported dtype or raw too short")
+    return y[: int(n)]

@@ -822,6 +822,257 @@ int32_t tkvo_quantized_gemm_node(const int32_t* aq, const int32_t* wq,
 }
 
 /* ===================================================================== */
+/* tv/quantization/int4.tkv: grouped INT4 (symmetric and AWQ-asym)       */
+/* ===================================================================== */
+
+/* int4.tkv:22-33 (_int4_scales_sym) and 36-57.  Per row and group, am =
+ * max |x| (f64 local), floored at 1e-8, scale = fl32(am / 7.0) (appended to a
+ * list[f32]).  Each pair (c, c + 1), c even, is coded with the scale of
+ * group c / group_size (the reference indexes the pair by its even column),
+ * inv = 1.0 / scale in f64, q = clamp(int(round(x * inv)), -8, 7) + 8, and
+ * the byte (q1 << 4) | q0 goes to packed[r * cols / 2 + c / 2].  Entries of
+ * packed past rows * cols / 2 are zeroed (the reference clears the whole
+ * list first). */
+int32_t tkvo_quantize_int4_grouped(const float* src, int64_t nsrc, int64_t rows, int64_t cols,
+                                   int64_t group_size, int32_t* packed, int64_t npacked,
+                                   float* scales) {
+    if (group_size <= 0 || cols % group_size != 0 || cols % 2 != 0) return TKVO_ERR_ARG;
+    if (nsrc < rows * cols || npacked < rows * (cols / 2)) return TKVO_ERR_ARG;
+    const int64_t ng = cols / group_size, half = cols / 2;
+    for (int64_t i = 0; i < npacked; i++) packed[i] = 0;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t g = 0; g < ng; g++) {
+            double am = 0.0;
+            for (int64_t c = 0; c < group_size; c++) {
+                double a = fabs((double)src[r * cols + g * group_size + c]);
+                if (a > am) am = a;
+            }
+            if (am < 0.00000001) am = 0.00000001;
+            scales[r * ng + g] = (float)(am / 7.0);
+        }
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c += 2) {
+            const double sc = (double)scales[r * ng + c / group_size];
+            const double inv = 1.0 / sc;
+            int64_t q0 = clamp_i64(net_to_i64(net_round((double)src[r * cols + c] * inv)), -8, 7) + 8;
+            int64_t q1 =
+                clamp_i64(net_to_i64(net_round((double)src[r * cols + c + 1] * inv)), -8, 7) + 8;
+            packed[r * half + c / 2] = (int32_t)((q1 << 4) | q0);
+        }
+    return 0;
+}
+
+/* int4.tkv:60-73: dst[c] = fl32(float(nibble - 8) * scale), the pair's
+ * scale again that of group c / group_size. */
+int32_t tkvo_dequantize_int4_grouped(const int32_t* packed, int64_t npacked, float* dst,
+                                     int64_t ndst, int64_t rows, int64_t cols,
+                                     int64_t group_size, const float* scales, int64_t nscales) {
+    if (group_size <= 0 || cols % 2 != 0) return TKVO_ERR_ARG;
+    const int64_t ng = cols / group_size, half = cols / 2;
+    if (nscales < rows * ng || ndst < rows * cols || npacked < rows * half) return TKVO_ERR_ARG;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c += 2) {
+            const double sc = (double)scales[r * ng + c / group_size];
+            const int64_t b = packed[r * half + c / 2];
+            dst[r * cols + c] = (float)((double)((b & 0xF) - 8) * sc);
+            dst[r * cols + c + 1] = (float)((double)(((b >> 4) & 0xF) - 8) * sc);
+        }
+    return 0;
+}
+
+/* int4.tkv:77-157.  Per row and group: mn / mx of the group (f64 locals),
+ * mx = mn + 1e-8 for a flat group, sc = (mx - mn) / 15, zp = clamp(int(round(
+ * -mn / sc)), 0, 15); an all-positive group (zp 0, mn > 0) takes sc = mx / 15
+ * (floored at 1e-8), zp 15 takes sc = -mn / 15; sc floored at 1e-8 and stored
+ * as f32.  Codes: mn = -zp * fl32(sc) (f64), q = clamp(int(round((x - mn) /
+ * sc)), 0, 15), the pair indexed by its even column as above. */
+int32_t tkvo_quantize_int4_grouped_asym(const float* src, int64_t nsrc, int64_t rows,
+                                        int64_t cols, int64_t group_size, int32_t* packed,
+                                        int64_t npacked, float* scales, int64_t* zps) {
+    if (group_size <= 0 || cols % group_size != 0 || cols % 2 != 0) return TKVO_ERR_ARG;
+    if (nsrc < rows * cols || npacked < rows * (cols / 2)) return TKVO_ERR_ARG;
+    const int64_t ng = cols / group_size, half = cols / 2;
+    for (int64_t i = 0; i < npacked; i++) packed[i] = 0;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t g = 0; g < ng; g++) {
+            double mn = (double)src[r * cols + g * group_size];
+            double mx = mn;
+            for (int64_t c = 1; c < group_size; c++) {
+                const double v = (double)src[r * cols + g * group_size + c];
+                if (v < mn) mn = v;
+                if (v > mx) mx = v;
+            }
+            if (mx - mn < 0.00000001) mx = mn + 0.00000001;
+            double sc = (mx - mn) / 15.0;
+            int64_t zp = net_to_i64(net_round(-mn / sc));
+            if (zp < 0) zp = 0;
+            if (zp > 15) zp = 15;
+            if (zp == 0) {
+                if (mn > 0) {
+                    sc = mx / 15.0;
+                    if (sc < 0.00000001) sc = 0.00000001;
+                    zp = 0;
+                }
+            } else if (zp == 15) {
+                sc = -mn / 15.0;
+            }
+            if (sc < 0.00000001) sc = 0.00000001;
+            scales[r * ng + g] = (float)sc;
+            zps[r * ng + g] = zp;
+        }
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c += 2) {
+            const int64_t gg = c / group_size;
+            const double sc = (double)scales[r * ng + gg];
+            const int64_t zp = zps[r * ng + gg];
+            const double mn = (double)(-zp) * sc;
+            int64_t q0 = clamp_i64(net_to_i64(net_round(((double)src[r * cols + c] - mn) / sc)), 0, 15);
+            int64_t q1 =
+                clamp_i64(net_to_i64(net_round(((double)src[r * cols + c + 1] - mn) / sc)), 0, 15);
+            packed[r * half + c / 2] = (int32_t)((q1 << 4) | q0);
+        }
+    return 0;
+}
+
+/* int4.tkv:160-170: dst = fl32(float(nibble - zp) * scale). */
+int32_t tkvo_dequantize_int4_grouped_asym(const int32_t* packed, int64_t npacked, float* dst,
+                                          int64_t ndst, int64_t rows, int64_t cols,
+                                          int64_t group_size, const float* scales,
+                                          const int64_t* zps, int64_t ngroups) {
+    if (group_size <= 0 || cols % 2 != 0) return TKVO_ERR_ARG;
+    const int64_t ng = cols / group_size, half = cols / 2;
+    if (ngroups < rows * ng || ndst < rows * cols || npacked < rows * half) return TKVO_ERR_ARG;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c += 2) {
+            const int64_t gg = c / group_size;
+            const double sc = (double)scales[r * ng + gg];
+            const int64_t zp = zps[r * ng + gg];
+            const int64_t b = packed[r * half + c / 2];
+            dst[r * cols + c] = (float)((double)((b & 0xF) - zp) * sc);
+            dst[r * cols + c + 1] = (float)((double)(((b >> 4) & 0xF) - zp) * sc);
+        }
+    return 0;
+}
+
+/* int4.tkv:175-192: out[r, c] = src[r, perm[c]] (inverse: out[r, perm[c]] =
+ * src[r, c]).  perm entries must lie in [0, cols). */
+int32_t tkvo_permute_cols(const float* src, int64_t rows, int64_t cols, const int64_t* perm,
+                          int64_t nperm, int32_t inverse, float* out) {
+    if (nperm != cols) return TKVO_ERR_ARG;
+    for (int64_t c = 0; c < cols; c++)
+        if (perm[c] < 0 || perm[c] >= cols) return TKVO_ERR_ARG;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c++) {
+            if (inverse)
+                out[r * cols + perm[c]] = src[r * cols + c];
+            else
+                out[r * cols + c] = src[r * cols + perm[c]];
+        }
+    return 0;
+}
+
+/* int4.tkv:195-239 (matmul_int4_grouped and, with perm != NULL,
+ * matmul_int4_grouped_ordered).  w = float(nibble - 8) * scales_w[n, kk /
+ * group_size] (f64, exact), acc = acc + x * w in f64 over kk in index order
+ * (each product exact: 24 + 4 + 24 bits), y = fl32(acc + bias) with bias 0.0
+ * when nbias == 0.  Nibble kk of row n is byte kk / 2 of that row, low
+ * nibble first.  The unordered form raises when scales_w is short
+ * (int4.tkv:220-221); the ordered form does not check. */
+int32_t tkvo_matmul_int4_grouped(const float* a, const int32_t* packed_w, const float* bias,
+                                 int64_t nbias, float* y, int64_t m, int64_t n, int64_t k,
+                                 int64_t group_size, const float* scales_w, int64_t nscales,
+                                 const int64_t* perm) {
+    if (group_size <= 0) return TKVO_ERR_ARG;
+    const int64_t ng = k / group_size, half = k / 2;
+    if (!perm && nscales < n * ng) return TKVO_ERR_ARG;
+    for (int64_t mm = 0; mm < m; mm++)
+        for (int64_t nn = 0; nn < n; nn++) {
+            double acc = 0.0;
+            for (int64_t kk = 0; kk < k; kk++) {
+                const int64_t b = packed_w[nn * half + kk / 2];
+                const int64_t nib = (kk % 2 == 0) ? (b & 0xF) : ((b >> 4) & 0xF);
+                const double w = (double)(nib - 8) * (double)scales_w[nn * ng + kk / group_size];
+                const double x = (double)a[mm * k + (perm ? perm[kk] : kk)];
+                acc = acc + x * w;
+            }
+            const double bb = nbias > 0 ? (double)bias[nn] : 0.0;
+            y[mm * n + nn] = (float)(acc + bb);
+        }
+    return 0;
+}
+
+/* ===================================================================== */
+/* tv/format/gguf.tkv: Q8_0 / Q4_0 / Q4_1 block decoding                  */
+/* ===================================================================== */
+
+/* IEEE binary16 bits -> f32 (exact for every code; NaN keeps its payload,
+ * quieted).  The reference reads halves through the runtime's
+ * gguf_f16_from_bits builtin (gguf.tkv:636). */
+float tkvo_f16_to_f32(int64_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15 & 1) << 31;
+    const int e = (int)(h >> 10 & 31);
+    uint32_t mant = (uint32_t)(h & 1023);
+    uint32_t bits;
+    if (e == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int shift = 0;
+            while (!(mant & 1024)) {
+                mant <<= 1;
+                shift++;
+            }
+            mant &= 1023;
+            bits = sign | (uint32_t)(127 - 15 + 1 - shift) << 23 | mant << 13;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (mant ? (0x400000u | mant << 13) : 0u);
+    } else {
+        bits = sign | (uint32_t)(e - 15 + 127) << 23 | mant << 13;
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* gguf.tkv:284-313 (_dequant_tensor for dtypes Q8_0 = 8, Q4_0 = 2,
+ * Q4_1 = 3).  n / 32 blocks from raw (little-endian):
+ *   Q8_0 (34 B): f16 d, 32 int8 q        -> out = d * q
+ *   Q4_0 (18 B): f16 d, 16 bytes         -> out[i] = d * ((byte_i & 15) - 8),
+ *                                           out[i + 16] = d * ((byte_i >> 4) - 8)
+ *   Q4_1 (20 B): f16 d, f16 m, 16 bytes  -> d * (byte_i & 15) - m, d * (byte_i >> 4) - m
+ * Products of an f16 and a small integer are exact in f32; Q4_1 rounds the
+ * difference once.  Elements past the last whole block stay 0 (the output
+ * list starts zeroed). */
+int32_t tkvo_dequantize_gguf(const uint8_t* raw, int64_t nraw, int64_t n, int32_t dtype,
+                             float* out) {
+    const int64_t step = dtype == 8 ? 34 : dtype == 2 ? 18 : dtype == 3 ? 20 : 0;
+    if (!step || n < 0) return TKVO_ERR_ARG;
+    const int64_t nb = n / 32;
+    if (nraw < nb * step) return TKVO_ERR_ARG;
+    for (int64_t i = 0; i < n; i++) out[i] = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t* p = raw + b * step;
+        const double d = (double)tkvo_f16_to_f32((int64_t)p[0] | (int64_t)p[1] << 8);
+        if (dtype == 8) {
+            for (int i = 0; i < 32; i++) out[b * 32 + i] = (float)(d * (double)(int8_t)p[2 + i]);
+        } else if (dtype == 2) {
+            for (int i = 0; i < 16; i++) {
+                out[b * 32 + i] = (float)(d * (double)((p[2 + i] & 15) - 8));
+                out[b * 32 + i + 16] = (float)(d * (double)((p[2 + i] >> 4 & 15) - 8));
+            }
+        } else {
+            const double mm = (double)tkvo_f16_to_f32((int64_t)p[2] | (int64_t)p[3] << 8);
+            for (int i = 0; i < 16; i++) {
+                out[b * 32 + i] = (float)(d * (double)(p[4 + i] & 15) - mm);
+                out[b * 32 + i + 16] = (float)(d * (double)(p[4 + i] >> 4 & 15) - mm);
+            }
+        }
+    }
+    return 0;
+}
+
+/* ===================================================================== */
 /* tv/training/gpt2_ref.tkv:1977-1991 input generator                    */
 /* ===================================================================== */
 

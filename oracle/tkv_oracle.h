@@ -12,6 +12,8 @@
  *   tv/quantization/types.tkv    FP8 e4m3 / e5m2 codec
  *   tv/runtime/f32_bits.tkv      f32 <-> f64 bit reinterpretation
  *   tv/runtime/session.tkv       QuantizedGemm / MatMulInteger / ONNX Q-DQ nodes
+ *   tv/quantization/int4.tkv     grouped INT4 (symmetric, AWQ-asym, act-order)
+ *   tv/format/gguf.tkv           GGUF Q8_0 / Q4_0 / Q4_1 block decoding
  *   tv/training/gpt2_ref.tkv     LCG31 + Box-Muller input generator
  *
  * Codes are int32 per element, as the reference stores them (List<int>).
@@ -159,6 +161,32 @@ int32_t tkvo_quantized_gemm_node(const int32_t* aq, const int32_t* wq,
                                  int64_t m, int64_t n, int64_t k, float scale_a,
                                  float scale_b, const float* scales_w,
                                  int64_t nscales, int32_t recipe);
+
+/* ---- int4.tkv: grouped INT4 ------------------------------------------- */
+int32_t tkvo_quantize_int4_grouped(const float* src, int64_t nsrc, int64_t rows, int64_t cols,
+                                   int64_t group_size, int32_t* packed, int64_t npacked,
+                                   float* scales);
+int32_t tkvo_dequantize_int4_grouped(const int32_t* packed, int64_t npacked, float* dst,
+                                     int64_t ndst, int64_t rows, int64_t cols,
+                                     int64_t group_size, const float* scales, int64_t nscales);
+int32_t tkvo_quantize_int4_grouped_asym(const float* src, int64_t nsrc, int64_t rows,
+                                        int64_t cols, int64_t group_size, int32_t* packed,
+                                        int64_t npacked, float* scales, int64_t* zps);
+int32_t tkvo_dequantize_int4_grouped_asym(const int32_t* packed, int64_t npacked, float* dst,
+                                          int64_t ndst, int64_t rows, int64_t cols,
+                                          int64_t group_size, const float* scales,
+                                          const int64_t* zps, int64_t ngroups);
+int32_t tkvo_permute_cols(const float* src, int64_t rows, int64_t cols, const int64_t* perm,
+                          int64_t nperm, int32_t inverse, float* out);
+int32_t tkvo_matmul_int4_grouped(const float* a, const int32_t* packed_w, const float* bias,
+                                 int64_t nbias, float* y, int64_t m, int64_t n, int64_t k,
+                                 int64_t group_size, const float* scales_w, int64_t nscales,
+                                 const int64_t* perm);
+
+/* ---- gguf.tkv: block formats ----------------------------------------- */
+float tkvo_f16_to_f32(int64_t h);
+int32_t tkvo_dequantize_gguf(const uint8_t* raw, int64_t nraw, int64_t n, int32_t dtype,
+                             float* out);
 
 /* ---- gpt2_ref.tkv input generator ------------------------------------ */
 int64_t tkvo_lcg31(int64_t state);

@@ -498,3 +498,191 @@ def test_generator_recurrence_and_moments():
     assert np.array_equal(z, O.gi_noise(200000, 0, 1.0))
     x = O.add_outliers(z, 0.001, 3, 4, 20.0)
     assert int(np.sum(x != z)) == 200
+
+
+# ---------------------------------------------------------------------------
+# grouped INT4 (int4.tkv) and GGUF block formats (gguf.tkv)
+# ---------------------------------------------------------------------------
+
+def _bytes(q):
+    """Pack nibble codes q[c] into the reference's bytes: low nibble = even c."""
+    q = np.asarray(q, np.int64)
+    return ((q[1::2] << 4) | q[0::2]).astype(np.int32)
+
+
+def test_int4_reference_kat():
+    """inference_tests.tkv:634-652 (test_awq_asym_and_fp16): a 1x8 ramp in
+    groups of 4 round-trips within 2 * max(scales); permute / inverse
+    permute restore the data (nonzero data here, zeros in the reference)."""
+    w = np.array([i - 2.0 for i in range(8)], np.float32)
+    pk, sc, zp = O.quantize_int4_grouped_asym(w, 1, 8, 4)
+    assert pk.size == 4 and sc.size == 2 and zp.size == 2
+    y = O.dequantize_int4_grouped_asym(pk, 1, 8, 4, sc, zp)
+    assert np.all(np.abs(w - y) < float(sc.max()) * 2.0)
+    p = np.arange(1, 7, dtype=np.float32)
+    fwd = O.permute_cols(p, 2, 3, [2, 0, 1])
+    assert np.array_equal(fwd, np.array([3, 1, 2, 6, 4, 5], np.float32))   # out[r,c] = src[r,perm[c]]
+    assert np.array_equal(O.permute_cols(fwd, 2, 3, [2, 0, 1], inverse=True), p)
+    with pytest.raises(ValueError):
+        O.permute_cols(p, 2, 3, [0, 1])
+
+
+def test_int4_sym_closed_forms():
+    # group max 7 -> scale exactly 1: codes are round-half-even(x) + 8, low nibble first
+    g = np.array([7.0, -7.0, 3.5, 2.5, -2.5, -0.5, 0.5, 1.5], np.float32)
+    pk, sc = O.quantize_int4_grouped(g, 1, 8, 8)
+    assert sc[0] == np.float32(1.0)
+    q = np.array([7, -7, 4, 2, -2, 0, 0, 2])
+    assert np.array_equal(pk, _bytes(q + 8))
+    assert np.array_equal(O.dequantize_int4_grouped(pk, 1, 8, 8, sc), q.astype(np.float32))
+    # scale = fl32(am / 7); a flat group floors am at 1e-8 and codes to 8
+    _, sc = O.quantize_int4_grouped(np.array([1, 0, 0, 0], np.float32), 1, 4, 4)
+    assert sc[0] == np.float32(1.0 / 7.0)
+    pk, sc = O.quantize_int4_grouped(np.zeros(4, np.float32), 1, 4, 4)
+    assert sc[0] == np.float32(1e-8 / 7.0) and np.all(pk == 0x88)
+    # odd group size: pair (c, c + 1) takes the scale of group c // gs.  Element 3
+    # (group 1, scale 1) is coded with group 0's scale 0.1: 3 / 0.1 clamps to 7.
+    x = np.array([0.7, 0.1, 0.1, 3.0, 7.0, 7.0], np.float32)
+    pk, sc = O.quantize_int4_grouped(x, 1, 6, 3)
+    assert sc[1] == np.float32(1.0)
+    assert np.array_equal(pk, _bytes(np.array([7, 1, 1, 7, 7, 7]) + 8))
+    y = O.dequantize_int4_grouped(pk, 1, 6, 3, sc)
+    assert y[3] == np.float32(7.0 * float(sc[0]))
+    # packed entries past rows * cols / 2 are cleared, as the reference clears the list
+    pk, _ = O.quantize_int4_grouped(g, 1, 8, 8, npacked=7)
+    assert pk.size == 7 and np.all(pk[4:] == 0)
+    with pytest.raises(ValueError):
+        O.quantize_int4_grouped(g, 1, 8, 3)
+
+
+def test_int4_asym_branches():
+    # ramp 0 .. 15 s: zp 0 (mn == 0 is not > 0), sc = (mx - mn) / 15 = s, codes = i
+    s = 0.25
+    pk, sc, zp = O.quantize_int4_grouped_asym((np.arange(16) * s).astype(np.float32), 1, 16, 16)
+    assert sc[0] == np.float32(s) and zp[0] == 0
+    assert np.array_equal(pk, _bytes(np.arange(16)))
+    # all-positive group (int4.tkv:118-137): zp 0 and sc = mx / 15
+    pk, sc, zp = O.quantize_int4_grouped_asym(np.array([2, 3, 4, 5], np.float32), 1, 4, 4)
+    assert zp[0] == 0 and sc[0] == np.float32(5.0 / 15.0)
+    assert np.array_equal(pk, _bytes([6, 9, 12, 15]))
+    # all-negative group: zp clamps to 15, sc = -mn / 15
+    pk, sc, zp = O.quantize_int4_grouped_asym(np.array([-5, -4, -3, -2], np.float32), 1, 4, 4)
+    assert zp[0] == 15 and sc[0] == np.float32(5.0 / 15.0)
+    y = O.dequantize_int4_grouped_asym(pk, 1, 4, 4, sc, zp)
+    assert np.all(np.abs(y - np.array([-5, -4, -3, -2])) <= float(sc[0]) / 2 + 1e-6)
+    # straddling zero: zp = round(-mn / sc) = round(1 / 0.2) = 5
+    pk, sc, zp = O.quantize_int4_grouped_asym(np.array([-1, 0, 1, 2], np.float32), 1, 4, 4)
+    assert zp[0] == 5 and sc[0] == np.float32(0.2)
+    assert np.array_equal(pk, _bytes([0, 5, 10, 15]))
+    # flat group: mx = mn + 1e-8, sc floored at 1e-8
+    pk, sc, zp = O.quantize_int4_grouped_asym(np.full(4, 3.0, np.float32), 1, 4, 4)
+    assert sc[0] == np.float32(max(3.0 / 15.0, 1e-8)) and zp[0] == 0
+
+
+def test_int4_roundtrip_error_bound():
+    """Every element of a group lies within the group's code range, so the
+    round trip errs by at most half a step (plus the f32 rounding of the
+    stored scale): |dq - x| <= sc / 2 (1 + 2^-18)."""
+    rows, cols, gs = 24, 256, 32
+    x = RNG.normal(0, 1, rows * cols).astype(np.float32)
+    x[::37] *= 30
+    x[:gs] = np.abs(x[:gs]) + 0.5       # an all-positive group
+    x[gs:2 * gs] = -np.abs(x[gs:2 * gs]) - 0.5   # an all-negative group
+    ng = cols // gs
+    pk, sc = O.quantize_int4_grouped(x, rows, cols, gs)
+    y = O.dequantize_int4_grouped(pk, rows, cols, gs, sc)
+    step = np.repeat(sc.astype(np.float64), gs)
+    assert np.all(np.abs(y.astype(np.float64) - x) <= step / 2 * (1 + 2.0 ** -18))
+    pk, sc, zp = O.quantize_int4_grouped_asym(x, rows, cols, gs)
+    assert np.all((zp >= 0) & (zp <= 15)) and sc.size == rows * ng
+    y = O.dequantize_int4_grouped_asym(pk, rows, cols, gs, sc, zp)
+    step = np.repeat(sc.astype(np.float64), gs)
+    # zp == 15 reached by rounding (-mn / sc in [14.5, 15)) with mx > 0 takes
+    # sc = -mn / 15, whose range [mn, 0] clips mx <= sc0 / 2 <= (15 / 29) sc
+    err = np.abs(y.astype(np.float64) - x)
+    assert np.all(err <= step * 15 / 29 * (1 + 2.0 ** -18) + 1e-7)
+    g15 = np.repeat(zp == 15, gs)
+    assert np.all(err[~g15] <= step[~g15] / 2 * (1 + 2.0 ** -18) + 1e-7)
+
+
+def _int4_dense(packed, scales, n, k, gs):
+    """Independent decode: nibble kk of row n is byte kk // 2, low nibble first,
+    scaled by the group of kk itself (matmul indexes per element)."""
+    b = np.asarray(packed, np.int64).reshape(n, k // 2)
+    nib = np.empty((n, k), np.int64)
+    nib[:, 0::2], nib[:, 1::2] = b & 15, (b >> 4) & 15
+    sc = np.asarray(scales, np.float64).reshape(n, k // gs)
+    return (nib - 8) * np.repeat(sc, gs, axis=1)
+
+
+def test_int4_matmul_exact_dyadic():
+    """Dyadic activations and power-of-two scales keep every partial sum
+    exact, so any summation order gives the reference's value: bit-exact
+    against an independent dense decode + f64 matmul."""
+    m, n, k, gs = 6, 9, 96, 32
+    a = (RNG.integers(-64, 64, m * k) / 16.0).astype(np.float32)
+    pk = RNG.integers(0, 256, n * k // 2).astype(np.int32)
+    sc = (2.0 ** -RNG.integers(1, 6, n * k // gs)).astype(np.float32)
+    b = (RNG.integers(-8, 8, n) / 8.0).astype(np.float32)
+    w = _int4_dense(pk, sc, n, k, gs)
+    want = (a.astype(np.float64).reshape(m, k) @ w.T + b.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc), want.reshape(-1))
+    want0 = (a.astype(np.float64).reshape(m, k) @ w.T).astype(np.float32)
+    assert np.array_equal(O.matmul_int4_grouped(a, pk, None, m, n, k, gs, sc), want0.reshape(-1))
+    with pytest.raises(ValueError):
+        O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc[:-1])
+
+
+def test_int4_matmul_general_and_ordered():
+    """General data: within the f64 reordering bound of the dense product.
+    The act-order form is the plain form on column-permuted activations, bit
+    for bit (same products in the same order)."""
+    m, n, k, gs = 7, 11, 128, 64
+    a = RNG.normal(0, 1, m * k).astype(np.float32)
+    w = RNG.normal(0, 0.05, n * k).astype(np.float32)
+    pk, sc = O.quantize_int4_grouped(w, n, k, gs)
+    b = RNG.normal(0, 0.1, n).astype(np.float32)
+    y = O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc).astype(np.float64)
+    wd = _int4_dense(pk, sc, n, k, gs)
+    A = a.astype(np.float64).reshape(m, k)
+    ref = (A @ wd.T + b.astype(np.float64)).reshape(-1)
+    bound = k * 2.0 ** -52 * (np.abs(A) @ np.abs(wd).T).reshape(-1) + np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(y - ref) <= bound)
+    perm = RNG.permutation(k)
+    yo = O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc, perm=perm)
+    ap = O.permute_cols(a, m, k, perm)
+    assert np.array_equal(yo, O.matmul_int4_grouped(ap, pk, b, m, n, k, gs, sc))
+
+
+def test_f16_decoder_all_codes():
+    """Every binary16 code against numpy's conversion (NaN as NaN)."""
+    h = np.arange(65536, dtype=np.int64)
+    want = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    got = np.array([O.f16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_gguf_block_known_answers():
+    q = (np.arange(32) * 8 - 128).astype(np.int8)
+    blk8 = np.concatenate([np.array([0x00, 0x38], np.uint8), q.view(np.uint8)])  # d = 0.5
+    neg8 = np.concatenate([np.array([0x00, 0xC0], np.uint8), q.view(np.uint8)])  # d = -2
+    raw = np.concatenate([blk8, neg8])
+    y = O.dequantize_gguf(raw, 70, O.GGUF_Q8_0)                    # 2 blocks + 6 tail zeros
+    assert np.array_equal(y[:32], 0.5 * q.astype(np.float32))
+    assert np.array_equal(y[32:64], -2.0 * q.astype(np.float32))
+    assert np.all(y[64:] == 0)
+    lo, hi = np.arange(16), (np.arange(16) * 7) % 16
+    qs = (hi << 4 | lo).astype(np.uint8)
+    y = O.dequantize_gguf(np.concatenate([np.array([0x00, 0x40], np.uint8), qs]), 32, O.GGUF_Q4_0)
+    assert np.array_equal(y[:16], 2.0 * (lo - 8)) and np.array_equal(y[16:], 2.0 * (hi - 8))
+    y = O.dequantize_gguf(np.concatenate([np.array([0x00, 0x34, 0x00, 0x3E], np.uint8), qs]), 32,
+                          O.GGUF_Q4_1)                             # d = 0.25, m = 1.5
+    assert np.array_equal(y[:16], 0.25 * lo - 1.5) and np.array_equal(y[16:], 0.25 * hi - 1.5)
+    # a subnormal half scale: d = 2^-24 (code 0x0001)
+    y = O.dequantize_gguf(np.concatenate([np.array([0x01, 0x00], np.uint8), q.view(np.uint8)]), 32,
+                          O.GGUF_Q8_0)
+    assert np.array_equal(y, (q.astype(np.float64) * 2.0 ** -24).astype(np.float32))
+    with pytest.raises(ValueError):
+        O.dequantize_gguf(raw[:40], 64, O.GGUF_Q8_0)
