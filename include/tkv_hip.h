@@ -357,6 +357,96 @@ int32_t tkv_hip_weight_info(int64_t handle, void** codes, float** scales, float*
 int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int64_t m,
                                int32_t act_mode, float* y);
 
+/* ======================================================================== */
+/* Grouped INT4 weights (tv/quantization/int4.tkv) and GGUF block formats   */
+/* (tv/format/gguf.tkv).  Host mirrors carry the reference's lists: packed  */
+/* codes as one int32 per byte (low nibble = even column), zero points as   */
+/* int64; device variants take packed bytes [rows, cols / 2].               */
+/* ======================================================================== */
+
+/* quantize_int4_grouped(src, rows, cols, group_size, packed_out, scales_out)
+ * int4.tkv:36-57: per (row, group) scale = fl32(max(max|x|, 1e-8) / 7), codes
+ * clamp(round(x / scale), -8, 7) + 8, the pair (c, c + 1) coded with group
+ * c / group_size; all n_packed entries are cleared first.  BAD_ARG where the
+ * .tkv raises (cols % group_size, odd cols, short src / packed_out) and when
+ * n_scales_out < rows * cols / group_size (the reference appends). */
+int32_t tkv_hip_quantize_int4_grouped(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                                      int64_t group_size, int32_t* packed_out, int64_t n_packed,
+                                      float* scales_out, int64_t n_scales_out);
+/* dequantize_int4_grouped(packed, dst, rows, cols, group_size, scales)
+ * int4.tkv:60-73: dst = fl32((nibble - 8) * scale).  Odd cols: UNSUPPORTED. */
+int32_t tkv_hip_dequantize_int4_grouped(const int32_t* packed, int64_t n_packed, float* dst,
+                                        int64_t n_dst, int64_t rows, int64_t cols,
+                                        int64_t group_size, const float* scales,
+                                        int64_t n_scales);
+/* quantize_int4_grouped_asym(src, rows, cols, group_size, packed_out,
+ * scales_out, zps_out)   int4.tkv:77-157 (AWQ-style scale and zero point per
+ * group, uint4 codes 0..15). */
+int32_t tkv_hip_quantize_int4_grouped_asym(const float* src, int64_t n_src, int64_t rows,
+                                           int64_t cols, int64_t group_size, int32_t* packed_out,
+                                           int64_t n_packed, float* scales_out, int64_t* zps_out,
+                                           int64_t n_groups_out);
+/* dequantize_int4_grouped_asym(packed, dst, rows, cols, group_size, scales, zps)
+ * int4.tkv:160-170: dst = fl32((nibble - zp) * scale). */
+int32_t tkv_hip_dequantize_int4_grouped_asym(const int32_t* packed, int64_t n_packed, float* dst,
+                                             int64_t n_dst, int64_t rows, int64_t cols,
+                                             int64_t group_size, const float* scales,
+                                             const int64_t* zps, int64_t n_groups);
+/* permute_cols(src, rows, cols, perm) / inv_permute_cols   int4.tkv:175-192:
+ * out[r, c] = src[r, perm[c]] (inverse: out[r, perm[c]] = src[r, c]).
+ * BAD_ARG for len(perm) != cols and entries outside [0, cols); the inverse
+ * of a non-permutation (ordered overwrites) is UNSUPPORTED. */
+int32_t tkv_hip_permute_cols(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                             const int64_t* perm, int64_t n_perm, float* out, int64_t n_out);
+int32_t tkv_hip_inv_permute_cols(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                                 const int64_t* perm, int64_t n_perm, float* out, int64_t n_out);
+/* matmul_int4_grouped(pa, packed_w, pbias, py, m, n, k, group_size, scales_w)
+ * int4.tkv:218-239: y = fl32(sum_k a * ((nibble - 8) * scale[n, k / gs]) +
+ * bias) with f64 accumulation (exact products; only the order of the f64
+ * additions differs from the reference's loop).  BAD_ARG when scales_w is
+ * short (int4.tkv:220-221); odd K or K not a multiple of group_size:
+ * UNSUPPORTED. */
+int32_t tkv_hip_matmul_int4_grouped(const float* pa, int64_t n_a, const int32_t* packed_w,
+                                    int64_t n_packed, const float* pbias, int64_t n_bias,
+                                    float* py, int64_t n_y, int64_t m, int64_t n, int64_t k,
+                                    int64_t group_size, const float* scales_w, int64_t n_scales);
+/* matmul_int4_grouped_ordered(..., perm)   int4.tkv:195-215 (GPTQ act-order:
+ * activation column perm[k] meets weight column k; entries outside [0, K)
+ * are UNSUPPORTED). */
+int32_t tkv_hip_matmul_int4_grouped_ordered(const float* pa, int64_t n_a, const int32_t* packed_w,
+                                            int64_t n_packed, const float* pbias, int64_t n_bias,
+                                            float* py, int64_t n_y, int64_t m, int64_t n,
+                                            int64_t k, int64_t group_size, const float* scales_w,
+                                            int64_t n_scales, const int64_t* perm,
+                                            int64_t n_perm);
+/* _dequant_tensor for GGUF dtype 8 (Q8_0), 2 (Q4_0), 3 (Q4_1)
+ * gguf.tkv:284-313: n / 32 blocks of raw (34 / 18 / 20 bytes), elements past
+ * the last whole block 0.  Other dtypes: UNSUPPORTED. */
+#define TKV_HIP_GGUF_Q4_0 2
+#define TKV_HIP_GGUF_Q4_1 3
+#define TKV_HIP_GGUF_Q8_0 8
+int32_t tkv_hip_dequantize_gguf(const uint8_t* raw, int64_t n_raw, int64_t n, int32_t dtype,
+                                float* out, int64_t n_out);
+
+/* Device-pointer variants (asynchronous on the context's stream).  packed:
+ * bytes [rows, cols / 2]; zps NULL selects the symmetric form. */
+int32_t tkv_hip_dev_quantize_int4_grouped(int64_t ctx, const float* src, int64_t rows,
+                                          int64_t cols, int64_t group_size, uint8_t* packed,
+                                          float* scales, int64_t* zps);
+int32_t tkv_hip_dev_dequantize_int4_grouped(int64_t ctx, const uint8_t* packed, int64_t rows,
+                                            int64_t cols, int64_t group_size, const float* scales,
+                                            const int64_t* zps, float* dst);
+int32_t tkv_hip_dev_permute_cols(int64_t ctx, const float* src, int64_t rows, int64_t cols,
+                                 const int64_t* perm, int32_t inverse, float* out);
+/* a f32 [M, K], packed_w bytes [N, K / 2], scales_w f32 [N, K / group_size],
+ * bias and perm may be NULL (perm entries outside [0, K) read 0). */
+int32_t tkv_hip_dev_matmul_int4_grouped(int64_t ctx, const float* a, const uint8_t* packed_w,
+                                        const float* scales_w, const float* bias,
+                                        const int64_t* perm, float* y, int64_t m, int64_t n,
+                                        int64_t k, int64_t group_size);
+int32_t tkv_hip_dev_dequantize_gguf(int64_t ctx, const uint8_t* raw, int64_t n, int32_t dtype,
+                                    float* out);
+
 #ifdef __cplusplus
 }
 #endif

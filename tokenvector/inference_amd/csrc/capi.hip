@@ -773,3 +773,266 @@ int32_t tkv_hip_dev_matmul_fp8_e4m3_fast(int64_t ctx, const uint8_t* a, const ui
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// grouped INT4 (int4.tkv) and GGUF blocks (gguf.tkv:284-313)
+// ---------------------------------------------------------------------------
+
+// Shape checks of the quantizers (int4.tkv:37-44); ZeroDivision for a group
+// size of 0 reads as the same ValueError.
+static int int4_quant_args(int64_t n_src, int64_t rows, int64_t cols, int64_t gs,
+                           int64_t n_packed, int64_t n_groups_out) {
+    if (rows < 0 || cols < 0 || gs <= 0) return set_error(TKV_HIP_BAD_ARG, "bad rows/cols/group_size");
+    if (cols % gs != 0) return set_error(TKV_HIP_BAD_ARG, "cols must be a multiple of group_size");
+    if (cols % 2 != 0) return set_error(TKV_HIP_BAD_ARG, "cols must be even for nibble packing");
+    if (n_src < rows * cols) return set_error(TKV_HIP_BAD_ARG, "src smaller than rows*cols");
+    if (n_packed < rows * (cols / 2)) return set_error(TKV_HIP_BAD_ARG, "packed_out too small");
+    if (n_groups_out < rows * (cols / gs))
+        return set_error(TKV_HIP_BAD_ARG, "scales_out smaller than rows*num_groups");
+    return TKV_HIP_OK;
+}
+
+static int host_int4_quantize(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                              int64_t gs, int32_t* packed_out, int64_t n_packed, float* scales_out,
+                              int64_t* zps_out, int64_t n_groups_out) {
+    TKV_RC_TRY(int4_quant_args(n_src, rows, cols, gs, n_packed, n_groups_out));
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    memset(packed_out, 0, (size_t)n_packed * 4);  // the reference clears the whole list
+    const int64_t bytes = rows * (cols / 2), groups = rows * (cols / gs);
+    if (bytes == 0) return TKV_HIP_OK;
+    void *dx, *dp, *ds, *dz = nullptr;
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)(rows * cols) * 4, &dx));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)bytes * 4, &dp));
+    TKV_RC_TRY(ctx_workspace(c, WS_SMALL, (size_t)groups * 4, &ds));
+    if (zps_out) TKV_RC_TRY(ctx_workspace(c, WS_Y, (size_t)groups * 8, &dz));
+    TKV_RC_TRY(launch_int4_quantize(c, static_cast<const float*>(dx), rows, cols, gs, zps_out != nullptr,
+                                    dp, true, static_cast<float*>(ds), static_cast<int64_t*>(dz)));
+    TKV_HIP_TRY(hipMemcpyAsync(packed_out, dp, (size_t)bytes * 4, hipMemcpyDeviceToHost, c->stream));
+    if (zps_out)
+        TKV_HIP_TRY(hipMemcpyAsync(zps_out, dz, (size_t)groups * 8, hipMemcpyDeviceToHost, c->stream));
+    return download(c, scales_out, ds, (size_t)groups * 4);
+}
+
+// Dequantize: the pair at column c reads group r * ng + c / gs (flat, as the
+// reference indexes); that index and the byte index must lie in the lists.
+static int host_int4_dequantize(const int32_t* packed, int64_t n_packed, float* dst,
+                                int64_t n_dst, int64_t rows, int64_t cols, int64_t gs,
+                                const float* scales, const int64_t* zps, int64_t n_groups) {
+    if (rows < 0 || cols < 0 || gs <= 0) return set_error(TKV_HIP_BAD_ARG, "bad rows/cols/group_size");
+    if (cols % 2 != 0)
+        return set_error(TKV_HIP_UNSUPPORTED, "odd cols: the reference's pairs overlap rows");
+    const int64_t ng = cols / gs, half = cols / 2;
+    if (n_dst < rows * cols) return set_error(TKV_HIP_BAD_ARG, "dst too small");
+    if (n_groups < rows * ng) return set_error(TKV_HIP_BAD_ARG, "scales smaller than rows*num_groups");
+    if (rows * half == 0) return TKV_HIP_OK;
+    if ((rows - 1) * ng + (cols - 2) / gs >= n_groups || n_packed < rows * half)
+        return set_error(TKV_HIP_BAD_ARG, "packed / scales index out of range");
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    const int64_t groups = (rows - 1) * ng + (cols - 2) / gs + 1;
+    void *dp, *ds, *dz = nullptr, *dy;
+    TKV_RC_TRY(upload(c, WS_IN, packed, (size_t)(rows * half) * 4, &dp));
+    TKV_RC_TRY(upload(c, WS_SMALL, scales, (size_t)groups * 4, &ds));
+    if (zps) TKV_RC_TRY(upload(c, WS_A, zps, (size_t)groups * 8, &dz));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)(rows * cols) * 4, &dy));
+    TKV_RC_TRY(launch_int4_dequantize(c, dp, true, rows, cols, gs, static_cast<float*>(ds),
+                                      static_cast<int64_t*>(dz), static_cast<float*>(dy)));
+    return download(c, dst, dy, (size_t)(rows * cols) * 4);
+}
+
+static int host_permute(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                        const int64_t* perm, int64_t n_perm, float* out, int64_t n_out,
+                        bool inverse) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    if (n_perm != cols) return set_error(TKV_HIP_BAD_ARG, "perm length must equal cols");
+    if (n_src < rows * cols || n_out < rows * cols) return set_error(TKV_HIP_BAD_ARG, "span too small");
+    std::vector<char> seen((size_t)cols, 0);
+    for (int64_t i = 0; i < cols; i++) {
+        if (perm[i] < 0 || perm[i] >= cols) return set_error(TKV_HIP_BAD_ARG, "perm entry out of range");
+        if (inverse && seen[(size_t)perm[i]]++)
+            return set_error(TKV_HIP_UNSUPPORTED, "inverse of a non-permutation (ordered overwrites)");
+    }
+    if (rows * cols == 0) return TKV_HIP_OK;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    void *dx, *dp, *dy;
+    TKV_RC_TRY(upload(c, WS_IN, src, (size_t)(rows * cols) * 4, &dx));
+    TKV_RC_TRY(upload(c, WS_SMALL, perm, (size_t)cols * 8, &dp));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)(rows * cols) * 4, &dy));
+    TKV_RC_TRY(launch_permute_cols(c, static_cast<float*>(dx), rows, cols,
+                                   static_cast<int64_t*>(dp), inverse, static_cast<float*>(dy)));
+    return download(c, out, dy, (size_t)(rows * cols) * 4);
+}
+
+// matmul_int4_grouped(_ordered): the HIP path takes even K with whole groups
+// (the reference's own quantizer produces nothing else) and perm entries in
+// [0, K); anything else is UNSUPPORTED so the caller keeps its loop.
+static int host_matmul_int4(const float* pa, int64_t n_a, const int32_t* packed_w,
+                            int64_t n_packed, const float* pbias, int64_t n_bias, float* py,
+                            int64_t n_y, int64_t m, int64_t n, int64_t k, int64_t gs,
+                            const float* scales_w, int64_t n_scales, const int64_t* perm,
+                            int64_t n_perm) {
+    if (m < 0 || n < 0 || k < 0 || gs <= 0) return set_error(TKV_HIP_BAD_ARG, "bad GEMM arguments");
+    const int64_t ng = k / gs, half = k / 2;
+    if (!perm && n_scales < n * ng) return set_error(TKV_HIP_BAD_ARG, "scales_w smaller than N*num_groups");
+    if (n_bias > 0 && n_bias < n) return set_error(TKV_HIP_BAD_ARG, "bias shorter than N");
+    if (n_y < m * n || n_a < m * k || n_packed < n * half || n_scales < n * ng)
+        return set_error(TKV_HIP_BAD_ARG, "span too small");
+    if (k % 2 != 0 || k % gs != 0)
+        return set_error(TKV_HIP_UNSUPPORTED, "matmul_int4: K must be even and a multiple of group_size");
+    if (perm) {
+        if (n_perm < k) return set_error(TKV_HIP_BAD_ARG, "perm shorter than K");
+        for (int64_t i = 0; i < k; i++)
+            if (perm[i] < 0 || perm[i] >= k)
+                return set_error(TKV_HIP_UNSUPPORTED, "perm entry outside [0, K)");
+    }
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    if (m == 0 || n == 0) return TKV_HIP_OK;
+    std::vector<uint8_t> wb((size_t)(n * half));
+    for (size_t i = 0; i < wb.size(); i++) wb[i] = (uint8_t)packed_w[i];  // nibbles are bits 0-7
+    void *da, *dw, *ds, *db = nullptr, *dp = nullptr, *dy;
+    TKV_RC_TRY(upload(c, WS_A, pa, (size_t)(m * k) * 4, &da));
+    TKV_RC_TRY(upload(c, WS_W, wb.data(), wb.size(), &dw));
+    TKV_RC_TRY(upload(c, WS_SMALL, scales_w, (size_t)(n * ng) * 4, &ds));
+    if (n_bias > 0) TKV_RC_TRY(upload(c, WS_IN, pbias, (size_t)n * 4, &db));
+    if (perm) TKV_RC_TRY(upload(c, WS_OUT, perm, (size_t)k * 8, &dp));
+    TKV_RC_TRY(ctx_workspace(c, WS_Y, (size_t)(m * n) * 4, &dy));
+    TKV_RC_TRY(launch_matmul_int4(c, static_cast<float*>(da), static_cast<uint8_t*>(dw),
+                                  static_cast<float*>(ds), static_cast<float*>(db),
+                                  static_cast<int64_t*>(dp), static_cast<float*>(dy), m, n, k, gs));
+    return download(c, py, dy, (size_t)(m * n) * 4);
+}
+
+extern "C" {
+
+int32_t tkv_hip_quantize_int4_grouped(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                                      int64_t group_size, int32_t* packed_out, int64_t n_packed,
+                                      float* scales_out, int64_t n_scales_out) {
+    return host_int4_quantize(src, n_src, rows, cols, group_size, packed_out, n_packed, scales_out,
+                              nullptr, n_scales_out);
+}
+
+int32_t tkv_hip_dequantize_int4_grouped(const int32_t* packed, int64_t n_packed, float* dst,
+                                        int64_t n_dst, int64_t rows, int64_t cols,
+                                        int64_t group_size, const float* scales,
+                                        int64_t n_scales) {
+    return host_int4_dequantize(packed, n_packed, dst, n_dst, rows, cols, group_size, scales,
+                                nullptr, n_scales);
+}
+
+int32_t tkv_hip_quantize_int4_grouped_asym(const float* src, int64_t n_src, int64_t rows,
+                                           int64_t cols, int64_t group_size, int32_t* packed_out,
+                                           int64_t n_packed, float* scales_out, int64_t* zps_out,
+                                           int64_t n_groups_out) {
+    if (!zps_out) return set_error(TKV_HIP_BAD_ARG, "zps_out is NULL");
+    return host_int4_quantize(src, n_src, rows, cols, group_size, packed_out, n_packed, scales_out,
+                              zps_out, n_groups_out);
+}
+
+int32_t tkv_hip_dequantize_int4_grouped_asym(const int32_t* packed, int64_t n_packed, float* dst,
+                                             int64_t n_dst, int64_t rows, int64_t cols,
+                                             int64_t group_size, const float* scales,
+                                             const int64_t* zps, int64_t n_groups) {
+    if (!zps) return set_error(TKV_HIP_BAD_ARG, "zps is NULL");
+    return host_int4_dequantize(packed, n_packed, dst, n_dst, rows, cols, group_size, scales, zps,
+                                n_groups);
+}
+
+int32_t tkv_hip_permute_cols(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                             const int64_t* perm, int64_t n_perm, float* out, int64_t n_out) {
+    return host_permute(src, n_src, rows, cols, perm, n_perm, out, n_out, false);
+}
+
+int32_t tkv_hip_inv_permute_cols(const float* src, int64_t n_src, int64_t rows, int64_t cols,
+                                 const int64_t* perm, int64_t n_perm, float* out, int64_t n_out) {
+    return host_permute(src, n_src, rows, cols, perm, n_perm, out, n_out, true);
+}
+
+int32_t tkv_hip_matmul_int4_grouped(const float* pa, int64_t n_a, const int32_t* packed_w,
+                                    int64_t n_packed, const float* pbias, int64_t n_bias,
+                                    float* py, int64_t n_y, int64_t m, int64_t n, int64_t k,
+                                    int64_t group_size, const float* scales_w, int64_t n_scales) {
+    return host_matmul_int4(pa, n_a, packed_w, n_packed, pbias, n_bias, py, n_y, m, n, k,
+                            group_size, scales_w, n_scales, nullptr, 0);
+}
+
+int32_t tkv_hip_matmul_int4_grouped_ordered(const float* pa, int64_t n_a, const int32_t* packed_w,
+                                            int64_t n_packed, const float* pbias, int64_t n_bias,
+                                            float* py, int64_t n_y, int64_t m, int64_t n,
+                                            int64_t k, int64_t group_size, const float* scales_w,
+                                            int64_t n_scales, const int64_t* perm,
+                                            int64_t n_perm) {
+    if (!perm) return set_error(TKV_HIP_BAD_ARG, "perm is NULL");
+    return host_matmul_int4(pa, n_a, packed_w, n_packed, pbias, n_bias, py, n_y, m, n, k,
+                            group_size, scales_w, n_scales, perm, n_perm);
+}
+
+int32_t tkv_hip_dequantize_gguf(const uint8_t* raw, int64_t n_raw, int64_t n, int32_t dtype,
+                                float* out, int64_t n_out) {
+    const int64_t step = gguf_block_bytes(dtype);
+    if (!step) return set_error(TKV_HIP_UNSUPPORTED, "gguf: only Q8_0, Q4_0 and Q4_1 blocks");
+    if (n < 0 || n_out < n) return set_error(TKV_HIP_BAD_ARG, "bad n / out too small");
+    if (n_raw < n / 32 * step) return set_error(TKV_HIP_BAD_ARG, "raw shorter than n / 32 blocks");
+    if (n == 0) return TKV_HIP_OK;
+    Ctx* c;
+    TKV_RC_TRY(begin_host(&c));
+    void *dr, *dy;
+    TKV_RC_TRY(upload(c, WS_IN, raw, (size_t)(n / 32 * step), &dr));
+    TKV_RC_TRY(ctx_workspace(c, WS_OUT, (size_t)n * 4, &dy));
+    TKV_RC_TRY(launch_gguf_blocks(c, static_cast<uint8_t*>(dr), n, dtype, static_cast<float*>(dy)));
+    return download(c, out, dy, (size_t)n * 4);
+}
+
+int32_t tkv_hip_dev_quantize_int4_grouped(int64_t ctx, const float* src, int64_t rows,
+                                          int64_t cols, int64_t group_size, uint8_t* packed,
+                                          float* scales, int64_t* zps) {
+    TKV_RC_TRY(int4_quant_args(rows * cols, rows, cols, group_size, rows * (cols / 2),
+                               group_size > 0 ? rows * (cols / group_size) : 0));
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_int4_quantize(c, src, rows, cols, group_size, zps != nullptr, packed, false,
+                                scales, zps);
+}
+
+int32_t tkv_hip_dev_dequantize_int4_grouped(int64_t ctx, const uint8_t* packed, int64_t rows,
+                                            int64_t cols, int64_t group_size, const float* scales,
+                                            const int64_t* zps, float* dst) {
+    if (rows < 0 || cols < 0 || group_size <= 0) return set_error(TKV_HIP_BAD_ARG, "bad rows/cols/group_size");
+    if (cols % 2 != 0) return set_error(TKV_HIP_UNSUPPORTED, "odd cols");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_int4_dequantize(c, packed, false, rows, cols, group_size, scales, zps, dst);
+}
+
+int32_t tkv_hip_dev_permute_cols(int64_t ctx, const float* src, int64_t rows, int64_t cols,
+                                 const int64_t* perm, int32_t inverse, float* out) {
+    if (rows < 0 || cols < 0) return set_error(TKV_HIP_BAD_ARG, "negative rows/cols");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_permute_cols(c, src, rows, cols, perm, inverse != 0, out);
+}
+
+int32_t tkv_hip_dev_matmul_int4_grouped(int64_t ctx, const float* a, const uint8_t* packed_w,
+                                        const float* scales_w, const float* bias,
+                                        const int64_t* perm, float* y, int64_t m, int64_t n,
+                                        int64_t k, int64_t group_size) {
+    if (m < 0 || n < 0 || k < 0 || group_size <= 0) return set_error(TKV_HIP_BAD_ARG, "bad GEMM arguments");
+    if (k % 2 != 0 || k % group_size != 0)
+        return set_error(TKV_HIP_UNSUPPORTED, "matmul_int4: K must be even and a multiple of group_size");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_matmul_int4(c, a, packed_w, scales_w, bias, perm, y, m, n, k, group_size);
+}
+
+int32_t tkv_hip_dev_dequantize_gguf(int64_t ctx, const uint8_t* raw, int64_t n, int32_t dtype,
+                                    float* out) {
+    if (!gguf_block_bytes(dtype)) return set_error(TKV_HIP_UNSUPPORTED, "gguf: only Q8_0, Q4_0 and Q4_1 blocks");
+    if (n < 0) return set_error(TKV_HIP_BAD_ARG, "negative n");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    return launch_gguf_blocks(c, raw, n, dtype, out);
+}
+
+}  // extern "C"

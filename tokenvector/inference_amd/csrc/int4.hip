@@ -1,0 +1,418 @@
+// int4.hip -- grouped INT4 weights (tv/quantization/int4.tkv) and the GGUF
+// block formats that feed quantized linears (tv/format/gguf.tkv:284-313).
+//
+//   group parameters   one wave per (row, group): max |x| (symmetric) or
+//                      min / max (AWQ-asym) by wave reduction, then the
+//                      reference's scalar f64 arithmetic for scale / zp.
+//   pack / unpack      one lane per byte (an even column and its neighbour),
+//                      the pair coded with the scale of group c / group_size
+//                      as in the reference.
+//   INT4 GEMM          y = fl32(sum_k x * ((nibble - 8) * scale) + bias) with
+//                      f64 accumulation on v_mfma_f64_16x16x4_f64.  Every
+//                      product x * w is exact in f64 (24 + 4 + 24 bits), so the
+//                      result differs from the reference's sequential f64 sum
+//                      only by the order of the additions.
+//   GGUF blocks        one lane per output element; f16 scales through the
+//                      hardware conversion (exact for every finite code).
+//
+// Codes are packed bytes on the device ([rows, cols / 2], low nibble = even
+// column); the host mirrors move the reference's int32-per-byte lists.
+#include "tkv_device.h"
+#include "tkv_internal.h"
+
+namespace tkv {
+
+namespace {
+
+constexpr int kI4Block = 256;
+
+// .NET Math.Round (half to even) then the saturating double -> long
+// conversion, clamped to [lo, hi].
+__device__ __forceinline__ int round_clamp(double v, int lo, int hi) {
+    const double r = __builtin_rint(v);
+    if (r != r) return lo > 0 ? lo : (hi < 0 ? hi : 0);  // int(NaN) = 0, then clamped
+    return r < (double)lo ? lo : (r > (double)hi ? hi : (int)r);
+}
+
+// ---------------------------------------------------------------------------
+// group parameters (int4.tkv:22-33 symmetric, 96-147 asymmetric)
+// ---------------------------------------------------------------------------
+
+// One wave per group, groups grid-strided.  Symmetric: am = max |x| floored at
+// 1e-8, scale = fl32(am / 7) (NaN elements never compare greater).  Asym: mn /
+// mx in the reference's scan order, which is the NaN-ignoring min / max unless
+// the group's first element is NaN (then both stay NaN).
+template <bool ASYM>
+__global__ __launch_bounds__(kI4Block) void k_int4_group_params(
+    const float* __restrict__ src, int64_t rows, int64_t cols, int64_t gs, float* __restrict__ scales,
+    int64_t* __restrict__ zps) {
+    const int64_t ng = cols / gs, groups = rows * ng;
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * (kI4Block / 64);
+    for (int64_t q = (int64_t)blockIdx.x * (kI4Block / 64) + (threadIdx.x >> 6); q < groups;
+         q += waves) {
+        const int64_t r = q / ng, g = q - r * ng;
+        const float* x = src + r * cols + g * gs;
+        float a = 0.0f, mn = __builtin_inff(), mx = -__builtin_inff();
+        for (int64_t c = lane; c < gs; c += 64) {
+            const float v = x[c];
+            if (ASYM) {
+                mn = fminf(mn, v);
+                mx = fmaxf(mx, v);
+            } else {
+                a = fmaxf(a, fabsf(v));
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            if (ASYM) {
+                mn = fminf(mn, __shfl_xor(mn, o, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            } else {
+                a = fmaxf(a, __shfl_xor(a, o, 64));
+            }
+        }
+        if (lane != 0) continue;
+        if (!ASYM) {
+            double am = (double)a;
+            if (am < 0.00000001) am = 0.00000001;
+            scales[q] = (float)(am / 7.0);
+            continue;
+        }
+        double dmn = (double)mn, dmx = (double)mx;
+        if (x[0] != x[0]) dmn = dmx = (double)x[0];
+        if (dmx - dmn < 0.00000001) dmx = dmn + 0.00000001;
+        double sc = (dmx - dmn) / 15.0;
+        int zp = round_clamp(-dmn / sc, 0, 15);
+        if (zp == 0) {
+            if (dmn > 0) {
+                sc = dmx / 15.0;
+                if (sc < 0.00000001) sc = 0.00000001;
+                zp = 0;
+            }
+        } else if (zp == 15) {
+            sc = -dmn / 15.0;
+        }
+        if (sc < 0.00000001) sc = 0.00000001;
+        scales[q] = (float)sc;
+        zps[q] = zp;
+    }
+}
+
+// One lane per byte: columns (c, c + 1), c even, coded with group c / gs.
+// Symmetric: q = clamp(round(x * (1.0 / scale)), -8, 7) + 8.  Asym: mn =
+// -zp * scale, q = clamp(round((x - mn) / scale), 0, 15).  OUT32 writes the
+// reference's int32-per-byte list.
+template <bool ASYM, bool OUT32>
+__global__ __launch_bounds__(kI4Block) void k_int4_pack(const float* __restrict__ src,
+                                                        int64_t rows, int64_t cols, int64_t gs,
+                                                        const float* __restrict__ scales,
+                                                        const int64_t* __restrict__ zps,
+                                                        void* __restrict__ packed) {
+    const int64_t half = cols / 2, total = rows * half, ng = cols / gs;
+    const int64_t stride = (int64_t)gridDim.x * kI4Block;
+    for (int64_t i = (int64_t)blockIdx.x * kI4Block + threadIdx.x; i < total; i += stride) {
+        const int64_t r = i / half, c = (i - r * half) * 2;
+        const int64_t gi = r * ng + c / gs;
+        const double sc = (double)scales[gi];
+        const double x0 = (double)src[r * cols + c], x1 = (double)src[r * cols + c + 1];
+        int q0, q1;
+        if (ASYM) {
+            const double mn = (double)(-zps[gi]) * sc;
+            q0 = round_clamp((x0 - mn) / sc, 0, 15);
+            q1 = round_clamp((x1 - mn) / sc, 0, 15);
+        } else {
+            const double inv = 1.0 / sc;
+            q0 = round_clamp(x0 * inv, -8, 7) + 8;
+            q1 = round_clamp(x1 * inv, -8, 7) + 8;
+        }
+        const int b = (q1 << 4) | q0;
+        if (OUT32)
+            static_cast<int32_t*>(packed)[i] = b;
+        else
+            static_cast<uint8_t*>(packed)[i] = (uint8_t)b;
+    }
+}
+
+// dst[c] = fl32(float(nibble - zp) * scale) with zp = 8 (symmetric) or the
+// group's zero point; IN32 reads int32-per-byte lists (low 8 bits).
+template <bool ASYM, bool IN32>
+__global__ __launch_bounds__(kI4Block) void k_int4_unpack(const void* __restrict__ packed,
+                                                          int64_t rows, int64_t cols, int64_t gs,
+                                                          const float* __restrict__ scales,
+                                                          const int64_t* __restrict__ zps,
+                                                          float* __restrict__ dst) {
+    const int64_t half = cols / 2, total = rows * half, ng = cols / gs;
+    const int64_t stride = (int64_t)gridDim.x * kI4Block;
+    for (int64_t i = (int64_t)blockIdx.x * kI4Block + threadIdx.x; i < total; i += stride) {
+        const int64_t r = i / half, c = (i - r * half) * 2;
+        const int64_t gi = r * ng + c / gs;
+        const int64_t b = IN32 ? (int64_t) static_cast<const int32_t*>(packed)[i]
+                               : (int64_t) static_cast<const uint8_t*>(packed)[i];
+        const double sc = (double)scales[gi];
+        const int64_t zp = ASYM ? zps[gi] : 8;
+        dst[r * cols + c] = (float)((double)((b & 0xF) - zp) * sc);
+        dst[r * cols + c + 1] = (float)((double)(((b >> 4) & 0xF) - zp) * sc);
+    }
+}
+
+// out[r, c] = src[r, perm[c]] (INV: out[r, perm[c]] = src[r, c]).  Entries
+// outside [0, cols) gather 0 / are skipped (the host mirror rejects them).
+template <bool INV>
+__global__ __launch_bounds__(kI4Block) void k_permute_cols(const float* __restrict__ src,
+                                                           int64_t rows, int64_t cols,
+                                                           const int64_t* __restrict__ perm,
+                                                           float* __restrict__ out) {
+    const int64_t total = rows * cols, stride = (int64_t)gridDim.x * kI4Block;
+    for (int64_t i = (int64_t)blockIdx.x * kI4Block + threadIdx.x; i < total; i += stride) {
+        const int64_t r = i / cols, c = i - r * cols;
+        const int64_t p = perm[c];
+        const bool ok = p >= 0 && p < cols;
+        if (INV) {
+            if (ok) out[r * cols + p] = src[i];
+        } else {
+            out[i] = ok ? src[r * cols + p] : 0.0f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// INT4 GEMM on f64 MFMA (int4.tkv:195-239)
+// ---------------------------------------------------------------------------
+
+// Workgroup tile 64 x 64 outputs, four waves of 32 x 32 (2 x 2 blocks of
+// v_mfma_f64_16x16x4_f64).  K goes in slices of 32: each slice stages A
+// (f32 -> f64, gathered through perm for the act-order form) and the
+// dequantized weights w = (nibble - 8) * scale[n, k / gs] (f64, exact) in LDS,
+// k-major with a row pitch of 80 doubles: the 4 k-rows one MFMA operand read
+// touches then fall into two halves of the 64 banks.  Operand layouts of the
+// 16x16x4 f64 MFMA: A lane l = row l % 16, k l / 16; B lane l = k l / 16,
+// column l % 16; D lane l, register v holds row l / 16 + 4 v, column l % 16.
+constexpr int kGBM = 64, kGBN = 64, kGBK = 32, kGPitch = 80;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <bool PERM>
+__global__ __launch_bounds__(256) void k_matmul_int4_f64(
+    const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
+    const float* __restrict__ bias, const int64_t* __restrict__ perm, float* __restrict__ Y,
+    int M, int N, int K, int gs) {
+    __shared__ double sA[kGBK][kGPitch];
+    __shared__ double sW[kGBK][kGPitch];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kGBM, n0 = blockIdx.x * kGBN;
+    const int ng = K / gs, half = K / 2;
+    f64x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+    // staging roles: row / column t / 4, k offset (t % 4) * 8 within the slice
+    const int sr = t >> 2, sk = (t & 3) * 8;
+    const int gm = m0 + sr, gn = n0 + sr;
+    for (int k0 = 0; k0 < K; k0 += kGBK) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int kk = k0 + sk + i;
+            float v = 0.0f;
+            if (gm < M && kk < K) {
+                // a perm entry outside [0, K) reads 0 (the host mirror rejects it)
+                const int64_t src_k = PERM ? perm[kk] : (int64_t)kk;
+                if (src_k >= 0 && src_k < K) v = A[(int64_t)gm * K + src_k];
+            }
+            sA[sk + i][sr] = (double)v;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const int kk = k0 + sk + i;  // even
+            double w0 = 0.0, w1 = 0.0;
+            if (gn < N && kk < K) {
+                const int b = Wp[(int64_t)gn * half + kk / 2];
+                w0 = (double)((b & 15) - 8) * (double)scales[(int64_t)gn * ng + kk / gs];
+                w1 = (double)(((b >> 4) & 15) - 8) * (double)scales[(int64_t)gn * ng + (kk + 1) / gs];
+            }
+            sW[sk + i][sr] = w0;
+            sW[sk + i + 1][sr] = w1;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kGBK; kk += 4) {
+            const int kr = kk + (lane >> 4), l16 = lane & 15;
+            const double a0 = sA[kr][wm * 32 + l16], a1 = sA[kr][wm * 32 + 16 + l16];
+            const double b0 = sW[kr][wn * 32 + l16], b1 = sW[kr][wn * 32 + 16 + l16];
+            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + wn * 32 + j * 16 + (lane & 15);
+            if (col >= N) continue;
+            const double b = bias ? (double)bias[col] : 0.0;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = m0 + wm * 32 + i * 16 + (lane >> 4) + 4 * v;
+                if (row < M) Y[(int64_t)row * N + col] = (float)(acc[i][j][v] + b);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// GGUF Q8_0 / Q4_0 / Q4_1 blocks (gguf.tkv:284-313)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float half_at(const uint8_t* p) {
+    const unsigned short h = (unsigned short)(p[0] | (p[1] << 8));
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// One lane per output element of the n / 32 whole blocks; the tail past them
+// is 0.  Products of an f16 scale and a small integer are exact in f32;
+// Q4_1's d * q - m rounds once.
+template <int DT>
+__global__ __launch_bounds__(kI4Block) void k_gguf_blocks(const uint8_t* __restrict__ raw,
+                                                          int64_t n, float* __restrict__ out) {
+    constexpr int STEP = DT == 8 ? 34 : DT == 2 ? 18 : 20;
+    const int64_t full = n / 32 * 32, stride = (int64_t)gridDim.x * kI4Block;
+    for (int64_t i = (int64_t)blockIdx.x * kI4Block + threadIdx.x; i < n; i += stride) {
+        if (i >= full) {
+            out[i] = 0.0f;
+            continue;
+        }
+        const uint8_t* p = raw + (i / 32) * STEP;
+        const int j = (int)(i & 31);
+        const float d = half_at(p);
+        float v;
+        if (DT == 8) {
+            v = d * (float)(int8_t)p[2 + j];
+        } else if (DT == 2) {
+            const int b = p[2 + (j & 15)];
+            v = d * (float)((j < 16 ? (b & 15) : (b >> 4)) - 8);
+        } else {
+            const int b = p[4 + (j & 15)];
+            const double dq = (double)d * (double)(j < 16 ? (b & 15) : (b >> 4));
+            v = (float)(dq - (double)half_at(p + 2));
+        }
+        out[i] = v;
+    }
+}
+
+unsigned grid_for(Ctx* c, int64_t work) {
+    int64_t g = (work + kI4Block - 1) / kI4Block;
+    const int64_t cap = (int64_t)c->num_cus * 8;
+    if (g > cap) g = cap;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
+int launch_int4_quantize(Ctx* c, const float* src, int64_t rows, int64_t cols, int64_t gs,
+                         bool asym, void* packed, bool out32, float* scales, int64_t* zps) {
+    const int64_t groups = rows * (cols / gs);
+    if (groups <= 0) return TKV_HIP_OK;
+    const unsigned gg = grid_for(c, groups * 64);
+    if (asym)
+        hipLaunchKernelGGL(k_int4_group_params<true>, dim3(gg), dim3(kI4Block), 0, c->stream, src,
+                           rows, cols, gs, scales, zps);
+    else
+        hipLaunchKernelGGL(k_int4_group_params<false>, dim3(gg), dim3(kI4Block), 0, c->stream,
+                           src, rows, cols, gs, scales, zps);
+    TKV_LAUNCH_CHECK();
+    const unsigned gp = grid_for(c, rows * (cols / 2));
+#define TKV_PACK(AS, O32)                                                                    \
+    hipLaunchKernelGGL((k_int4_pack<AS, O32>), dim3(gp), dim3(kI4Block), 0, c->stream, src, \
+                       rows, cols, gs, scales, zps, packed)
+    if (asym && out32)
+        TKV_PACK(true, true);
+    else if (asym)
+        TKV_PACK(true, false);
+    else if (out32)
+        TKV_PACK(false, true);
+    else
+        TKV_PACK(false, false);
+#undef TKV_PACK
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+int launch_int4_dequantize(Ctx* c, const void* packed, bool in32, int64_t rows, int64_t cols,
+                           int64_t gs, const float* scales, const int64_t* zps, float* dst) {
+    const int64_t work = rows * (cols / 2);
+    if (work <= 0) return TKV_HIP_OK;
+    const unsigned g = grid_for(c, work);
+#define TKV_UNPACK(AS, I32)                                                                    \
+    hipLaunchKernelGGL((k_int4_unpack<AS, I32>), dim3(g), dim3(kI4Block), 0, c->stream, packed, \
+                       rows, cols, gs, scales, zps, dst)
+    if (zps && in32)
+        TKV_UNPACK(true, true);
+    else if (zps)
+        TKV_UNPACK(true, false);
+    else if (in32)
+        TKV_UNPACK(false, true);
+    else
+        TKV_UNPACK(false, false);
+#undef TKV_UNPACK
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+int launch_permute_cols(Ctx* c, const float* src, int64_t rows, int64_t cols, const int64_t* perm,
+                        bool inverse, float* out) {
+    if (rows * cols <= 0) return TKV_HIP_OK;
+    const unsigned g = grid_for(c, rows * cols);
+    if (inverse)
+        hipLaunchKernelGGL(k_permute_cols<true>, dim3(g), dim3(kI4Block), 0, c->stream, src, rows,
+                           cols, perm, out);
+    else
+        hipLaunchKernelGGL(k_permute_cols<false>, dim3(g), dim3(kI4Block), 0, c->stream, src, rows,
+                           cols, perm, out);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* scales,
+                       const float* bias, const int64_t* perm, float* y, int64_t m, int64_t n,
+                       int64_t k, int64_t gs) {
+    if (m <= 0 || n <= 0) return TKV_HIP_OK;
+    if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX || (n + kGBN - 1) / kGBN > INT32_MAX ||
+        (m + kGBM - 1) / kGBM > 65535)
+        return set_error(TKV_HIP_UNSUPPORTED, "matmul_int4_grouped: sizes beyond the grid");
+    const dim3 grid((unsigned)((n + kGBN - 1) / kGBN), (unsigned)((m + kGBM - 1) / kGBM));
+    if (perm)
+        hipLaunchKernelGGL(k_matmul_int4_f64<true>, grid, dim3(256), 0, c->stream, a, wp, scales,
+                           bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+    else
+        hipLaunchKernelGGL(k_matmul_int4_f64<false>, grid, dim3(256), 0, c->stream, a, wp, scales,
+                           bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+int launch_gguf_blocks(Ctx* c, const uint8_t* raw, int64_t n, int dtype, float* out) {
+    if (n <= 0) return TKV_HIP_OK;
+    const unsigned g = grid_for(c, n);
+    switch (dtype) {
+        case 8:
+            hipLaunchKernelGGL(k_gguf_blocks<8>, dim3(g), dim3(kI4Block), 0, c->stream, raw, n, out);
+            break;
+        case 2:
+            hipLaunchKernelGGL(k_gguf_blocks<2>, dim3(g), dim3(kI4Block), 0, c->stream, raw, n, out);
+            break;
+        case 3:
+            hipLaunchKernelGGL(k_gguf_blocks<3>, dim3(g), dim3(kI4Block), 0, c->stream, raw, n, out);
+            break;
+        default:
+            return set_error(TKV_HIP_UNSUPPORTED, "gguf: only Q8_0, Q4_0 and Q4_1 blocks");
+    }
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+int64_t gguf_block_bytes(int dtype) { return dtype == 8 ? 34 : dtype == 2 ? 18 : dtype == 3 ? 20 : 0; }
+
+}  // namespace tkv

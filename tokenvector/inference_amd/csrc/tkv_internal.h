@@ -162,6 +162,24 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
 // rows of W [rows_w, cols] (both compact).
 int launch_row_sums_i8(Ctx* c, const int8_t* a, int64_t rows_a, const int8_t* w, int64_t rows_w,
                        int64_t cols, int32_t* out);
+
+// Grouped INT4 (int4.hip).  packed: bytes, or int32 per byte (out32 / in32,
+// the reference's list format); zps NULL selects the symmetric form.
+int launch_int4_quantize(Ctx* c, const float* src, int64_t rows, int64_t cols, int64_t gs,
+                         bool asym, void* packed, bool out32, float* scales, int64_t* zps);
+int launch_int4_dequantize(Ctx* c, const void* packed, bool in32, int64_t rows, int64_t cols,
+                           int64_t gs, const float* scales, const int64_t* zps, float* dst);
+int launch_permute_cols(Ctx* c, const float* src, int64_t rows, int64_t cols, const int64_t* perm,
+                        bool inverse, float* out);
+// y[m, n] = fl32(sum_k a[m, perm[k]] * w[n, k] + bias[n]) in f64; K even,
+// a multiple of gs (perm, bias may be NULL).
+int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* scales,
+                       const float* bias, const int64_t* perm, float* y, int64_t m, int64_t n,
+                       int64_t k, int64_t gs);
+// GGUF block decoding, dtype 8 (Q8_0), 2 (Q4_0) or 3 (Q4_1); bytes per
+// 32-element block (0 for any other dtype).
+int launch_gguf_blocks(Ctx* c, const uint8_t* raw, int64_t n, int dtype, float* out);
+int64_t gguf_block_bytes(int dtype);
 // K granularity of the GEMM main loop: operands whose row stride is a
 // multiple of it (and 16-byte aligned) run without repacking.
 int64_t gemm_k_align();

@@ -289,6 +289,38 @@ def matmul_fp8_e4m3(ctx, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias,
                   int(scale_a_stride), _vp(scales_w), _vp(bias), _vp(y)))
 
 
+# ---- grouped INT4 / GGUF blocks (device pointers) ---------------------------
+
+def quantize_int4_grouped(ctx, src, rows, cols, group_size, packed, scales, zps=None) -> None:
+    """packed: bytes [rows, cols / 2]; zps given selects the AWQ-asym form."""
+    _lib.check(_lib.lib().tkv_hip_dev_quantize_int4_grouped(
+        ctx.handle, _vp(src), int(rows), int(cols), int(group_size), _vp(packed), _vp(scales),
+        _vp(zps)))
+
+
+def dequantize_int4_grouped(ctx, packed, rows, cols, group_size, scales, zps, dst) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_dequantize_int4_grouped(
+        ctx.handle, _vp(packed), int(rows), int(cols), int(group_size), _vp(scales), _vp(zps),
+        _vp(dst)))
+
+
+def permute_cols(ctx, src, rows, cols, perm, inverse, out) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_permute_cols(ctx.handle, _vp(src), int(rows), int(cols),
+                                                   _vp(perm), int(bool(inverse)), _vp(out)))
+
+
+def matmul_int4_grouped(ctx, a, packed_w, scales_w, bias, perm, y, m, n, k, group_size) -> None:
+    """y[m, n] = a[m, k] . W_int4[n, k]^T + bias with f64 accumulation."""
+    _lib.check(_lib.lib().tkv_hip_dev_matmul_int4_grouped(
+        ctx.handle, _vp(a), _vp(packed_w), _vp(scales_w), _vp(bias), _vp(perm), _vp(y), int(m),
+        int(n), int(k), int(group_size)))
+
+
+def dequantize_gguf(ctx, raw, n, dtype, out) -> None:
+    _lib.check(_lib.lib().tkv_hip_dev_dequantize_gguf(ctx.handle, _vp(raw), int(n), int(dtype),
+                                                      _vp(out)))
+
+
 class QuantizedLinear:
     """A device-resident quantized weight [N, K] (+ bias) and its forward."""
 
