@@ -37,6 +37,7 @@ PEAK_INT8_TOPS = 5000.0      # MI355X dense INT8 MFMA
 PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
 PEAK_F16_TFLOPS = 2500.0     # MI355X dense FP16 MFMA
 PEAK_HBM_GBPS = 8000.0       # MI355X HBM3E
+PEAK_F64_TFLOPS = 78.6       # MI355X FP64 matrix (v_mfma_f64)
 
 
 def log(*a):
@@ -143,6 +144,7 @@ def run_gpu(steps, warmup):
     fp8 = bench_fp8(ctx, D, O)
     decode = bench_decode(ctx, D, O)
     qlinear = bench_qlinear(ctx, D)
+    int4 = bench_int4(ctx, D, O)
     ctx.close()
     return {
         "ms_per_step": ms_per_step,
@@ -155,6 +157,7 @@ def run_gpu(steps, warmup):
         "fp8": fp8,
         "decode": decode,
         "qlinear": qlinear,
+        "int4": int4,
         "ops_per_step": ops_step,
     }
 
@@ -239,6 +242,64 @@ def bench_qlinear(ctx, D, m=M, reps=20):
                 buf.close()
         w.close()
     out["note"] = "int8 in / int8 out, zero points and requantization fused in the epilogue"
+    return out
+
+
+def bench_int4(ctx, D, O, ms=(1, 32, 8192), gs=128):
+    """Grouped INT4 (int4.tkv) on the four GPT-2 shapes: the GEMM with f64
+    accumulation (exact products; v_mfma_f64_16x16x4_f64, peak 78.6 TFLOP/s)
+    at decode and prefill batches, the symmetric weight quantizer, and GGUF
+    Q8_0 decoding of the same weights.  Weights are quantized once, outside
+    the timed launches; 12 layers' weights are cycled so decode batches stream
+    them from HBM."""
+    out = {}
+    for (name, n, k) in SHAPES:
+        ws = []
+        for l in range(LAYERS):
+            w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 500 + l, 0.02))
+            pk = D.DeviceBuffer.empty(ctx, n * k // 2, np.uint8)
+            sc = D.DeviceBuffer.empty(ctx, n * k // gs, np.float32)
+            D.quantize_int4_grouped(ctx, w, n, k, gs, pk, sc)
+            ws.append((w, pk, sc))
+        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 600, 0.01))
+        for m in ms:
+            dx = D.DeviceBuffer.from_host(ctx, O.gi_noise(m * k, 601, 1.0))
+            dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+            reps = 5 if m > 1024 else 30
+            us = _time_us(ctx, D, lambda i: D.matmul_int4_grouped(
+                ctx, dx, ws[i % LAYERS][1], ws[i % LAYERS][2], b, None, dy, m, n, k, gs), reps)
+            flops = 2.0 * m * n * k
+            nbytes = n * k // 2 + n * k // gs * 4 + 4 * m * k + 4 * m * n
+            tf = flops / (us * 1e-6) / 1e12
+            out[f"gemm_{name}_m{m}"] = {"us": round(us, 2), "tflops_f64": round(tf, 2),
+                                        "frac_of_f64_peak": round(tf / PEAK_F64_TFLOPS, 3),
+                                        "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+            dx.close()
+            dy.close()
+        w, pk, sc = ws[0]
+        us = _time_us(ctx, D, lambda i: D.quantize_int4_grouped(ctx, w, n, k, gs, pk, sc), 20)
+        nbytes = 4 * n * k + n * k // 2 + n * k // gs * 4
+        out[f"quantize_{name}"] = {"us": round(us, 2),
+                                   "frac_of_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 3)}
+        for t in ws:
+            for buf in t:
+                buf.close()
+        b.close()
+    # GGUF Q8_0: 34 bytes per 32 weights in, f32 out (the mlp weights, 12 layers' worth)
+    n = 3072 * 768 * LAYERS
+    raw = np.random.default_rng(3).integers(0, 256, n // 32 * 34).astype(np.uint8)
+    hs = np.float16(np.random.default_rng(4).uniform(1e-3, 2e-3, n // 32)).view(np.uint16)
+    raw.reshape(-1, 34)[:, 0], raw.reshape(-1, 34)[:, 1] = hs & 255, hs >> 8
+    dr = D.DeviceBuffer.from_host(ctx, raw)
+    dy = D.DeviceBuffer.empty(ctx, n, np.float32)
+    us = _time_us(ctx, D, lambda i: D.dequantize_gguf(ctx, dr, n, 8, dy), 20)
+    nbytes = n // 32 * 34 + 4 * n
+    out["gguf_q8_0_decode"] = {"us": round(us, 2), "elements": n,
+                               "frac_of_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 3)}
+    dr.close()
+    dy.close()
+    out["note"] = (f"group_size {gs}; GEMM y = fl32(sum f64 + bias), bytes = int4 weights + scales "
+                   "+ f32 activations and outputs")
     return out
 
 
@@ -457,6 +518,7 @@ def main():
         "fp8": r["fp8"],
         "decode": r["decode"],
         "qlinear": r["qlinear"],
+        "int4": r["int4"],
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_rows)

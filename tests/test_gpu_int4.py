@@ -158,7 +158,8 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
     return 2 * k * 2.0 ** -53 * s.reshape(-1) + np.spacing(np.abs(yref)).astype(np.float64)
 
 
-GEMM_SHAPES = [(1, 100, 64, 32), (5, 37, 96, 32), (70, 130, 256, 64), (33, 2304, 768, 128),
+GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 256, 64),
+               (32, 130, 512, 128), (70, 130, 256, 64), (33, 2304, 768, 128),
                (300, 768, 768, 128), (129, 768, 3072, 32)]
 
 

@@ -8,7 +8,8 @@
 //                      the pair coded with the scale of group c / group_size
 //                      as in the reference.
 //   INT4 GEMM          y = fl32(sum_k x * ((nibble - 8) * scale) + bias) with
-//                      f64 accumulation on v_mfma_f64_16x16x4_f64.  Every
+//                      f64 accumulation on v_mfma_f64_16x16x4_f64 (decode
+//                      batches: one wave per column with f64 FMAs).  Every
 //                      product x * w is exact in f64 (24 + 4 + 24 bits), so the
 //                      result differs from the reference's sequential f64 sum
 //                      only by the order of the additions.
@@ -191,7 +192,11 @@ __global__ __launch_bounds__(kI4Block) void k_permute_cols(const float* __restri
 constexpr int kGBM = 64, kGBN = 64, kGBK = 32, kGPitch = 80;
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-template <bool PERM>
+// The next slice's raw operands are loaded into registers before the current
+// slice's MFMAs, so their latency overlaps the matrix work.  VEC: A rows and W
+// rows allow 16-byte / 4-byte loads (K % 8 == 0, aligned bases, no perm) and
+// every 8-element run of k lies in one group (gs % 8 == 0).
+template <bool PERM, bool VEC>
 __global__ __launch_bounds__(256) void k_matmul_int4_f64(
     const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
     const float* __restrict__ bias, const int64_t* __restrict__ perm, float* __restrict__ Y,
@@ -210,31 +215,63 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
     // staging roles: row / column t / 4, k offset (t % 4) * 8 within the slice
     const int sr = t >> 2, sk = (t & 3) * 8;
     const int gm = m0 + sr, gn = n0 + sr;
+    float ra[8], rs[8];
+    int rb[4];
+    auto fetch = [&](int k0) {
+        const int kb = k0 + sk;
+        if (VEC && gm < M && kb + 7 < K) {
+            const float4* p = reinterpret_cast<const float4*>(A + (int64_t)gm * K + kb);
+            const float4 u = p[0], v = p[1];
+            ra[0] = u.x, ra[1] = u.y, ra[2] = u.z, ra[3] = u.w;
+            ra[4] = v.x, ra[5] = v.y, ra[6] = v.z, ra[7] = v.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int kk = kb + i;
+                float x = 0.0f;
+                if (gm < M && kk < K) {
+                    // a perm entry outside [0, K) reads 0 (the host mirror rejects it)
+                    const int64_t src_k = PERM ? perm[kk] : (int64_t)kk;
+                    if (src_k >= 0 && src_k < K) x = A[(int64_t)gm * K + src_k];
+                }
+                ra[i] = x;
+            }
+        }
+        if (VEC && gn < N && kb + 7 < K) {
+            const uint32_t w4 = *reinterpret_cast<const uint32_t*>(Wp + (int64_t)gn * half + kb / 2);
+            const float sc = scales[(int64_t)gn * ng + kb / gs];
+#pragma unroll
+            for (int i = 0; i < 4; i++) rb[i] = (int)(w4 >> (8 * i)) & 255;
+#pragma unroll
+            for (int i = 0; i < 8; i++) rs[i] = sc;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = kb + 2 * i;  // even
+                int bb = 0x88;              // codes 8: w = 0
+                float s0 = 0.0f, s1 = 0.0f;
+                if (gn < N && kk < K) {
+                    bb = Wp[(int64_t)gn * half + kk / 2];
+                    s0 = scales[(int64_t)gn * ng + kk / gs];
+                    s1 = scales[(int64_t)gn * ng + (kk + 1) / gs];
+                }
+                rb[i] = bb;
+                rs[2 * i] = s0;
+                rs[2 * i + 1] = s1;
+            }
+        }
+    };
+    fetch(0);
     for (int k0 = 0; k0 < K; k0 += kGBK) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int kk = k0 + sk + i;
-            float v = 0.0f;
-            if (gm < M && kk < K) {
-                // a perm entry outside [0, K) reads 0 (the host mirror rejects it)
-                const int64_t src_k = PERM ? perm[kk] : (int64_t)kk;
-                if (src_k >= 0 && src_k < K) v = A[(int64_t)gm * K + src_k];
-            }
-            sA[sk + i][sr] = (double)v;
-        }
+        for (int i = 0; i < 8; i++) sA[sk + i][sr] = (double)ra[i];
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            const int kk = k0 + sk + i;  // even
-            double w0 = 0.0, w1 = 0.0;
-            if (gn < N && kk < K) {
-                const int b = Wp[(int64_t)gn * half + kk / 2];
-                w0 = (double)((b & 15) - 8) * (double)scales[(int64_t)gn * ng + kk / gs];
-                w1 = (double)(((b >> 4) & 15) - 8) * (double)scales[(int64_t)gn * ng + (kk + 1) / gs];
-            }
-            sW[sk + i][sr] = w0;
-            sW[sk + i + 1][sr] = w1;
+        for (int i = 0; i < 4; i++) {
+            sW[sk + 2 * i][sr] = (double)((rb[i] & 15) - 8) * (double)rs[2 * i];
+            sW[sk + 2 * i + 1][sr] = (double)(((rb[i] >> 4) & 15) - 8) * (double)rs[2 * i + 1];
         }
         __syncthreads();
+        if (k0 + kGBK < K) fetch(k0 + kGBK);
 #pragma unroll
         for (int kk = 0; kk < kGBK; kk += 4) {
             const int kr = kk + (lane >> 4), l16 = lane & 15;
@@ -259,6 +296,67 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
                 const int row = m0 + wm * 32 + i * 16 + (lane >> 4) + 4 * v;
                 if (row < M) Y[(int64_t)row * N + col] = (float)(acc[i][j][v] + b);
             }
+        }
+}
+
+// Decode batches (M <= MM <= kGemvRows, MM a power of two): one wave per
+// output column streams that
+// weight row once; lane l takes bytes l, l + 64, ... (k pairs), every row's
+// products are added with f64 FMAs (the products are exact, so each FMA
+// rounds like the reference's add), and the 64 lane sums are combined in a
+// fixed butterfly order.
+constexpr int kGemvRows = 32;
+
+template <int MM, bool PERM>
+__global__ __launch_bounds__(256) void k_gemv_int4_f64(
+    const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
+    const float* __restrict__ bias, const int64_t* __restrict__ perm, float* __restrict__ Y,
+    int M, int N, int K, int gs) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;  // whole waves
+    const int half = K / 2, ng = K / gs;
+    const uint8_t* __restrict__ wr = Wp + (int64_t)n * half;
+    const float* __restrict__ sr = scales + (int64_t)n * ng;
+    double acc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; m++) acc[m] = 0.0;
+    for (int kb = lane; kb < half; kb += 64) {
+        const int b = wr[kb], k0 = 2 * kb;
+        const double w0 = (double)((b & 15) - 8) * (double)sr[k0 / gs];
+        const double w1 = (double)(((b >> 4) & 15) - 8) * (double)sr[(k0 + 1) / gs];
+        int64_t c0 = k0, c1 = k0 + 1;
+        bool ok0 = true, ok1 = true;
+        if (PERM) {
+            c0 = perm[k0];
+            c1 = perm[k0 + 1];
+            ok0 = c0 >= 0 && c0 < K;
+            ok1 = c1 >= 0 && c1 < K;
+        }
+#pragma unroll
+        for (int m = 0; m < MM; m++)
+            if (m < M) {
+                double x0, x1;
+                if (PERM) {
+                    x0 = ok0 ? (double)A[(int64_t)m * K + c0] : 0.0;
+                    x1 = ok1 ? (double)A[(int64_t)m * K + c1] : 0.0;
+                } else {  // K even: the pair is one aligned 8-byte load
+                    const float2 u = *reinterpret_cast<const float2*>(A + (int64_t)m * K + k0);
+                    x0 = (double)u.x;
+                    x1 = (double)u.y;
+                }
+                acc[m] = __builtin_fma(x0, w0, acc[m]);
+                acc[m] = __builtin_fma(x1, w1, acc[m]);
+            }
+    }
+    const double bb = bias ? (double)bias[n] : 0.0;
+#pragma unroll
+    for (int m = 0; m < MM; m++)
+        if (m < M) {
+            double v = acc[m];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+            if (lane == 0) Y[(int64_t)m * N + n] = (float)(v + bb);
         }
 }
 
@@ -382,13 +480,38 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX || (n + kGBN - 1) / kGBN > INT32_MAX ||
         (m + kGBM - 1) / kGBM > 65535)
         return set_error(TKV_HIP_UNSUPPORTED, "matmul_int4_grouped: sizes beyond the grid");
+    if (m <= kGemvRows && (perm || aligned(a, 8))) {
+        const unsigned g = (unsigned)((n + 3) / 4);
+#define TKV_GEMV(MM)                                                                              \
+    if (m <= MM) {                                                                                \
+        if (perm)                                                                                 \
+            hipLaunchKernelGGL((k_gemv_int4_f64<MM, true>), dim3(g), dim3(256), 0, c->stream, a, \
+                               wp, scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);       \
+        else                                                                                      \
+            hipLaunchKernelGGL((k_gemv_int4_f64<MM, false>), dim3(g), dim3(256), 0, c->stream,   \
+                               a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);    \
+        TKV_LAUNCH_CHECK();                                                                       \
+        return TKV_HIP_OK;                                                                        \
+    }
+        TKV_GEMV(1)
+        TKV_GEMV(2)
+        TKV_GEMV(4)
+        TKV_GEMV(8)
+        TKV_GEMV(16)
+        TKV_GEMV(32)
+#undef TKV_GEMV
+    }
     const dim3 grid((unsigned)((n + kGBN - 1) / kGBN), (unsigned)((m + kGBM - 1) / kGBM));
+    const bool vec = !perm && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4);
     if (perm)
-        hipLaunchKernelGGL(k_matmul_int4_f64<true>, grid, dim3(256), 0, c->stream, a, wp, scales,
-                           bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+        hipLaunchKernelGGL((k_matmul_int4_f64<true, false>), grid, dim3(256), 0, c->stream, a, wp,
+                           scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+    else if (vec)
+        hipLaunchKernelGGL((k_matmul_int4_f64<false, true>), grid, dim3(256), 0, c->stream, a, wp,
+                           scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
     else
-        hipLaunchKernelGGL(k_matmul_int4_f64<false>, grid, dim3(256), 0, c->stream, a, wp, scales,
-                           bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+        hipLaunchKernelGGL((k_matmul_int4_f64<false, false>), grid, dim3(256), 0, c->stream, a, wp,
+                           scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
