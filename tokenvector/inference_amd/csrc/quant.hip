@@ -599,7 +599,13 @@ int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_d
                       void* q, bool out_i32) {
     if (n <= 0) return TKV_HIP_OK;
     int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
-    int64_t blocks = stream_blocks(c, vec ? n / 4 : n, vec);
+    // The e4m3 encode is ALU-heavy (about 27 operations per element): six
+    // blocks per CU overlap it with the loads better than the light streams'
+    // two (46.6 against 50.9 us at 201 MB, same box, interleaved medians).
+    int64_t blocks = ceil_div(vec ? n / 4 : n, (int64_t)kBlock * kUnroll);
+    const int64_t cap = (int64_t)c->num_cus * (vec ? 6 : 16);
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
     if (out_i32)
         hipLaunchKernelGGL(k_fp8_encode<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
                            x, n, vec, scaled, q);
