@@ -102,6 +102,25 @@ struct EpiOperands {
         else
             return sa_r[0][0];
     }
+    // A copy whose values pass through an empty asm where the epilogue
+    // starts.  The operands are loaded when the tile starts and used after its
+    // K loop; without this the compiler hoists their first use (a conversion
+    // to f64) next to the loads, and the wait for them there -- vmcnt retires
+    // in issue order -- also waits for every output store of the previous
+    // tile, serialising the stores with this tile's MFMAs.
+    __device__ __forceinline__ EpiOperands pinned() const {
+        EpiOperands o = *this;
+#pragma unroll
+        for (int i = 0; i < (ROWS ? C::TM : 1); i++)
+#pragma unroll
+            for (int r = 0; r < (ROWS ? 16 : 1); r++) o.sa_r[i][r] = pin(o.sa_r[i][r]);
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            o.sw[j] = pin(o.sw[j]);
+            o.b[j] = pin(o.b[j]);
+        }
+        return o;
+    }
 };
 
 // Rows past M read row M - 1 and columns past N column N - 1 (never stored).
@@ -161,7 +180,8 @@ struct EpiI8 {
     // accumulator register r of block (i, j): f32 bits, or the INT32 itself.
     template <class C, class P, class F>
     __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
-                                               const Operands<C>& o, F&& f) const {
+                                               const Operands<C>& o_in, F&& f) const {
+        const Operands<C> o = o_in.pinned();
         if constexpr (MODE == EPI_ACCUM_I32) {
             f([&](int i, int j, int r) { return (uint32_t)pin(acc[i][j][r]); });
         } else if constexpr (MODE == EPI_PER_CHANNEL && RECIPE == TKV_HIP_RECIPE_PRIMARY) {
@@ -249,7 +269,8 @@ struct EpiF8 {
 
     template <class C, class P, class F>
     __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
-                                               const Operands<C>& o, F&& f) const {
+                                               const Operands<C>& o_in, F&& f) const {
+        const Operands<C> o = o_in.pinned();
         f([&](int i, int j, int r) {
             double v = (double)(pin(acc[i][j][r]) * P::kAccScale);
             if (SCALED) {
@@ -314,6 +335,17 @@ struct EpiQL {
     struct Operands {
         int32_t rt[C::TM][16];  // I32: K zpa zpw - zpw ra; else ra
         int32_t ct[C::TN];      // I32: zpa cw; else cw
+        // see EpiOperands::pinned
+        __device__ __forceinline__ Operands pinned() const {
+            Operands o = *this;
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o.rt[i][r] = pin(o.rt[i][r]);
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) o.ct[j] = pin(o.ct[j]);
+            return o;
+        }
     };
 
     // Rows past M read row M - 1 and columns past N column N - 1 (never stored).
@@ -341,7 +373,8 @@ struct EpiQL {
 
     template <class C, class P, class F>
     __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
-                                               const Operands<C>& o, F&& f) const {
+                                               const Operands<C>& o_in, F&& f) const {
+        const Operands<C> o = o_in.pinned();
         if constexpr (I32) {
             // clamp(rint(p) + zpy) == clamp(rint(p), -128 - zpy, 127 - zpy) + zpy for an
             // integer zpy; the launcher takes this path only for a finite mult, so p
