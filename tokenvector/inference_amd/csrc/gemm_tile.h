@@ -410,56 +410,43 @@ __device__ __forceinline__ uint32_t dec2_f16(uint32_t x) {
     return h | ((x & 0x00800080u) << 8);
 }
 
-__device__ __forceinline__ v8h dec8_f16(uint32_t lo, uint32_t hi) {
-    // bytes b0..b3 of lo then b4..b7 of hi -> 8 f16 in K order
-    const uint32_t p0 = dec2_f16(__builtin_amdgcn_perm(0u, lo, 0x0c010c00u));
-    const uint32_t p1 = dec2_f16(__builtin_amdgcn_perm(0u, lo, 0x0c030c02u));
-    const uint32_t p2 = dec2_f16(__builtin_amdgcn_perm(0u, hi, 0x0c010c00u));
-    const uint32_t p3 = dec2_f16(__builtin_amdgcn_perm(0u, hi, 0x0c030c02u));
-    return __builtin_bit_cast(v8h, v4i{(int)p0, (int)p1, (int)p2, (int)p3});
-}
-
-// FP8 with the reference's products: both operands decoded by the
-// reference's decoder into (exact) f16 and multiplied on
-// v_mfma_f32_32x32x16_f16, accumulating at f32-class precision.  The f16 MFMA
-// runs at half the FP8 rate; this is the drop-in path for matmul_fp8_e4m3.
-struct PolicyF8Ref {
+// f16 operands (pre-decoded e4m3 codes, 2 bytes per element) on
+// v_mfma_f32_32x32x16_f16.  A 16-byte LDS chunk holds the 8 halves one lane
+// feeds a 32-byte k-step of that MFMA (lane l: row / column l % 32, halves
+// 8 (l / 32) .. + 7), the same byte layout as the INT8 MFMA's, so the slice
+// is PolicyI8's with the f16 instruction.  kAccScale undoes the decoder's
+// 2^-8 pre-scale on both operands.
+struct PolicyF16 {
     typedef v16f Acc;
-    static constexpr float kAccScale = 65536.0f;  // undo the 2^-8 * 2^-8 pre-scale
+    static constexpr float kAccScale = 65536.0f;
     template <class C>
     __device__ __forceinline__ static void slice(const uint8_t* sa, const uint8_t* sw,
                                                  const int (&a_row)[C::TM],
                                                  const int (&w_row)[C::TN], int khalf,
                                                  Acc (&acc)[C::TM][C::TN]) {
-        constexpr int KS = C::BK / 32;  // 16 K-bytes per lane per 32-K step
+        constexpr int KS = C::BK / 32, D = C::FRAG_DEPTH;
         v4i af[KS][C::TM], bf[KS][C::TN];
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
+        auto load = [&](int ks) {
             const int ch = ks * 2 + khalf;
 #pragma unroll
             for (int i = 0; i < C::TM; i++) af[ks][i] = lds_chunk<C>(sa, a_row[i], ch);
 #pragma unroll
             for (int j = 0; j < C::TN; j++) bf[ks][j] = lds_chunk<C>(sw, w_row[j], ch);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        };
+#pragma unroll
+        for (int ks = 0; ks < D - 1 && ks < KS; ks++) load(ks);
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
+            if (ks + D - 1 < KS) load(ks + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                v8h ah[C::TM], bh[C::TN];
-#pragma unroll
-                for (int i = 0; i < C::TM; i++)
-                    ah[i] = dec8_f16((uint32_t)af[ks][i][2 * h], (uint32_t)af[ks][i][2 * h + 1]);
+            for (int i = 0; i < C::TM; i++)
 #pragma unroll
                 for (int j = 0; j < C::TN; j++)
-                    bh[j] = dec8_f16((uint32_t)bf[ks][j][2 * h], (uint32_t)bf[ks][j][2 * h + 1]);
-#pragma unroll
-                for (int i = 0; i < C::TM; i++)
-#pragma unroll
-                    for (int j = 0; j < C::TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j],
-                                                                           0, 0, 0);
-            }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(v8h, af[ks][i]), __builtin_bit_cast(v8h, bf[ks][j]),
+                        acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 };

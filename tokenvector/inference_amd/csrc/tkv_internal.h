@@ -55,7 +55,7 @@ struct Ctx {
     RedPartial* partials = nullptr;
     tkv_hip_qparams_dev* params = nullptr;  // 64 slots of per-call params
     // grow-only workspaces
-    static constexpr int kSlots = 10;
+    static constexpr int kSlots = 12;  // 10, 11: f16-decoded FP8 operands
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
     bool capturing = false;  // between capture_begin and capture_end
