@@ -160,6 +160,119 @@ def test_calibrators_misaligned_device(ctx, n):
         assert _same_qp(D.read_params(p), O.calibrate_mse(x, 37))
 
 
+def _same_f32_nan(a, b):
+    """Bit-exact, except that any NaN matches any NaN: the sign and payload of
+    a NaN made by arithmetic differ between x86 and the GPU and carry no
+    meaning in the reference."""
+    a = np.asarray(a, np.float32).reshape(-1)
+    b = np.asarray(b, np.float32).reshape(-1)
+    na, nb = np.isnan(a), np.isnan(b)
+    return (a.shape == b.shape and np.array_equal(na, nb)
+            and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
+
+
+def _same_qp_nan(a, b):
+    return a.zero_point == b.zero_point and _same_f32_nan([a.scale, a.min_val, a.max_val],
+                                                         [b.scale, b.min_val, b.max_val])
+
+
+def _nan_cases(n):
+    """NaN first (calibrate_minmax and DynamicQuantizeLinear seed min / max
+    with x[0], so the result is NaN), NaN inside (skipped by every strict
+    comparison), all NaN (the absmax loops that start from 0 give 0), a
+    finite first element before NaN only, and +inf first."""
+    base = _x(n, 71 + n % 13, 1.0)
+    first = base.copy(); first[0] = np.nan
+    inside = base.copy(); inside[n // 2] = np.nan; inside[n - 1] = np.nan
+    fin = np.full(n, np.nan, np.float32); fin[0] = -0.75
+    inf = base.copy(); inf[0] = np.inf; inf[n // 3] = np.nan
+    return {"first": first, "inside": inside, "all": np.full(n, np.nan, np.float32),
+            "finite-first": fin, "inf-first": inf}
+
+
+@pytest.mark.parametrize("n", [2, 1000, 65539, 786432])
+def test_nan_inputs_tensor(ctx, n):
+    """NaN handling of the per-tensor calibrators and the fused calibrate +
+    quantize, against the oracle (engine.tkv:13-36, 165-197, 216-226;
+    session.tkv:2853-2876).  calibrate_kl and calibrate_percentile are left
+    out: the reference's histogram index and heap sort of a NaN are undefined
+    (int(NaN) as a list index, comparisons that are always false)."""
+    say(f"NaN inputs, tensor n={n}")
+    dq = D.DeviceBuffer.empty(ctx, n, np.int8)
+    p = D.params_buffer(ctx)
+    dyn = S.new_node("dyn", S.OperatorType_DynamicQuantizeLinear)
+    for name, x in _nan_cases(n).items():
+        for sym in (1, 0):
+            g, o = Q.calibrate_minmax(x, sym), O.calibrate_minmax(x, sym)
+            assert _same_qp_nan(g, o), (name, sym, g, o)
+        g, o = Q.calibrate_mse(x, 20), O.calibrate_mse(x, 20)
+        assert _same_qp_nan(g, o), (name, "mse", g, o)
+        dx = D.DeviceBuffer.from_host(ctx, x)
+        D.quantize_int8_dynamic_tensor(ctx, dx.ptr, n, dq, p)
+        want = O.calibrate_minmax(x, 1)
+        got = D.read_params(p)
+        assert _same_f32_nan([got.scale, got.min_val, got.max_val],
+                             [want.scale, want.min_val, want.max_val]), (name, got, want)
+        assert np.array_equal(dq.download().astype(np.int32),
+                              O.quantize_int8_symmetric(x, want.scale)), name
+        if n <= 65539:
+            yq, ys, yz = dyn.execute([(x, [n])], [])
+            oq, oys, oyz = O.dynamic_quantize_linear(x)
+            assert np.array_equal(yq, oq) and _same_f32_nan([ys, yz], [oys, oyz]), name
+
+
+@pytest.mark.parametrize("cols", [768, 700, 3072, 37, 4])
+def test_nan_inputs_rows(hip, cols):
+    """Per-row NaN handling: calibrate_per_channel_minmax seeds each row's
+    min / max with its first element (engine.tkv:202-213 -> 13-36);
+    quantize_dynamic_int8_rowwise takes max |x| from 0 (engine.tkv:266-285),
+    so a row of NaN gets the 1e-8 floor.  Row widths cover the register-held
+    row kernel with whole and partial float4 lanes (768, 700, 3072) and the
+    scalar row kernel (37)."""
+    say(f"NaN inputs, rows cols={cols}")
+    rows = 24
+    x = _x(rows * cols, 91 + cols, 1.0).reshape(rows, cols)
+    x[1, 0] = np.nan                    # NaN first
+    x[2, cols // 2] = np.nan            # NaN inside
+    x[3, :] = np.nan                    # all NaN
+    x[4, 1:] = np.nan                   # finite first, then NaN only
+    x[5, 0] = np.inf                    # +inf first
+    x[6, cols - 1] = -np.inf            # -inf last
+    x[7, :] = 0.0                       # all zero: 1e-8 floor
+    x = x.reshape(-1)
+    for sym in (1, 0):
+        g = Q.calibrate_per_channel_minmax(x, rows, cols, sym)
+        o = O.calibrate_per_channel_minmax(x, rows, cols, sym)
+        assert all(_same_qp_nan(a, b) for a, b in zip(g, o)), sym
+    q = np.zeros(rows * cols, np.int32)
+    so = np.zeros(rows, np.float32)
+    Q.quantize_dynamic_int8_rowwise(x, q, rows, cols, so)
+    oq, os_ = O.quantize_dynamic_int8_rowwise(x, rows, cols)
+    assert np.array_equal(q, oq) and _same_f32_nan(so, os_)
+
+
+@pytest.mark.parametrize("rows,cols", [(3 * 8192 + 5, 768), (2 * 8192 + 3, 700), (20000, 256)])
+def test_dynamic_rowwise_many_rows(ctx, rows, cols):
+    """More rows than the row kernel's resident waves (8 blocks of 4 waves
+    per CU), so each wave walks several rows through both register sets and
+    the prefetch past the last row; int8 codes through the device entry point
+    and int32 codes through the host mirror, against the oracle."""
+    say(f"dynamic rowwise many rows {rows}x{cols}")
+    x = _x(rows * cols, 13 + cols, 1.0)
+    x[cols * 7: cols * 8] = 0.0
+    oq, os_ = O.quantize_dynamic_int8_rowwise(x, rows, cols)
+    dx = D.DeviceBuffer.from_host(ctx, x)
+    dq = D.DeviceBuffer.empty(ctx, rows * cols, np.int8)
+    ds = D.DeviceBuffer.empty(ctx, rows, np.float32)
+    D.quantize_dynamic_int8_rowwise(ctx, dx, rows, cols, dq, ds)
+    assert np.array_equal(dq.download().astype(np.int32), oq)
+    assert _same_f32(ds.download(), os_)
+    q = np.zeros(rows * cols, np.int32)
+    so = np.zeros(rows, np.float32)
+    Q.quantize_dynamic_int8_rowwise(x, q, rows, cols, so)
+    assert np.array_equal(q, oq) and _same_f32(so, os_)
+
+
 # ---------------------------------------------------------------------------
 # quantize / dequantize (config 2 shapes)
 # ---------------------------------------------------------------------------

@@ -69,8 +69,11 @@ __global__ __launch_bounds__(kBlock) void k_cal_prep(const float* __restrict__ x
     reduce_partials(x, nparts, track_zero, partials, dmn, dmx);
     for (int64_t i = threadIdx.x; i < hist_len; i += kBlock) hist[i] = 0;
     if (threadIdx.x == 0) {
-        double am = fabs(dmx);
-        if (fabs(dmn) > am) am = fabs(dmn);
+        // max|x| from 0 (engine.tkv:45-49, 170-174) skips NaN; all NaN gives
+        // 0 (the partials then hold min +inf > max -inf).  mn / mx feed the
+        // calibrate_minmax fallback, seeded by x[0].
+        const double am = dmn <= dmx ? fmax(fabs(dmn), fabs(dmx)) : 0.0;
+        nan_first(x, dmn, dmx);
         st->am = am;
         st->bw = num_bins > 0 ? am / (double)num_bins : 0.0;
         st->mn = dmn;

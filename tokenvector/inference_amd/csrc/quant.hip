@@ -117,6 +117,7 @@ __global__ __launch_bounds__(kBlock) void k_minmax_finalize(const float* __restr
                                                             tkv_hip_qparams_dev* __restrict__ out) {
     double dmn, dmx;
     reduce_partials(x, nparts, track_zero, partials, dmn, dmx);
+    nan_first(x, dmn, dmx);
     if (threadIdx.x == 0) finalize_minmax(dmn, dmx, mode, recipe, out);
 }
 
@@ -166,9 +167,12 @@ int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe
 // Per-tensor int8 quantize: q = clamp(rne(x * inv), +-127), inv from params
 // (engine.tkv:216-226).  OUT_I32 writes the reference's int32 codes.
 // ---------------------------------------------------------------------------
+// Low bytes of a, b, c, d as one little-endian word: two byte permutes
+// (selector 0x0c yields a zero byte) and an or.
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-           ((uint32_t)(d & 0xff) << 24);
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
+    return lo | hi;
 }
 
 template <bool OUT_I32>
@@ -202,6 +206,7 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restr
     if constexpr (FUSED) {
         double dmn, dmx;
         reduce_partials(x, nparts, 0, partials, dmn, dmx);
+        nan_first(x, dmn, dmx);
         tkv_hip_qparams_dev prm;
         finalize_minmax(dmn, dmx, MM_SYMMETRIC, recipe, &prm);
         inv = prm.inv;
@@ -334,22 +339,32 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float* __restrict__ x, in
         }
         mn = wave_min(mn);
         mx = wave_max(mx);
+        double dmn = mn, dmx = mx;
         if (mode == RM_CALIBRATE_FULL) {
             zi = wave_min_u64(zi);
             if (lane == 0) {
-                double dmn = mn, dmx = mx;
                 if (tz && zi != ~0ull) {
                     double z = xr[zi];
                     if (mn == 0.0f) dmn = z;
                     if (mx == 0.0f) dmx = z;
                 }
+                nan_first(xr, dmn, dmx);
                 finalize_minmax(dmn, dmx, symmetric ? MM_SYMMETRIC : MM_ASYMMETRIC,
                                 TKV_HIP_RECIPE_PRIMARY, row_params + r);
             }
             return;
         }
-        double am = fabs((double)mx);
-        if (fabs((double)mn) > am) am = fabs((double)mn);
+        double am;
+        if (mode == RM_CALIBRATE) {
+            // calibrate_minmax per row: the row's first element seeds min / max.
+            nan_first(xr, dmn, dmx);
+            am = fabs(dmx);
+            if (fabs(dmn) > am) am = fabs(dmn);
+        } else {
+            // RM_DYNAMIC: am = max |x| from 0 (engine.tkv:272-276), so NaN is
+            // skipped and a row of NaN only gives 0 (min +inf > max -inf).
+            am = mn <= mx ? fmax(fabs(dmn), fabs(dmx)) : 0.0;
+        }
         if (am < 0.00000001) am = 0.00000001;
         double sc = am / 127.0;
         if (mode == RM_CALIBRATE) {
@@ -384,65 +399,89 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float* __restrict__ x, in
 // lane (lane + 64 c), so every row is read from HBM once; with PIPE the next
 // row's loads are issued before the current row is reduced and quantized.
 // Same numerics as k_rows' RM_DYNAMIC branch.
-template <int C4>
-__device__ __forceinline__ void load_row(const float* __restrict__ x, int64_t r, int64_t cols,
+//
+// The loop body is kept free of branches so the next row's loads stay in
+// flight while the current row is processed (a load or store under a lane
+// guard makes the wait before the current row's first use drain every
+// outstanding load and store):
+//  * FULL (cols / 4 == 64 * C4): every lane owns C4 float4, no guard at all;
+//  * otherwise lanes past the row end load the row's last float4 again
+//    (a duplicate element leaves the row's min and max unchanged) and only
+//    the stores are guarded;
+//  * the prefetch past the last row re-reads row rows - 1;
+//  * every lane stores the row's scale (one value, one address).
+template <int C4, bool FULL>
+__device__ __forceinline__ void load_row(const float* x, int64_t r, int64_t cols,
                                          int lane, float4 (&v)[C4]) {
-    const float4* __restrict__ xr = reinterpret_cast<const float4*>(x + r * cols);
+    const int64_t cols4 = cols / 4;
+    const float4* xr = reinterpret_cast<const float4*>(x + r * cols);
 #pragma unroll
-    for (int c = 0; c < C4; c++)
-        if (lane + 64 * c < cols / 4) v[c] = ld4<true>(xr + lane + 64 * c);
+    for (int c = 0; c < C4; c++) {
+        int64_t i = lane + 64 * c;
+        if constexpr (!FULL) i = i < cols4 ? i : cols4 - 1;
+        v[c] = ld4<true>(xr + i);
+    }
 }
 
-template <int C4, bool OUT_I32>
+template <int C4, bool FULL, bool OUT_I32>
 __device__ __forceinline__ void quant_row(const float4 (&v)[C4], int64_t r, int64_t cols, int lane,
-                                          void* __restrict__ q, float* __restrict__ scales_out) {
+                                          void* q, float* scales_out) {
     const int64_t cols4 = cols / 4;
-    float mn = FLT_MAX * 2.0f, mx = -FLT_MAX * 2.0f;
+    // am = max |x| from 0 (engine.tkv:272-276): fmaxf skips NaN as the
+    // reference's strict comparison does, and a row of NaN gives 0.
+    float al = 0.0f;
 #pragma unroll
     for (int c = 0; c < C4; c++)
-        if (lane + 64 * c < cols4) {
-            mn = fminf(fminf(mn, v[c].x), fminf(v[c].y, fminf(v[c].z, v[c].w)));
-            mx = fmaxf(fmaxf(mx, v[c].x), fmaxf(v[c].y, fmaxf(v[c].z, v[c].w)));
-        }
-    mn = wave_min(mn);
-    mx = wave_max(mx);
-    double am = fabs((double)mx);
-    if (fabs((double)mn) > am) am = fabs((double)mn);
+        al = fmaxf(fmaxf(al, fabsf(v[c].x)),
+                   fmaxf(fabsf(v[c].y), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+    double am = (double)wave_max(al);
     if (am < 0.00000001) am = 0.00000001;
     const double sc = am / 127.0;
-    if (lane == 0) scales_out[r] = (float)sc;
+    scales_out[r] = (float)sc;
     const double inv = 1.0 / sc;
     const int64_t base4 = r * cols4;
 #pragma unroll
     for (int c = 0; c < C4; c++)
-        if (lane + 64 * c < cols4)
+        if (FULL || lane + 64 * c < cols4)
             store4<OUT_I32>(q, base4 + lane + 64 * c, rne_clamp((double)v[c].x * inv, -127.0, 127.0),
                             rne_clamp((double)v[c].y * inv, -127.0, 127.0),
                             rne_clamp((double)v[c].z * inv, -127.0, 127.0),
                             rne_clamp((double)v[c].w * inv, -127.0, 127.0));
 }
 
-template <int C4, bool OUT_I32, bool PIPE>
-__global__ __launch_bounds__(kBlock) void k_rows_dynamic(const float* __restrict__ x, int64_t rows,
-                                                         int64_t cols, void* __restrict__ q,
-                                                         float* __restrict__ scales_out) {
+template <int C4, bool FULL, bool OUT_I32, bool PIPE>
+__global__ __launch_bounds__(kBlock) void k_rows_dynamic(const float* x, int64_t rows,
+                                                         int64_t cols, void* q,
+                                                         float* scales_out) {
     const int lane = threadIdx.x & 63;
     const int64_t nw = (int64_t)gridDim.x * (kBlock / 64);
-    int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
-    if (r >= rows) return;
-    float4 cur[C4];
-    load_row<C4>(x, r, cols, lane, cur);
-    for (; r < rows; r += nw) {
-        if constexpr (PIPE) {
-            float4 nxt[C4];
-            if (r + nw < rows) load_row<C4>(x, r + nw, cols, lane, nxt);
-            quant_row<C4, OUT_I32>(cur, r, cols, lane, q, scales_out);
-#pragma unroll
-            for (int c = 0; c < C4; c++) cur[c] = nxt[c];
-        } else {
-            if (r != (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6))
-                load_row<C4>(x, r, cols, lane, cur);
-            quant_row<C4, OUT_I32>(cur, r, cols, lane, q, scales_out);
+    const int64_t r0 = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    if (r0 >= rows) return;
+    float4 a[C4];
+    load_row<C4, FULL>(x, r0, cols, lane, a);
+    if constexpr (PIPE) {
+        // Two register sets in turn: each row's loads are issued one row
+        // ahead and no copy between the sets waits on them.  The pointers
+        // are deliberately not __restrict__: the row's stores may then alias
+        // the input, which keeps the compiler from sinking the prefetch below
+        // them.  The loop is entered after the first row so that at its head
+        // the same memory operations are outstanding on both incoming paths
+        // (the next row's loads, then this row's stores), and the wait for
+        // the next row need not drain the stores.
+        float4 b[C4];
+        load_row<C4, FULL>(x, r0 + nw < rows ? r0 + nw : rows - 1, cols, lane, b);
+        quant_row<C4, FULL, OUT_I32>(a, r0, cols, lane, q, scales_out);
+        for (int64_t r = r0 + nw; r < rows; r += 2 * nw) {
+            load_row<C4, FULL>(x, r + nw < rows ? r + nw : rows - 1, cols, lane, a);
+            quant_row<C4, FULL, OUT_I32>(b, r, cols, lane, q, scales_out);
+            if (r + nw >= rows) break;
+            load_row<C4, FULL>(x, r + 2 * nw < rows ? r + 2 * nw : rows - 1, cols, lane, b);
+            quant_row<C4, FULL, OUT_I32>(a, r + nw, cols, lane, q, scales_out);
+        }
+    } else {
+        for (int64_t r = r0; r < rows; r += nw) {
+            if (r != r0) load_row<C4, FULL>(x, r, cols, lane, a);
+            quant_row<C4, FULL, OUT_I32>(a, r, cols, lane, q, scales_out);
         }
     }
 }
@@ -455,9 +494,15 @@ static bool launch_rows_dynamic(Ctx* c, const float* x, int64_t rows, int64_t co
     const int64_t cap = (int64_t)c->num_cus * 8;
     if (blocks > cap) blocks = cap;
     const dim3 grid((unsigned)blocks), block(kBlock);
-#define TKV_ROWS_DYN(C4, PIPE)                                                               \
-    hipLaunchKernelGGL((k_rows_dynamic<C4, OUT_I32, PIPE>), grid, block, 0, c->stream, x, rows, \
-                       cols, q, scales_out)
+#define TKV_ROWS_DYN(C4, PIPE)                                                                 \
+    do {                                                                                       \
+        if (cols / 4 == 64 * (C4))                                                             \
+            hipLaunchKernelGGL((k_rows_dynamic<C4, true, OUT_I32, PIPE>), grid, block, 0,      \
+                               c->stream, x, rows, cols, q, scales_out);                       \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_rows_dynamic<C4, false, OUT_I32, PIPE>), grid, block, 0,     \
+                               c->stream, x, rows, cols, q, scales_out);                       \
+    } while (0)
     if (per_lane <= 1) TKV_ROWS_DYN(1, true);
     else if (per_lane <= 2) TKV_ROWS_DYN(2, true);
     else if (per_lane <= 3) TKV_ROWS_DYN(3, true);

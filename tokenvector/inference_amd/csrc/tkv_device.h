@@ -13,13 +13,17 @@
 
 namespace tkv {
 
-// clamp(int(round(p)), lo, hi) with the reference's saturating conversion.
+// clamp(int(round(p)), lo, hi) with the reference's saturating conversion;
+// lo and hi are integers within int32 range.  v_cvt_i32_f64 saturates
+// out-of-range values (infinities included) to INT32_MIN / INT32_MAX and
+// converts NaN to 0, so rint, the hardware conversion and an integer med3
+// give the same result as clamping in f64 first.
 __device__ __forceinline__ int rne_clamp(double p, double lo, double hi) {
-    double r = __builtin_rint(p);
-    if (r != r) return 0;
-    r = r < lo ? lo : r;
-    r = r > hi ? hi : r;
-    return (int)r;
+    const double r = __builtin_rint(p);
+    int i;
+    asm("v_cvt_i32_f64 %0, %1" : "=v"(i) : "v"(r));
+    const int l = (int)lo, h = (int)hi;
+    return i < l ? l : (i > h ? h : i);
 }
 
 // e4m3 encode of the reference (types.tkv:154-191 with bias 7, 3 mantissa

@@ -84,6 +84,15 @@ __device__ __forceinline__ void mm_acc(float v, int64_t idx, bool track_zero, fl
     if (track_zero && v == 0.0f && (unsigned long long)idx < zi) zi = (unsigned long long)idx;
 }
 
+// calibrate_minmax and DynamicQuantizeLinear seed their min and max with
+// x[0] and replace them only on a strict comparison (engine.tkv:16-23,
+// session.tkv:2866-2872): a NaN first element stays the result, while NaN
+// anywhere else never compares and is skipped, as fminf / fmaxf skip it.
+__device__ __forceinline__ void nan_first(const float* x, double& dmn, double& dmx) {
+    const float x0 = x[0];
+    if (x0 != x0) dmn = dmx = (double)x0;
+}
+
 // Reduces the per-block partials (every thread of a kBlock-thread block
 // takes part; the result is returned to all of them) to the reference's f64
 // min / max locals.  The reference keeps the first element reaching an
