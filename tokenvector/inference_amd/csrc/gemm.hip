@@ -504,11 +504,15 @@ template <class C, class P, class E>
 __global__ __launch_bounds__(C::THREADS, C::MIN_WAVES_EU) void k_gemm_ws(const uint8_t* __restrict__ A,
                                                         const uint8_t* __restrict__ W, int M,
                                                         int N, int ldk, E ep,
-                                                        void* __restrict__ Y) {
+                                                        void* __restrict__ Y, int stagger) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS_BYTES];
     const int tiles_n = (N + C::BN - 1) / C::BN;
     const int tiles = ((M + C::BM - 1) / C::BM) * tiles_n;
     const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    // Every other workgroup of each XCD starts `stagger` x 1024 cycles late
+    // (see launch_ws).
+    if ((b >> 3) & 1)
+        for (int i = 0; i < stagger; i++) __builtin_amdgcn_s_sleep(16);
     const int my_tiles = b < tiles ? (tiles - 1 - b) / G + 1 : 0;
     const int nk = ldk / C::BK;
     const int total = my_tiles * nk;
@@ -762,6 +766,18 @@ static int launch_cfg(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
     return TKV_HIP_OK;
 }
 
+// Start stagger of the persistent kernel, in units of s_sleep 16 (1024
+// cycles, ~0.4 us).  Every workgroup runs the same sequence of equal tiles, so
+// without it all CUs issue their output stores at the same moments: each
+// burst saturates the HBM write path while the next tile's operand DMA waits
+// behind the stores in the CU's memory pipeline.  Delaying every other
+// workgroup of each XCD by ~1.7 us puts half of the machine's store bursts
+// into the other half's K loops.  Measured over the four GPT-2 shapes at
+// M = 8192 (sum of back-to-back GEMM times, interleaved medians, two boxes):
+// 95.2 and 96.9 us against 97.8 and 99.2 us without; longer delays or four
+// phase groups were slower.  Results do not depend on it.
+constexpr int kStartStagger = 4;
+
 template <class C, class P, class E>
 static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                      int64_t ldk, const E& ep, void* y) {
@@ -770,7 +786,7 @@ static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int6
     const int64_t tiles = tiles_of<C>(m, n);
     const int64_t grid = tiles < resident ? tiles : resident;
     hipLaunchKernelGGL((k_gemm_ws<C, P, E>), dim3((unsigned)grid), dim3(C::THREADS), 0,
-                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y);
+                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, kStartStagger);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
