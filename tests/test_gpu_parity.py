@@ -781,9 +781,13 @@ DECODE_SHAPES = [(m, n, k) for m in (1, 4, 16, 32)
 
 
 def test_linear_forward_per_token(ctx):
-    """Config 5 decode shapes (skinny kernel, M <= 32) plus M = 33 (tiled)."""
+    """Config 5 decode shapes (skinny kernel, M <= 32; for N = 768 with K
+    split over workgroups, whose partial-sum buffer each call must leave
+    cleared for the next), the skinny kernel on N > 4096 columns and on K too
+    short to split, then M = 33 (tiled) and the first shape again."""
     say("linear per-token (decode shapes)")
-    for m, n, k in DECODE_SHAPES + [(33, 768, 768)]:
+    for m, n, k in DECODE_SHAPES + [(4, 8320, 256), (4, 768, 256), (33, 768, 768),
+                                    DECODE_SHAPES[0]]:
         x = _x(m * k, 11, 1.0)
         w = _x(n * k, 12, 0.02)
         b = _x(n, 13, 0.01)
@@ -804,9 +808,10 @@ def test_linear_forward_per_token(ctx):
 @pytest.mark.parametrize("cfg", GEMM_CFGS)
 def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
     """Device QLinearMatMul (fused requantizing epilogue, int8 out) on every
-    GEMM configuration, including the skinny kernel (M <= 32), bit-exact."""
+    GEMM configuration, including the skinny kernel (M <= 32; at N = 768
+    with K split over workgroups), bit-exact."""
     gemm_cfg(cfg)
-    for (m, n, k) in [(37, 100, 200), (1024, 768, 768), (16, 2304, 768)]:
+    for (m, n, k) in [(37, 100, 200), (1024, 768, 768), (16, 2304, 768), (16, 768, 3072)]:
         say(f"dev qlinear cfg={cfg} {m}x{n}x{k}")
         a = RNG.integers(-128, 128, m * k).astype(np.int8)
         w = RNG.integers(-128, 128, n * k).astype(np.int8)   # [N, K] = B transposed

@@ -657,24 +657,39 @@ struct CfgGemv {
 constexpr int kGemvMaxM = 32;
 constexpr int kGemvUnroll = 8;
 
-template <int KW, class E>
+// SPLIT: workgroup b takes column block b % ncb and the K steps of split
+// b / ncb (of `splits`), so narrow N still spreads over the CUs.  Its INT32
+// partial sums go into part[block][1024] with device-scope atomic adds (exact
+// in any order); after a release fence it counts itself into
+// arrivals[block].  The workgroup that completes the count takes the sums
+// with an exchange that also clears them, clears the count, and runs the
+// epilogue: no workgroup ever waits for another, and part / arrivals are
+// zero again when the kernel ends (zeroed at context creation).
+template <int KW, bool SPLIT, class E>
 __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__ A,
                                                      const uint8_t* __restrict__ W, int M, int N,
-                                                     int ldk, E ep, void* __restrict__ Y) {
+                                                     int ldk, E ep, void* __restrict__ Y,
+                                                     int splits, int32_t* __restrict__ part,
+                                                     unsigned* __restrict__ arrivals) {
     __shared__ int32_t red[16 * 64];
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int n0 = blockIdx.x * 32;
+    const int ncb = (N + 31) / 32;
+    const int cb = SPLIT ? (int)blockIdx.x % ncb : (int)blockIdx.x;
+    const int sp = SPLIT ? (int)blockIdx.x / ncb : 0;
+    const int n0 = cb * 32;
     const int r = lane & 31, kh = lane >> 5;
     for (int i = threadIdx.x; i < 16 * 64; i += KW * 64) red[i] = 0;
     const auto eo = ep.template load<CfgGemv>(0, n0, M, N);
     const uint8_t* arow = A + (int64_t)(r < M ? r : M - 1) * ldk + kh * 16;
     const uint8_t* wrow = W + (int64_t)(n0 + r < N ? n0 + r : N - 1) * ldk + kh * 16;
     const int nks = ldk / 32;
+    const int k_lo = SPLIT ? (int)((int64_t)nks * sp / splits) : 0;
+    const int k_hi = SPLIT ? (int)((int64_t)nks * (sp + 1) / splits) : nks;
     v16i acc;
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[i] = 0;
-    int ks = wave;
-    for (; ks + (kGemvUnroll - 1) * KW < nks; ks += kGemvUnroll * KW) {
+    int ks = k_lo + wave;
+    for (; ks + (kGemvUnroll - 1) * KW < k_hi; ks += kGemvUnroll * KW) {
         v4i af[kGemvUnroll], wf[kGemvUnroll];
 #pragma unroll
         for (int u = 0; u < kGemvUnroll; u++) {
@@ -686,27 +701,48 @@ __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__
         for (int u = 0; u < kGemvUnroll; u++)
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[u], wf[u], acc, 0, 0, 0);
     }
-    for (; ks < nks; ks += KW) {
+    for (; ks < k_hi; ks += KW) {
         const v4i af = *reinterpret_cast<const v4i*>(arow + ks * 32);
         const v4i wf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + ks * 32));
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, acc, 0, 0, 0);
     }
     __syncthreads();  // red[] zeroed
-    if (KW == 1) {
-        typename PolicyI8::Acc one[1][1];
-        one[0][0] = acc;
-        ep.template store<CfgGemv, PolicyI8>(one, eo, 0, n0, M, N, Y);
-        return;
-    }
+    typename PolicyI8::Acc sum[1][1];
+    if constexpr (KW == 1) {
+        sum[0][0] = acc;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 16; i++) atomicAdd(&red[i * 64 + lane], acc[i]);
-    __syncthreads();
-    if (wave == 0) {
-        typename PolicyI8::Acc sum[1][1];
+        for (int i = 0; i < 16; i++) atomicAdd(&red[i * 64 + lane], acc[i]);
+        __syncthreads();
+        if (wave != 0) return;
 #pragma unroll
         for (int i = 0; i < 16; i++) sum[0][0][i] = red[i * 64 + lane];
-        ep.template store<CfgGemv, PolicyI8>(sum, eo, 0, n0, M, N, Y);
     }
+    if constexpr (SPLIT) {
+        int32_t* pc = part + (int64_t)cb * 1024;
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            __hip_atomic_fetch_add(pc + i * 64 + lane, sum[0][0][i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        // The adds are device-scope atomics, performed where every XCD sees
+        // them; waiting for their completion (vmcnt counts atomics) before
+        // the arrival is issued orders them before it without a cache
+        // writeback.  The memory clobber keeps the compiler from moving them.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        int last = 0;
+        if (lane == 0)
+            last = __hip_atomic_fetch_add(arrivals + cb, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(splits - 1);
+        // The exchanges below issue only after the arrival has returned.
+        if (!__shfl(last, 0, 64)) return;
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            sum[0][0][i] = __hip_atomic_exchange(pc + i * 64 + lane, 0, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+            __hip_atomic_store(arrivals + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ep.template store<CfgGemv, PolicyI8>(sum, eo, 0, n0, M, N, Y);
 }
 
 // ---- tile configurations ---------------------------------------------------
@@ -793,25 +829,42 @@ static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int6
 
 // Waves per workgroup of the skinny kernel: enough workgroups x waves for
 // the weight stream to fill the machine, but never more waves than K steps.
+// When the column blocks cover at most a quarter of the CUs, K is split
+// over workgroups too (SPLIT kernel): up to one workgroup per CU, at least 8
+// K steps (two per wave) per split.  Per-token decode calls (quantize + GEMM,
+// interleaved medians): mlp_down (N = 768, 24 blocks) 12.3 -> 9.1 us at M = 1
+// and 17.2 -> 10.8 us at M = 32; splitting at half the CUs also took qkv and
+// mlp_up (72 and 96 blocks), which lost 0.4-0.7 us.
 template <class E>
 static int launch_gemv(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                        int64_t ldk, const E& ep, void* y) {
     const int64_t wgs = ceil_div(n, (int64_t)32);
     const int64_t nks = ldk / 32;
+    if (wgs * 4 <= c->num_cus && wgs <= kGemvSplitBlocks) {
+        int64_t splits = ceil_div((int64_t)c->num_cus, wgs);
+        if (splits > nks / 8) splits = nks / 8;
+        if (splits >= 2) {
+            hipLaunchKernelGGL((k_gemv_i8<4, true, E>), dim3((unsigned)(wgs * splits)),
+                               dim3(4 * 64), 0, c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y,
+                               (int)splits, c->gemv_part, c->gemv_arrivals);
+            TKV_LAUNCH_CHECK();
+            return TKV_HIP_OK;
+        }
+    }
     int64_t kw = ceil_div((int64_t)c->num_cus * 8, wgs);
     if (kw > nks) kw = nks;
+#define TKV_GEMV(KW)                                                                          \
+    hipLaunchKernelGGL((k_gemv_i8<KW, false, E>), dim3((unsigned)wgs), dim3(KW * 64), 0,     \
+                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, 1, nullptr, nullptr)
     if (kw >= 16)
-        hipLaunchKernelGGL((k_gemv_i8<16, E>), dim3((unsigned)wgs), dim3(16 * 64), 0, c->stream,
-                           a, w, (int)m, (int)n, (int)ldk, ep, y);
+        TKV_GEMV(16);
     else if (kw >= 8)
-        hipLaunchKernelGGL((k_gemv_i8<8, E>), dim3((unsigned)wgs), dim3(8 * 64), 0, c->stream, a,
-                           w, (int)m, (int)n, (int)ldk, ep, y);
+        TKV_GEMV(8);
     else if (kw >= 4)
-        hipLaunchKernelGGL((k_gemv_i8<4, E>), dim3((unsigned)wgs), dim3(4 * 64), 0, c->stream, a,
-                           w, (int)m, (int)n, (int)ldk, ep, y);
+        TKV_GEMV(4);
     else
-        hipLaunchKernelGGL((k_gemv_i8<1, E>), dim3((unsigned)wgs), dim3(64), 0, c->stream, a, w,
-                           (int)m, (int)n, (int)ldk, ep, y);
+        TKV_GEMV(1);
+#undef TKV_GEMV
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -68,7 +68,9 @@ int ctx_create(int device, Ctx** out) {
         return fail_hip(e, "hipStreamCreateWithFlags", __FILE__, __LINE__);
     }
     c->stream = c->own_stream;
-    size_t red_bytes = sizeof(RedPartial) * kMaxReduceBlocks + 256 + sizeof(tkv_hip_qparams_dev) * 64;
+    const size_t gemv_bytes = (size_t)kGemvSplitBlocks * 1024 * sizeof(int32_t);
+    size_t red_bytes = sizeof(RedPartial) * kMaxReduceBlocks + 256 + sizeof(tkv_hip_qparams_dev) * 64 +
+                       256 + gemv_bytes + (size_t)kGemvSplitBlocks * sizeof(unsigned);
     void* red = nullptr;
     e = hipMalloc(&red, red_bytes);
     if (e != hipSuccess) {
@@ -79,6 +81,8 @@ int ctx_create(int device, Ctx** out) {
     c->partials = static_cast<RedPartial*>(red);
     c->params = reinterpret_cast<tkv_hip_qparams_dev*>(static_cast<char*>(red) +
                                                        sizeof(RedPartial) * kMaxReduceBlocks + 256);
+    c->gemv_part = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(c->params + 64) + 256);
+    c->gemv_arrivals = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(c->gemv_part) + gemv_bytes);
     // One-time zeroing at creation, so params read before any calibration
     // are defined (never inside a caller's stream capture).
     e = hipMemset(red, 0, red_bytes);

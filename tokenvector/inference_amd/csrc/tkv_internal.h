@@ -38,6 +38,8 @@ int fail_hip(hipError_t e, const char* what, const char* file, int line);
 // thread at a time; the default context of each thread is thread_local.
 // ---------------------------------------------------------------------------
 constexpr int kMaxReduceBlocks = 2048;
+// Column blocks (32 columns each) of the split-K skinny GEMM's partial sums.
+constexpr int kGemvSplitBlocks = 128;
 
 struct RedPartial {
     float mn;
@@ -54,6 +56,11 @@ struct Ctx {
     // partials kernel, read by the finalize kernel; no clearing needed)
     RedPartial* partials = nullptr;
     tkv_hip_qparams_dev* params = nullptr;  // 64 slots of per-call params
+    // Split-K skinny GEMM: kGemvSplitBlocks x 1024 INT32 partial sums and
+    // kGemvSplitBlocks arrival counts, zeroed at creation and cleared again
+    // by the kernel that uses them.
+    int32_t* gemv_part = nullptr;
+    unsigned* gemv_arrivals = nullptr;
     // grow-only workspaces
     static constexpr int kSlots = 12;  // 10, 11: f16-decoded FP8 operands
     void* ws[kSlots] = {};
