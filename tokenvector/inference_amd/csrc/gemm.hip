@@ -811,7 +811,9 @@ static int launch_cfg(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
 // into the other half's K loops.  Measured over the four GPT-2 shapes at
 // M = 8192 (sum of back-to-back GEMM times, interleaved medians, two boxes):
 // 95.2 and 96.9 us against 97.8 and 99.2 us without; longer delays or four
-// phase groups were slower.  Results do not depend on it.
+// phase groups were slower.  Epilogues with int8 outputs (QLinearMatMul)
+// store a quarter of the bytes and only lose the delay (attn_out 12.9 ->
+// 15.2 us in a trace): they start unstaggered.  Results do not depend on it.
 constexpr int kStartStagger = 4;
 
 template <class C, class P, class E>
@@ -822,7 +824,8 @@ static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int6
     const int64_t tiles = tiles_of<C>(m, n);
     const int64_t grid = tiles < resident ? tiles : resident;
     hipLaunchKernelGGL((k_gemm_ws<C, P, E>), dim3((unsigned)grid), dim3(C::THREADS), 0,
-                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, kStartStagger);
+                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y,
+                       E::kOut32 ? kStartStagger : 0);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
