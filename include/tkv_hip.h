@@ -78,7 +78,11 @@ int32_t tkv_hip_last_error(char* buf, int32_t len);
 int32_t tkv_hip_ctx_create(int32_t device, int64_t* ctx_out);
 int32_t tkv_hip_ctx_destroy(int64_t ctx);
 /* Use an external hipStream_t (e.g. torch's) for subsequent dev calls;
- * NULL restores the context's own stream. */
+ * NULL restores the context's own stream.  The previous stream is drained
+ * first: work on one context never runs on two streams at once (its calls
+ * share workspaces and the split-K partial sums).  Calls that overlap on one
+ * context from several host threads race on those buffers: drive a context
+ * from one thread at a time. */
 int32_t tkv_hip_ctx_set_stream(int64_t ctx, void* stream);
 int32_t tkv_hip_ctx_get_stream(int64_t ctx, void** stream_out);
 int32_t tkv_hip_ctx_synchronize(int64_t ctx);
@@ -106,14 +110,22 @@ int32_t tkv_hip_event_elapsed_ms(int64_t ev_start, int64_t ev_end, float* ms_out
  * one launch per sequence.  Between begin and end the context's stream
  * records instead of running; every entry point called in between must
  * find its workspace already sized by an identical earlier call (it fails
- * with TKV_HIP_BAD_ARG otherwise), and host-pointer entry points, copies to
- * or from the host and synchronizations fail.  A graph replays the captured
- * device pointers and scalars as they were; device-resident QuantParams are
- * re-read on every replay. */
+ * with TKV_HIP_BAD_ARG otherwise), and host-pointer entry points, weight
+ * creation, stream switches, copies to or from the host and
+ * synchronizations fail.  A graph replays the captured device pointers and
+ * scalars as they were, workspace addresses included: while any graph of a
+ * context is alive, a workspace that grows keeps its old buffer (it is
+ * freed with the context's last graph, or with the context), so a replay
+ * after a larger eager call still reads and writes valid memory.
+ * Device-resident QuantParams are re-read on every replay.  Destroy a
+ * context's graphs before the context; replays and eager calls on one
+ * context are ordered on its stream. */
 int32_t tkv_hip_capture_begin(int64_t ctx);
 int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out);
 int32_t tkv_hip_graph_launch(int64_t ctx, int64_t graph);
 int32_t tkv_hip_graph_destroy(int64_t graph);
+/* Number of workspace buffers kept alive for live graphs (diagnostics). */
+int32_t tkv_hip_ctx_retired_buffers(int64_t ctx, int64_t* count_out);
 
 /* ======================================================================== */
 /* Host-pointer mirrors (one per .tkv function).  ctx-free: each calling    */

@@ -96,6 +96,9 @@ def _declare(L: C.CDLL) -> None:
         "tkvo_dequantize_fp8_e4m3": (I32, [P, I64, P]),
         "tkvo_matmul_fp8_e4m3": (I32, [P, P, P, I64, P, I64, I64, I64]),
         "tkvo_matmul_fp8_e4m3_exact": (I32, [P, P, P, P, I64, I64, I64]),
+        "tkvo_quantize_fp8_e4m3_dynamic_tensor": (I32, [P, I64, P, P]),
+        "tkvo_fp8_weight_pack": (I32, [P, I64, I64, P, P]),
+        "tkvo_matmul_fp8_e4m3_scaled": (I32, [P, P, P, I64, P, I64, I64, I64, P, I64, P]),
         "tkvo_matmul_integer": (I32, [P, I64, P, I64, P, I64, I64, I64, I64]),
         "tkvo_qlinear_matmul": (I32, [P, I64, F32, I64, P, I64, F32, I64, F32, I64, P, I64,
                                       I64, I64, I64, I32]),
@@ -358,6 +361,40 @@ def matmul_fp8_e4m3_exact(a, w, m, n, k):
     asum = np.zeros(int(m) * int(n), dtype=np.float64)
     lib().tkvo_matmul_fp8_e4m3_exact(_p(A), _p(W), _p(acc), _p(asum), int(m), int(n), int(k))
     return acc, asum
+
+
+# ---- FP8 W8A8 linear (R-ext: the scaled extension of matmul_fp8_e4m3) -------
+
+def quantize_fp8_e4m3_dynamic_tensor(src):
+    """Per-tensor FP8 activation pack: (codes, scale) with scale =
+    fl32(max(am, 1e-8) / 240) and codes = encode(fl32(x * fl32(1 / scale))) - 128."""
+    x = _f32(src)
+    dst = np.zeros(x.size, dtype=np.int32)
+    s = C.c_float()
+    lib().tkvo_quantize_fp8_e4m3_dynamic_tensor(_p(x), x.size, _p(dst), C.byref(s))
+    return dst, np.float32(s.value)
+
+
+def fp8_weight_pack(w, rows: int, cols: int):
+    """Per-output-channel FP8 weight pack: (codes [rows * cols], scales [rows])."""
+    x = _f32(w)
+    dst = np.zeros(int(rows) * int(cols), dtype=np.int32)
+    sc = np.zeros(int(rows), dtype=np.float32)
+    lib().tkvo_fp8_weight_pack(_p(x), int(rows), int(cols), _p(dst), _p(sc))
+    return dst, sc
+
+
+def matmul_fp8_e4m3_scaled(a, w, bias, m, n, k, scale_a, scales_w, per_token=False):
+    """y = fl32(fl64(fl64(S * sa) * sw[n]) + b[n]), S the exact product sum;
+    scale_a is one value (per tensor) or m values (per_token=True)."""
+    A, W = _i32(a), _i32(w)
+    b, nb = _bias(bias)
+    sa = _f32(np.atleast_1d(scale_a))
+    sw = _f32(scales_w)
+    y = np.zeros(int(m) * int(n), dtype=np.float32)
+    lib().tkvo_matmul_fp8_e4m3_scaled(_p(A), _p(W), _p(b), nb, _p(y), int(m), int(n), int(k),
+                                      _p(sa), 1 if per_token else 0, _p(sw))
+    return y
 
 
 # ---- session.tkv nodes -----------------------------------------------------

@@ -664,6 +664,91 @@ int32_t tkvo_matmul_fp8_e4m3_exact(const int32_t* a, const int32_t* w, int64_t* 
 }
 
 /* ===================================================================== */
+/* FP8 W8A8 linear (R-ext): the scaled form of matmul_fp8_e4m3.          */
+/* The reference's FP8 GEMM (matmul.tkv:46-58) takes raw codes and has   */
+/* no scales; configs[3] of the benchmark quantizes activations per      */
+/* tensor and weights per output channel into e4m3 range, then applies a */
+/* per-channel dequant + bias epilogue.  The build defines that          */
+/* extension on the reference's own pieces:                              */
+/*   scale  s  = fl32(max(am, 1e-8) / 240)   (am from the calibrate_minmax */
+/*               scan, engine.tkv:13-36; 240 is the largest e4m3 value   */
+/*               the reference encoder reaches before its >= 248         */
+/*               saturation step, types.tkv:176-177)                     */
+/*   codes     = encode(fl32(x * fl32(1 / s)))  (types.tkv:154-191)      */
+/*   y[m, n]   = fl32(fl64(fl64(S * sa[m]) * sw[n]) + b[n])              */
+/* with S the reference's own exact f64 product sum (matmul.tkv:52-55)   */
+/* and the epilogue chain of matmul_int8_per_channel's primary reading   */
+/* (matmul.tkv:28-29, R11).                                              */
+/* ===================================================================== */
+
+static float fp8_target_scale(double am) {
+    if (am < 0.00000001) am = 0.00000001;
+    return (float)(am / 240.0);
+}
+
+/* Per-tensor activation pack: am is the calibrate_minmax absmax
+ * (min / max seeded with x[0], so a leading NaN propagates as there). */
+int32_t tkvo_quantize_fp8_e4m3_dynamic_tensor(const float* x, int64_t n, int32_t* dst,
+                                              float* scale_out) {
+    double am = 0.0;
+    if (n > 0) {
+        double mn = x[0], mx = x[0];
+        for (int64_t i = 1; i < n; i++) {
+            double v = x[i];
+            if (v < mn) mn = v;
+            if (v > mx) mx = v;
+        }
+        am = fabs(mx);
+        if (fabs(mn) > am) am = fabs(mn);
+    }
+    float s = fp8_target_scale(am);
+    float inv = 1.0f / s;
+    for (int64_t i = 0; i < n; i++) dst[i] = (int32_t)(tkvo_fp8_e4m3_encode(x[i] * inv) - 128);
+    if (scale_out) *scale_out = s;
+    return 0;
+}
+
+/* Per-output-channel weight pack: row r's absmax is taken from 0 with NaN
+ * never comparing greater (as absmax_f64 / the rowwise quantizer,
+ * engine.tkv:272-276), then the same scale and encode as above. */
+int32_t tkvo_fp8_weight_pack(const float* w, int64_t rows, int64_t cols, int32_t* dst,
+                             float* scales) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float* wr = w + r * cols;
+        float s = fp8_target_scale(absmax_f64(wr, cols));
+        float inv = 1.0f / s;
+        for (int64_t c = 0; c < cols; c++)
+            dst[r * cols + c] = (int32_t)(tkvo_fp8_e4m3_encode(wr[c] * inv) - 128);
+        scales[r] = s;
+    }
+    return 0;
+}
+
+/* Scaled FP8 GEMM: S is the reference's f64 running sum of decoded
+ * products (exact for K < 2^15: every product is a multiple of 2^-20 below
+ * 2^18), sa[m * sa_stride] the activation scale (stride 0: per tensor),
+ * sw[n] the weight scales.  nbias == 0: no bias. */
+int32_t tkvo_matmul_fp8_e4m3_scaled(const int32_t* a, const int32_t* w, const float* bias,
+                                    int64_t nbias, float* y, int64_t m, int64_t n, int64_t k,
+                                    const float* sa, int64_t sa_stride, const float* sw) {
+    for (int64_t mm = 0; mm < m; mm++) {
+        double s_a = (double)sa[mm * sa_stride];
+        for (int64_t nn = 0; nn < n; nn++) {
+            double acc = 0.0;
+            for (int64_t kk = 0; kk < k; kk++) {
+                float p = fp8_code_decode(a[mm * k + kk]) * fp8_code_decode(w[nn * k + kk]);
+                acc = acc + (double)p;
+            }
+            double v = acc * s_a;
+            v = v * (double)sw[nn];
+            double b = nbias > 0 ? (double)bias[nn] : 0.0;
+            y[mm * n + nn] = (float)(v + b);
+        }
+    }
+    return 0;
+}
+
+/* ===================================================================== */
 /* tv/runtime/session.tkv nodes                                          */
 /* ===================================================================== */
 

@@ -130,6 +130,20 @@ int32_t tkvo_matmul_fp8_e4m3(const int32_t* a, const int32_t* w, const float* bi
 int32_t tkvo_matmul_fp8_e4m3_exact(const int32_t* a, const int32_t* w, int64_t* acc_q20,
                                    double* abs_sum, int64_t m, int64_t n, int64_t k);
 
+/* ---- FP8 W8A8 linear (R-ext, an extension defined on matmul.tkv) ------
+ * The reference's FP8 GEMM has no scales; configs[3] needs per-tensor
+ * activation and per-channel weight scales:
+ *   s = fl32(max(am, 1e-8) / 240), codes = encode(fl32(x * fl32(1 / s))),
+ *   y[m, n] = fl32(fl64(fl64(S * sa[m * sa_stride]) * sw[n]) + b[n])
+ * with S the reference's exact product sum (matmul.tkv:52-55). */
+int32_t tkvo_quantize_fp8_e4m3_dynamic_tensor(const float* x, int64_t n, int32_t* dst,
+                                              float* scale_out);
+int32_t tkvo_fp8_weight_pack(const float* w, int64_t rows, int64_t cols, int32_t* dst,
+                             float* scales);
+int32_t tkvo_matmul_fp8_e4m3_scaled(const int32_t* a, const int32_t* w, const float* bias,
+                                    int64_t nbias, float* y, int64_t m, int64_t n, int64_t k,
+                                    const float* sa, int64_t sa_stride, const float* sw);
+
 /* ---- session.tkv nodes ----------------------------------------------- */
 /* MatMulInteger (session.tkv:2789-2851): B is row-major [K,N]; reads outside
  * na/nb are zero and writes outside ny are dropped, as in the reference. */

@@ -385,13 +385,11 @@ DYN_SIZES = [1, 3, 4, 1000, 1023, GRID_CHUNK, GRID_CHUNK + 1, 5 * GRID_CHUNK + 7
              8192 * 768, 8192 * 3072, 8192 * 3072 + 4]
 
 
-@pytest.mark.parametrize("n", DYN_SIZES)
-@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n,offset", [(n, 0) for n in DYN_SIZES] + [(1000, 1), (8192 * 768, 1)])
 def test_int8_dynamic_tensor(ctx, n, offset):
     """calibrate_minmax(x, 1) + quantize_int8_symmetric on the device in one
-    call (engine.tkv:13-36, 216-226): QuantParams and codes bit-exact."""
-    if offset and n not in (1000, 8192 * 768):
-        pytest.skip("misaligned x: two sizes suffice")
+    call (engine.tkv:13-36, 216-226): QuantParams and codes bit-exact, for
+    every size aligned and for two sizes with x one float off 16 bytes."""
     say(f"int8 dynamic tensor n={n} offset={offset}")
     x = _x(n, 17 + n % 1000, 1.0)
     if n > 100:
@@ -905,4 +903,48 @@ def test_graph_capture_replays(hip):
     layer()
     ctx.synchronize()
     assert np.array_equal(dy.download(), want[1][1])
+    ctx.close()
+
+
+def test_graph_survives_workspace_growth(hip):
+    """A graph captured over a call that repacks its operands into workspace
+    still replays correctly after a larger eager call has grown those
+    workspaces: the old buffers stay alive (retired) while the graph does,
+    and are freed with it."""
+    say("graph replay after workspace growth")
+    ctx = D.Context(0)
+    m, n, k = 64, 96, 200                       # K = 200 repacks into slots 2 / 3
+    a = RNG.integers(-127, 128, (m, k)).astype(np.int8)
+    w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
+    da, dw = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, w)
+    dacc = D.DeviceBuffer.empty(ctx, (m, n), np.int32)
+    D.matmul_int8_accum(ctx, da, dw, m, n, k, dacc)
+    ctx.synchronize()
+    want = (a.astype(np.int64) @ w.astype(np.int64).T)
+    assert np.array_equal(dacc.download(), want)
+    with D.Graph(ctx) as g:
+        D.matmul_int8_accum(ctx, da, dw, m, n, k, dacc)
+    assert ctx.retired_buffers() == 0
+    # K = 300 pads to 384: 4100 x 384 bytes outgrows the 1 MiB repack slot
+    bm, bk = 4100, 300
+    ba = RNG.integers(-127, 128, (bm, bk)).astype(np.int8)
+    bw = RNG.integers(-127, 128, (n, bk)).astype(np.int8)
+    dba, dbw = D.DeviceBuffer.from_host(ctx, ba), D.DeviceBuffer.from_host(ctx, bw)
+    dbacc = D.DeviceBuffer.empty(ctx, (bm, n), np.int32)
+    D.matmul_int8_accum(ctx, dba, dbw, bm, n, bk, dbacc)
+    ctx.synchronize()
+    assert ctx.retired_buffers() >= 1
+    assert np.array_equal(dbacc.download(), ba.astype(np.int64) @ bw.astype(np.int64).T)
+    for rep in range(3):
+        D.memset(ctx, dacc, 0, m * n * 4)
+        da.upload(np.roll(a, rep, axis=0))
+        ctx.synchronize()
+        g.launch()
+        ctx.synchronize()
+        assert np.array_equal(dacc.download(), np.roll(want, rep, axis=0)), rep
+    g.close()
+    assert ctx.retired_buffers() == 0
+    D.matmul_int8_accum(ctx, da, dw, m, n, k, dacc)
+    ctx.synchronize()
+    assert np.array_equal(dacc.download(), np.roll(want, 2, axis=0))
     ctx.close()

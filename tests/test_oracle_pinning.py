@@ -318,6 +318,110 @@ def test_fp8_quantize_codes():
 
 
 # ---------------------------------------------------------------------------
+# FP8 W8A8 linear (R-ext, the scaled extension of matmul.tkv:46-66)
+# ---------------------------------------------------------------------------
+
+def _fp8_pack_check(x, codes, s):
+    """Independent restatement of one scaled e4m3 pack: the scale is the
+    correctly rounded f32 of fl64(max|x| / 240) (Fractions), the codes the
+    spec encoder's on numpy's f32 product, and the round trip within half an
+    e4m3 step (a full subnormal step in the reference's clamped band)."""
+    am = Fraction(float(np.max(np.abs(x.astype(np.float64)))))
+    am = max(am, Fraction(1e-8))
+    assert s == np.float32(float(am / 240)), (s, float(am))
+    inv = np.float32(1.0) / s
+    xs = x * inv                                       # numpy f32 multiply (RNE)
+    assert np.array_equal(codes + 128, [O.spec_e4m3_encode(float(v)) for v in xs])
+    ocp = np.array([_ocp_e4m3_value(int(c)) for c in codes + 128])
+    err = np.abs(ocp - xs.astype(np.float64))
+    normal = np.abs(xs) >= 2.0 ** -6
+    assert np.all(err[normal] <= 2.0 ** -4 * np.abs(xs[normal]))
+    assert np.all(err[~normal] <= 2.0 ** -9)
+    top = np.argmax(np.abs(x))                         # amax maps to +-240 (code 0x77)
+    assert (codes[top] + 128) & 0x7F == 0x77
+
+
+def test_fp8_act_pack_closed_form():
+    x = O.add_outliers(O.gi_noise(6000, 5, 1.0), 0.001, 3, 4, 20.0)
+    x[17] = -np.max(np.abs(x)) * 1.5                   # a negative extreme
+    codes, s = O.quantize_fp8_e4m3_dynamic_tensor(x)
+    _fp8_pack_check(x, codes, s)
+    # a tiny-range tensor lands on the 1e-8 scale floor (codes all subnormal or 0)
+    z = np.full(64, 3e-9, np.float32)
+    codes, s = O.quantize_fp8_e4m3_dynamic_tensor(z)
+    assert s == np.float32(1e-8 / 240)
+    assert np.array_equal(codes + 128, [O.spec_e4m3_encode(float(v)) for v in z * (np.float32(1) / s)])
+    # calibrate_minmax seeds min / max with x[0]: a leading NaN gives a NaN scale
+    codes, s = O.quantize_fp8_e4m3_dynamic_tensor(np.array([np.nan, 1.0, -2.0], np.float32))
+    assert np.isnan(s)
+
+
+def test_fp8_weight_pack_per_row():
+    rows, cols = 37, 200
+    w = O.gi_noise(rows * cols, 9, 0.02).reshape(rows, cols)
+    w[3] *= 100.0                                      # rows of very different ranges
+    w[5] = 0.0                                         # an all-zero row: scale floor
+    codes, sc = O.fp8_weight_pack(w, rows, cols)
+    codes = codes.reshape(rows, cols)
+    for r in range(rows):
+        if r == 5:
+            assert sc[r] == np.float32(1e-8 / 240) and np.all(codes[r] == -128)
+            continue
+        _fp8_pack_check(w[r], codes[r], sc[r])
+        c2, s2 = O.quantize_fp8_e4m3_dynamic_tensor(w[r])
+        assert s2 == sc[r] and np.array_equal(c2, codes[r])
+
+
+def _fp8_codes_any(shape):
+    codes = [c for c in range(256) if (c & 0x7F) != 0x7F]
+    return (RNG.choice(codes, shape) - 128).astype(np.int32)
+
+
+def test_fp8_scaled_gemm_unit_and_power_of_two_scales():
+    """sa = sw = 1 reduces to matmul_fp8_e4m3 (pinned above by Fractions);
+    power-of-two scales commute with every rounding, so
+    y(sa = 2^ea, sw[n] = 2^eb[n], b) == 2^(ea + eb[n]) * y_unscaled(b * 2^-(ea + eb[n]))
+    bit for bit.  A dropped scale, sw indexed by row, or a bias applied
+    before the scaling fails it."""
+    m, n, k = 6, 9, 96
+    a, w = _fp8_codes_any((m, k)), _fp8_codes_any((n, k))
+    b = RNG.normal(0, 1, n).astype(np.float32)
+    y1 = O.matmul_fp8_e4m3_scaled(a, w, b, m, n, k, np.float32(1), np.ones(n, np.float32))
+    assert np.array_equal(y1.view(np.uint32), O.matmul_fp8_e4m3(a, w, b, m, n, k).view(np.uint32))
+    ea = -7
+    eb = RNG.integers(-12, -3, n)
+    sw = (2.0 ** eb).astype(np.float32)
+    y = O.matmul_fp8_e4m3_scaled(a, w, b, m, n, k, np.float32(2.0 ** ea), sw).reshape(m, n)
+    bs = (b.astype(np.float64) * 2.0 ** -(ea + eb)).astype(np.float32)
+    assert np.array_equal(bs.astype(np.float64) * 2.0 ** (ea + eb), b.astype(np.float64))
+    yu = O.matmul_fp8_e4m3(a, w, bs, m, n, k).reshape(m, n).astype(np.float64)
+    want = (yu * 2.0 ** (ea + eb)[None, :]).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp8_scaled_gemm_fraction_bound_and_per_token():
+    """General scales: within half an f32 ulp plus two f64 roundings of the
+    exact S * sa * sw + b (Fractions); per-token scales index by row."""
+    m, n, k = 5, 7, 64
+    a, w = _fp8_codes_any((m, k)), _fp8_codes_any((n, k))
+    b = RNG.normal(0, 0.01, n).astype(np.float32)
+    sa = RNG.uniform(0.001, 0.05, m).astype(np.float32)
+    sw = RNG.uniform(1e-4, 3e-4, n).astype(np.float32)
+    y = O.matmul_fp8_e4m3_scaled(a, w, b, m, n, k, sa, sw, per_token=True).reshape(m, n)
+    t = _dec_table()
+    da, dw = t[a + 128], t[w + 128]
+    for i in range(m):
+        yt = O.matmul_fp8_e4m3_scaled(a[i:i + 1], w, b, 1, n, k, sa[i], sw)
+        assert np.array_equal(yt.view(np.uint32), y[i].view(np.uint32))
+        for j in range(n):
+            s = sum(Fraction(float(p)) for p in da[i] * dw[j])
+            ex = s * Fraction(float(sa[i])) * Fraction(float(sw[j])) + Fraction(float(b[j]))
+            mag = abs(s * Fraction(float(sa[i])) * Fraction(float(sw[j]))) + abs(Fraction(float(b[j])))
+            tol = Fraction(float(np.spacing(np.float32(abs(float(ex)))))) / 2 + mag * Fraction(3, 2 ** 53)
+            assert abs(Fraction(float(y[i, j])) - ex) <= tol, (i, j)
+
+
+# ---------------------------------------------------------------------------
 # session.tkv nodes
 # ---------------------------------------------------------------------------
 

@@ -101,6 +101,7 @@ int host_gemm_i8(const int32_t* pa, const int32_t* pw, const float* pbias, int64
     ep.scale_w = scale_w;
     ep.scales_w = scales_w ? fs + 1 : nullptr;
     ep.bias = has_bias ? fs + 1 + n : nullptr;
+    ep.k_logical = k;  // rows are zero padded to ldk
     TKV_RC_TRY(launch_gemm_i8(c, static_cast<int8_t*>(da), static_cast<int8_t*>(dw), m, n, ldk,
                               ep, dy));
     return download(c, py, dy, ybytes);

@@ -983,7 +983,7 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
                    const I8Epilogue& e, void* y) {
     if (m <= 0 || n <= 0) return TKV_HIP_OK;
-    TKV_RC_TRY(gemm::check_sizes(m, n, k, "INT8 GEMM"));
+    TKV_RC_TRY(gemm::check_sizes(m, n, e.k_logical > 0 ? e.k_logical : k, "INT8 GEMM"));
     const void *pa = a, *pw = w;
     int64_t ldk;
     TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));

@@ -62,7 +62,8 @@ static int weight_alloc(Ctx* c, Weight* wt, int64_t n, int64_t k, int format, co
     wt->ldk = (k + ka - 1) / ka * ka;  // the GEMM slice depth: no per-call repack
     TKV_HIP_TRY(hipMalloc(&wt->codes, (size_t)(n * wt->ldk)));
     TKV_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&wt->scales), (size_t)n * 4));
-    TKV_HIP_TRY(hipMemsetAsync(wt->codes, 0, (size_t)(n * wt->ldk), c->stream));
+    // zero padding past k (a kernel: the library records no memset nodes)
+    TKV_RC_TRY(launch_fill(c, wt->codes, 0, n * wt->ldk));
     if (bias) {
         TKV_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&wt->bias), (size_t)n * 4));
         TKV_HIP_TRY(hipMemcpyAsync(wt->bias, bias, (size_t)n * 4, hipMemcpyDeviceToDevice, c->stream));
@@ -93,6 +94,8 @@ int32_t tkv_hip_weight_create(int64_t ctx, const float* w, int64_t n, int64_t k,
     TKV_RC_TRY(ctx_get(ctx, &c));
     if (!w || !handle_out || n <= 0 || k <= 0)
         return set_error(TKV_HIP_BAD_ARG, "weight_create: empty weight or NULL output");
+    if (c->capturing)
+        return set_error(TKV_HIP_BAD_ARG, "weight_create: allocates and synchronizes, not inside a stream capture");
     if (format != TKV_HIP_WEIGHT_INT8 && format != TKV_HIP_WEIGHT_FP8 &&
         format != TKV_HIP_WEIGHT_FP8_FAST)
         return set_error(TKV_HIP_BAD_ARG, "weight_create: unknown format");
@@ -143,6 +146,8 @@ int32_t tkv_hip_weight_create_int8(int64_t ctx, const int8_t* codes, const float
     TKV_RC_TRY(ctx_get(ctx, &c));
     if (!codes || !scales || !handle_out || n <= 0 || k <= 0)
         return set_error(TKV_HIP_BAD_ARG, "weight_create_int8: bad arguments");
+    if (c->capturing)
+        return set_error(TKV_HIP_BAD_ARG, "weight_create_int8: allocates and synchronizes, not inside a stream capture");
     Weight* wt = new (std::nothrow) Weight();
     if (!wt) return set_error(TKV_HIP_OOM, "weight_create_int8: host allocation failed");
     int rc = weight_alloc(c, wt, n, k, TKV_HIP_WEIGHT_INT8, bias);

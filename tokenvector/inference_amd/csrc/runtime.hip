@@ -9,6 +9,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <new>
 #include <string>
 
 #include "tkv_internal.h"
@@ -104,6 +105,7 @@ int ctx_destroy(Ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     for (int i = 0; i < Ctx::kSlots; i++)
         if (c->ws[i]) (void)hipFree(c->ws[i]);
+    for (void* p : c->retired) (void)hipFree(p);
     if (c->partials) (void)hipFree(c->partials);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
@@ -140,8 +142,13 @@ int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out) {
                                  " would grow inside a stream capture: make the same calls "
                                  "once before capturing");
         if (c->ws[slot]) {
-            TKV_HIP_TRY(hipStreamSynchronize(c->stream));
-            TKV_HIP_TRY(hipFree(c->ws[slot]));
+            if (c->live_graphs > 0) {
+                // a live graph may replay into the old buffer: keep it
+                c->retired.push_back(c->ws[slot]);
+            } else {
+                TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+                TKV_HIP_TRY(hipFree(c->ws[slot]));
+            }
             c->ws[slot] = nullptr;
             c->ws_bytes[slot] = 0;
         }
@@ -244,7 +251,13 @@ int32_t tkv_hip_ctx_destroy(int64_t ctx) {
 int32_t tkv_hip_ctx_set_stream(int64_t ctx, void* stream) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
-    c->stream = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
+    if (c->capturing) return set_error(TKV_HIP_BAD_ARG, "set_stream: context is capturing");
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
+    // Work already queued on the previous stream shares this context's
+    // workspaces and split-K buffers with what the next stream will run:
+    // drain it so the two never overlap.
+    if (next != c->stream) TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    c->stream = next;
     return TKV_HIP_OK;
 }
 
@@ -335,6 +348,12 @@ int32_t tkv_hip_capture_begin(int64_t ctx) {
     return TKV_HIP_OK;
 }
 
+// A captured graph and the context whose workspaces it replays.
+struct Graph {
+    hipGraphExec_t exec = nullptr;
+    Ctx* ctx = nullptr;
+};
+
 int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
@@ -348,7 +367,15 @@ int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out) {
     const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate", __FILE__, __LINE__);
-    *graph_out = reinterpret_cast<int64_t>(x);
+    Graph* gr = new (std::nothrow) Graph();
+    if (!gr) {
+        (void)hipGraphExecDestroy(x);
+        return set_error(TKV_HIP_OOM, "capture_end: host allocation failed");
+    }
+    gr->exec = x;
+    gr->ctx = c;
+    c->live_graphs++;
+    *graph_out = reinterpret_cast<int64_t>(gr);
     return TKV_HIP_OK;
 }
 
@@ -357,12 +384,32 @@ int32_t tkv_hip_graph_launch(int64_t ctx, int64_t graph) {
     TKV_RC_TRY(ctx_get(ctx, &c));
     if (!graph) return set_error(TKV_HIP_BAD_ARG, "graph_launch: NULL graph");
     if (c->capturing) return set_error(TKV_HIP_BAD_ARG, "graph_launch: context is capturing");
-    TKV_HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), c->stream));
+    TKV_HIP_TRY(hipGraphLaunch(reinterpret_cast<Graph*>(graph)->exec, c->stream));
     return TKV_HIP_OK;
 }
 
 int32_t tkv_hip_graph_destroy(int64_t graph) {
-    if (graph) TKV_HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph)));
+    Graph* gr = reinterpret_cast<Graph*>(graph);
+    if (!gr) return TKV_HIP_OK;
+    Ctx* c = gr->ctx;
+    TKV_HIP_TRY(hipSetDevice(c->device));
+    // replays already queued must finish before the graph or the buffers
+    // it reads go away
+    TKV_HIP_TRY(hipStreamSynchronize(c->stream));
+    TKV_HIP_TRY(hipGraphExecDestroy(gr->exec));
+    delete gr;
+    if (--c->live_graphs == 0) {
+        for (void* p : c->retired) TKV_HIP_TRY(hipFree(p));
+        c->retired.clear();
+    }
+    return TKV_HIP_OK;
+}
+
+int32_t tkv_hip_ctx_retired_buffers(int64_t ctx, int64_t* count_out) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (!count_out) return set_error(TKV_HIP_BAD_ARG, "retired_buffers: NULL output");
+    *count_out = (int64_t)c->retired.size();
     return TKV_HIP_OK;
 }
 

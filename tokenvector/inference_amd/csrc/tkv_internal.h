@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <string>
+#include <vector>
 
 #include "../../../include/tkv_hip.h"
 
@@ -66,6 +67,12 @@ struct Ctx {
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
     bool capturing = false;  // between capture_begin and capture_end
+    // Graphs captured on this context and not yet destroyed.  They replay
+    // the workspace addresses they captured, so while any is alive a slot
+    // that grows keeps its old buffer here (freed with the last graph, or
+    // with the context) instead of freeing it.
+    int live_graphs = 0;
+    std::vector<void*> retired;
 };
 
 int ctx_create(int device, Ctx** out);
@@ -148,6 +155,9 @@ struct I8Epilogue {
     float scale_w;             // symmetric weight scale
     const float* scales_w;     // device [N] (per-channel) or null
     const float* bias;         // device [N] or null
+    // K of the caller's product when the operands arrive already zero padded
+    // to a longer row stride (0: the stride is K); bounds |acc| < 2^31.
+    int64_t k_logical = 0;
 };
 enum { EPI_PER_CHANNEL = 0, EPI_SYMMETRIC = 1, EPI_ACCUM_I32 = 2 };
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,

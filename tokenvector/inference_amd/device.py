@@ -41,6 +41,12 @@ class Context:
     def synchronize(self) -> None:
         _lib.check(_lib.lib().tkv_hip_ctx_synchronize(self.handle))
 
+    def retired_buffers(self) -> int:
+        """Workspace buffers kept alive for this context's live graphs."""
+        n = C.c_int64()
+        _lib.check(_lib.lib().tkv_hip_ctx_retired_buffers(self.handle, C.byref(n)))
+        return n.value
+
     def close(self) -> None:
         if self.handle:
             _lib.check(_lib.lib().tkv_hip_ctx_destroy(self.handle))
