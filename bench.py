@@ -48,7 +48,10 @@ def gemm_bytes(m, n, k):
     return m * k + n * k + 8 * n + 4 * m * n
 
 
-def run_gpu(steps, warmup):
+SECTIONS = ("step", "quant", "fp8", "decode", "qlinear", "int4")
+
+
+def run_gpu(steps, warmup, sections=SECTIONS):
     import oracle as O
     from tokenvector.inference_amd import _lib
     from tokenvector.inference_amd import device as D
@@ -56,7 +59,22 @@ def run_gpu(steps, warmup):
     if _lib.lib().tkv_hip_device_count() < 1:
         raise SystemExit("bench.py: no gfx950 device visible")
     ctx = D.Context(0)
+    r = {}
+    if "step" in sections:
+        r.update(bench_step(ctx, D, O, steps, warmup))
+    for name, fn in (("quant", lambda: bench_quant(ctx, D, O)), ("fp8", lambda: bench_fp8(ctx, D, O)),
+                     ("decode", lambda: bench_decode(ctx, D, O)),
+                     ("qlinear", lambda: bench_qlinear(ctx, D)),
+                     ("int4", lambda: bench_int4(ctx, D, O))):
+        if name in sections:
+            log(f"bench section {name}")
+            r[name] = fn()
+    ctx.close()
+    return r
 
+
+def bench_step(ctx, D, O, steps, warmup):
+    """the timed W8A8 step over all 48 GPT-2 linears."""
     # ---- inputs (generated on the host once, resident in HBM) ----
     t0 = time.time()
     x_host = {768: O.gi_noise(M * 768, 0, 1.0), 3072: O.gi_noise(M * 3072, 7, 1.0)}
@@ -139,13 +157,11 @@ def run_gpu(steps, warmup):
     ctx.synchronize()
     b2b_us = e0.elapsed_ms(e1) * 1e3 / (2 * n_gemm)
 
-    # ---- config 2: quantize / calibrate bandwidth at M = 65536 x 768 ----
-    quant = bench_quant(ctx, D, O)
-    fp8 = bench_fp8(ctx, D, O)
-    decode = bench_decode(ctx, D, O)
-    qlinear = bench_qlinear(ctx, D)
-    int4 = bench_int4(ctx, D, O)
-    ctx.close()
+    for lin in layers:
+        for (name, n, k, q, dx, dy, qa, db) in lin:
+            for buf in (dx, dy, qa, db):
+                buf.close()
+            q.close()
     return {
         "ms_per_step": ms_per_step,
         "value": ops_step / (ms_per_step * 1e-3) / 1e12,
@@ -153,11 +169,6 @@ def run_gpu(steps, warmup):
                  "achieved_gbps": achieved_gbps, "bytes_per_launch": bytes_per_launch,
                  "launches_timed": len(gemm_ms), "per_shape": per_shape,
                  "back_to_back_us": b2b_us},
-        "quant": quant,
-        "fp8": fp8,
-        "decode": decode,
-        "qlinear": qlinear,
-        "int4": int4,
         "ops_per_step": ops_step,
     }
 
@@ -303,33 +314,43 @@ def bench_int4(ctx, D, O, ms=(1, 32, 8192), gs=128):
     return out
 
 
-def bench_decode(ctx, D, O, ms=(1, 4, 16, 32), reps=50):
+def bench_decode(ctx, D, O, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
     """decode batches, INT8 weights pre-quantized per channel,
     activations quantized per token inside the timed call
-    (tkv_hip_linear_forward, ACT_PER_TOKEN: rowwise quantize + skinny GEMM).
-    12 layers' distinct weights are cycled per shape, as a model would."""
+    (tkv_hip_linear_forward, ACT_PER_TOKEN: one kernel for M <= 32).
+    Cold: distinct weight sets totalling `cold_bytes` (2.5x the 256 MB
+    Infinity Cache) are rotated, one per call, so every call streams its
+    weights from HBM.  Warm: one weight set repeated (L2 / Infinity Cache)."""
     shapes = [("qkv", 2304, 768), ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)]
     out = {}
     for (name, n, k) in shapes:
-        lins = []
-        for l in range(LAYERS):
-            w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 300 + l, 0.02))
-            b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 400 + l, 0.01))
-            lins.append((D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_INT8), b))
-            w.close()
+        w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 300, 0.02))
+        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 400, 0.01))
+        base = D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_INT8)
+        w.close()
+        nsets = max(2, -(-cold_bytes // (n * k)))
+        lins = [base] + [D.QuantizedLinear.from_int8(ctx, base.codes, base.scales, n, k, b)
+                         for _ in range(nsets - 1)]
         for m in ms:
             dx = D.DeviceBuffer.from_host(ctx, O.gi_noise(m * k, 24, 1.0))
             dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
-            us = _time_us(ctx, D, lambda i: lins[i % LAYERS][0].forward(dx, m, dy, D.ACT_PER_TOKEN),
-                          reps)
-            out[f"{name}_m{m}"] = {"us": round(us, 2),
-                                   "weight_GBps": round(n * k / (us * 1e-6) / 1e9, 1)}
+            cold = _time_us(ctx, D, lambda i: lins[i % nsets].forward(dx, m, dy, D.ACT_PER_TOKEN),
+                            nsets)
+            warm = _time_us(ctx, D, lambda i: base.forward(dx, m, dy, D.ACT_PER_TOKEN), 200)
+            nbytes = n * k + 8 * n + 4 * m * k + 4 * m * n
+            out[f"{name}_m{m}"] = {"cold_us": round(cold, 2), "warm_us": round(warm, 2),
+                                   "cold_GBps": round(nbytes / (cold * 1e-6) / 1e9, 1),
+                                   "cold_frac_of_hbm": round(nbytes / (cold * 1e-6) / 1e9
+                                                             / PEAK_HBM_GBPS, 3)}
             dx.close()
             dy.close()
-        for lin, b in lins:
+        for lin in lins:
             lin.close()
-            b.close()
-    out["note"] = "per call: per-token int8 quantize + skinny INT8 GEMM + dequant/bias; weight bytes / call time"
+        b.close()
+    out["note"] = ("per call: per-token int8 quantize + INT8 GEMM + dequant/bias in one kernel; "
+                   "us = HIP-event time per call over back-to-back calls (launch gaps included); "
+                   "bytes = N*K int8 weights + 8N scales/bias + 4MK f32 x + 4MN f32 y; cold rotates "
+                   f"{cold_bytes >> 20} MiB of distinct weight sets")
     return out
 
 
@@ -438,28 +459,89 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(rows=4096):
-    """The oracle's scalar restatement of the reference loops (one thread),
-    on a bounded sample of the same workload: `rows` activation rows of each
-    of the four linear shapes (calibrate + quantize + INT8 GEMM + epilogue)."""
-    import oracle as O
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_layer(O, rows, threads):
+    """One layer of configs[2] on the host at `rows` activation rows: per
+    shape, calibrate + quantize the activation (one thread, O(MK)) and the
+    INT8 GEMM with its per-channel epilogue (`threads` workers over rows).
+    Returns (seconds, ops)."""
     t_total, ops = 0.0, 0.0
     for j, (name, n, k) in enumerate(SHAPES):
-        x = O.gi_noise(rows * k, 0, 1.0)
-        w = O.gi_noise(n * k, 11 + j, 0.02)
-        b = O.gi_noise(n, 61 + j, 0.01)
+        x = O.gi_noise(rows * k, 0 if k == 768 else 7, 1.0)
+        w = O.gi_noise(n * k, 10 + j + 1, 0.02)
+        b = O.gi_noise(n, 10 + j + 51, 0.01)
         sw = np.array([p.scale for p in O.calibrate_per_channel_minmax(w, n, k)], np.float32)
         wq = O.quantize_int8_per_channel(w, n, k, sw)
         t0 = time.perf_counter()
         p = O.calibrate_minmax(x, 1)
         xq = O.quantize_int8_symmetric(x, p.scale)
-        O.matmul_int8_per_channel(xq, wq, b, rows, n, k, p.scale, sw)
+        O.matmul_int8_per_channel(xq, wq, b, rows, n, k, p.scale, sw, threads=threads)
         t_total += time.perf_counter() - t0
         ops += 2.0 * rows * n * k
-    return {"value": round(ops / t_total / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "port",
-            "sample": f"{rows} of 8192 activation rows of each GPT-2 linear shape "
-                      f"(one layer: calibrate + quantize + INT8 GEMM + dequant), "
-                      f"{ops / 1e9:.1f} GOP in {t_total:.1f} s; oracle/tkv_oracle.c -O2, 1 thread"}
+    return t_total, ops
+
+
+def cpu_baseline(rows_single=2048, rows_all=M):
+    """The oracle's restatement of the reference's scalar loops (oracle/tkv_oracle.c,
+    -O2 -ffp-contract=off), timed on this host in the same run as the GPU:
+      * all cores: one whole layer of configs[2] (M = 8192, the four
+        shapes; every layer does the same work, so the 12-layer step takes
+        12x as long), the GEMM split over rows on the host's worker threads;
+      * single thread: `rows_single` of the 8192 rows of each shape,
+        faithful to the reference's single-threaded IL loops;
+      * the reference's own smoke shape (compare_rivals.tkv:131-158:
+        matmul_int8_symmetric, M = 16, K = 256, N = 256, 200 times), single
+        thread, beside the GPU host mirror of the same call."""
+    import oracle as O
+    threads = O.host_threads()
+    t_all, ops_all = _cpu_layer(O, rows_all, threads)
+    t_one, ops_one = _cpu_layer(O, rows_single, 1)
+    # courtesy row: the reference's smoke benchmark shape
+    m, n, k, iters = 16, 256, 256, 200
+    xf, wf = O.gi_noise(m * k, 1, 1.0), O.gi_noise(n * k, 2, 1.0)
+    p = O.calibrate_minmax(xf, 1)
+    xi, wi = O.quantize_int8_symmetric(xf, p.scale), O.quantize_int8_symmetric(wf, p.scale)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        O.matmul_int8_symmetric(xi, wi, None, m, n, k, p.scale, p.scale)
+    smoke_cpu_ms = (time.perf_counter() - t0) * 1e3
+    smoke_gpu_ms = None
+    try:
+        from tokenvector.inference_amd import quantization as Q
+        y = np.zeros(m * n, np.float32)
+        Q.matmul_int8_symmetric(xi, wi, [], y, m, n, k, p.scale, p.scale)
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            Q.matmul_int8_symmetric(xi, wi, [], y, m, n, k, p.scale, p.scale)
+        smoke_gpu_ms = round((time.perf_counter() - t0) * 1e3, 2)
+    except Exception as e:  # noqa: BLE001 -- the courtesy row is optional
+        log(f"cpu_baseline: GPU host-mirror smoke row skipped: {e}")
+    model = _cpu_model()
+    return {"value": round(ops_all / t_all / 1e12, 6), "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"one whole configs[2] layer (M=8192, qkv/attn_out/mlp_up/mlp_down: "
+                      f"calibrate + quantize + INT8 GEMM + dequant), {ops_all / 1e9:.1f} GOP in "
+                      f"{t_all:.2f} s on {threads} threads; the 12-layer step is 12x this work "
+                      f"({12 * t_all:.1f} s)",
+            "nproc": os.cpu_count(), "cpu_model": model,
+            "single_thread": {"value": round(ops_one / t_one / 1e12, 6), "unit": "TOPS", "cores": 1,
+                              "sample": f"{rows_single} of 8192 rows of each shape, "
+                                        f"{ops_one / 1e9:.1f} GOP in {t_one:.2f} s"},
+            "reference_smoke_shape": {"shape": "matmul_int8_symmetric M=16 K=256 N=256 x200",
+                                      "cpu_1thread_ms": round(smoke_cpu_ms, 2),
+                                      "gpu_host_mirror_ms": smoke_gpu_ms,
+                                      "note": "host mirror: int32 code lists in and f32 out "
+                                              "through PCIe each call"}}
 
 
 def main():
@@ -468,9 +550,13 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=4096)
+    ap.add_argument("--cpu-rows", type=int, default=2048,
+                    help="rows per shape of the single-thread CPU baseline sample")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the launches profiled for HBM traffic (no JSON line)")
+    ap.add_argument("--sections", default=",".join(SECTIONS),
+                    help="comma list of bench sections to run (profiling runs); the JSON line "
+                         "needs 'step'")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
@@ -480,7 +566,11 @@ def main():
         traffic_probe()
         return
 
-    r = run_gpu(args.steps, args.warmup)
+    sections = tuple(x for x in args.sections.split(",") if x)
+    r = run_gpu(args.steps, args.warmup, sections)
+    if "step" not in sections:
+        print(json.dumps({k: v for k, v in r.items()}), flush=True)
+        return
     gemm = r["gemm"]
     line = {
         "metric": "INT8/FP8 GEMM TOPS + quantize GB/s (% of roofline) on GPT-2-124M linears",
@@ -514,14 +604,13 @@ def main():
                      "avg_launch_us": round(gemm["avg_launch_us"], 2),
                      "back_to_back_us": round(gemm["back_to_back_us"], 2),
                      "per_shape": gemm["per_shape"]},
-        "quantize": r["quant"],
-        "fp8": r["fp8"],
-        "decode": r["decode"],
-        "qlinear": r["qlinear"],
-        "int4": r["int4"],
     }
+    for key, sec in (("quantize", "quant"), ("fp8", "fp8"), ("decode", "decode"),
+                     ("qlinear", "qlinear"), ("int4", "int4")):
+        if sec in r:
+            line[key] = r[sec]
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+        line["cpu_baseline"] = cpu_baseline(rows_single=args.cpu_rows)
     print(json.dumps(line), flush=True)
 
 

@@ -803,6 +803,58 @@ def test_linear_forward_per_token(ctx):
         lin.close()
 
 
+def _per_token_want(x, w, b, m, n, k):
+    osw = np.array([p.scale for p in O.calibrate_per_channel_minmax(w, n, k)], np.float32)
+    owq = O.quantize_int8_per_channel(w, n, k, osw)
+    oxq, osa = O.quantize_dynamic_int8_rowwise(x, m, k)
+    acc = O.matmul_int8_accum(oxq, owq, m, n, k).reshape(m, n).astype(np.float64)
+    return (acc * osa.astype(np.float64)[:, None] * osw.astype(np.float64)[None, :]
+            + b.astype(np.float64)[None, :]).astype(np.float32)
+
+
+DECODE_EDGE = [(1, 100, 64), (3, 17, 128), (5, 33, 192), (17, 200, 1024), (31, 2304, 768),
+               (32, 768, 3072), (2, 768, 3072), (8, 3072, 768)]
+
+
+@pytest.mark.parametrize("rg", [None, "1", "3", "16"])
+def test_decode_linear_edge_cases(ctx, monkeypatch, rg):
+    """The one-kernel decode linear (per-token quantize + INT8 GEMM +
+    epilogue, M <= 32): ragged row groups and column blocks, one to sixteen
+    waves, a zero row (scale floor), a row holding NaN (skipped by the
+    absmax, coded 0), an outlier row; forced row-group sizes; and a
+    misaligned x, which takes the two-kernel path.  Bit-exact."""
+    if rg is not None:
+        monkeypatch.setenv("TKV_DECODE_RG", rg)
+    for m, n, k in DECODE_EDGE:
+        say(f"decode linear rg={rg} {m}x{n}x{k}")
+        x = _x(m * k, 31 + m, 1.0).reshape(m, k)
+        x[0] = 0.0
+        if m > 1:
+            x[1, 5] = np.nan
+        if m > 2:
+            x[2, k // 3] = 3.0e4
+        x = x.reshape(-1)
+        w = _x(n * k, 32, 0.02)
+        w[:k] = 0.0                                     # an all-zero weight row
+        b = _x(n, 33, 0.01)
+        dw, db = D.DeviceBuffer.from_host(ctx, w), D.DeviceBuffer.from_host(ctx, b)
+        lin = D.QuantizedLinear.from_float(ctx, dw, n, k, db, D.WEIGHT_INT8)
+        dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+        want = _per_token_want(x, w, b, m, n, k)
+        dx = D.DeviceBuffer.from_host(ctx, x)
+        lin.forward(dx, m, dy, D.ACT_PER_TOKEN)
+        assert _same_f32(dy.download(), want), (rg, m, n, k)
+        if rg is None and k % 128 == 0:
+            # x one float past a 16-byte boundary: the two-kernel fallback
+            dxo = D.DeviceBuffer.from_host(ctx, np.concatenate([np.zeros(1, np.float32), x]))
+            lin.forward(dxo.ptr + 4, m, dy, D.ACT_PER_TOKEN)
+            assert _same_f32(dy.download(), want), ("misaligned", m, n, k)
+            dxo.close()
+        for buf in (dx, dw, db, dy):
+            buf.close()
+        lin.close()
+
+
 @pytest.mark.parametrize("cfg", GEMM_CFGS)
 def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
     """Device QLinearMatMul (fused requantizing epilogue, int8 out) on every

@@ -1,0 +1,224 @@
+// decode.hip -- the per-token W8A8 linear of decode batches (M <= 32) as
+// one kernel: per-token absmax + int8 quantize of the activation rows
+// (quantize_dynamic_int8_rowwise, tv/quantization/engine.tkv:266-285), the
+// INT8 GEMM against a resident per-channel weight (matmul_int8_per_channel,
+// tv/quantization/matmul.tkv:17-29, _dot_int8 :116-127) and the dequant +
+// bias epilogue with the token's scale (the per-token form of the R11 chain:
+// y = fl32(fl64(fl64(acc * sa[m]) * sw[n]) + b[n]), sa[m] = fl32(am / 127)).
+//
+// Workgroup (cb, rg) owns output columns [16 cb, 16 cb + 16) and token rows
+// [RG rg, RG rg + RG).  It needs its rows' full activation (the token scale
+// is the row's absmax over all of K) and its columns' full weight rows, so
+// it reads both itself and nothing crosses workgroups: no atomics, no
+// barrier, no scratch memory, and the result does not depend on scheduling.
+//   * Every load is issued at the start: the weight fragments (16 B per lane
+//     per 64-deep k-step, the B operand of v_mfma_i32_16x16x64_i8) and the
+//     activation fragments (16 f32 per lane per k-step, the A operand's
+//     elements before quantization); one memory latency covers both.
+//   * Wave w takes the contiguous k-steps [KSW w, KSW w + KSW); the row
+//     absmax is reduced over the 4 lanes sharing a row (shuffles) and then
+//     over the waves (LDS), then each wave quantizes its fragments in
+//     registers and runs its MFMAs.
+//   * The waves' INT32 partial tiles are summed exactly with LDS atomics and
+//     wave 0 runs the epilogue.
+// Splitting the tokens into row groups keeps the activation bytes per
+// workgroup near its weight bytes (16 K each at RG = 4): a CU then moves
+// ~32 K bytes per workgroup whatever M is, instead of 4 M K.
+// Workgroups sharing a column block sit on one XCD (consecutive tile ids per
+// XCD), so their repeated weight reads come from that XCD's L2.
+#include <cstdlib>
+
+#include "gemm_tile.h"
+#include "tkv_device.h"
+#include "tkv_internal.h"
+
+namespace tkv {
+namespace {
+
+using gemm::v4i;
+using gemm::wave_id;
+using gemm::xcd_tile;
+
+constexpr int kKsw = 3;         // 64-deep k-steps per wave
+constexpr int kMaxWaves = 16;   // K <= 16 * 3 * 64 = 3072
+constexpr int kDecodeMaxM = 32;
+
+// Four f32 -> int8 codes (rne, clamp +-127, NaN -> 0) packed little-endian.
+__device__ __forceinline__ int quant4(const float4 v, double inv) {
+    const int a = rne_clamp((double)v.x * inv, -127.0, 127.0);
+    const int b = rne_clamp((double)v.y * inv, -127.0, 127.0);
+    const int c = rne_clamp((double)v.z * inv, -127.0, 127.0);
+    const int d = rne_clamp((double)v.w * inv, -127.0, 127.0);
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
+    return (int)(lo | hi);
+}
+
+__device__ __forceinline__ float amax4(float m, const float4 v) {
+    return fmaxf(fmaxf(m, fabsf(v.x)), fmaxf(fmaxf(fabsf(v.y), fabsf(v.z)), fabsf(v.w)));
+}
+
+// x f32 [M, K] (16-byte aligned rows, K % 64 == 0), W int8 [N, ldk]
+// (K-major, ldk % 16 == 0), sw f32 [N], bias f32 [N] or null, y f32 [M, N].
+// ncb = ceil(N / 16) column blocks, ngr = ceil(M / RG) row groups.
+//
+// The activation is quantized only for the group's valid rows: chunk
+// c < nks * 4 * rows is 16 consecutive elements of row c % rows at k =
+// 16 (c / rows); a lane holds up to kChunks chunks in registers, the row
+// absmax is reduced with LDS atomics on the f32 bits (non-negative, NaN
+// already skipped), threads 0 .. rows - 1 form the row's reciprocal once,
+// and each chunk's 16 codes are written to LDS where the MFMA A fragment of
+// its k-step expects them: 16 bytes at ((ks * 4 + kg) * 16 + row) * 16.
+// (Measured against one float4 per thread per row with DPP row maxima and
+// swizzled 4-byte code stores: the chunk form was 0.5-1.4 us faster per call
+// up to M = 16 in a kernel trace of both on one box.)
+constexpr int kChunks = 3;  // 16 rows * 3072 / (16 elements * 1024 threads) = 3
+
+__global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
+    const float* __restrict__ x, const uint8_t* __restrict__ W, int M, int N, int K, int ldk,
+    int RG, int ncb, int ngr, const float* __restrict__ sw, const float* __restrict__ bias,
+    float* __restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_a[];  // 16 K bytes
+    __shared__ uint32_t s_am[16];
+    __shared__ double s_inv[16];
+    __shared__ float s_sa[16];
+    __shared__ int32_t s_acc[256];
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int nthreads = (int)blockDim.x;
+    const int t = xcd_tile((int)blockIdx.x, ncb * ngr);
+    const int cb = t / ngr, rg = t % ngr;
+    const int n0 = cb * 16, r0 = rg * RG;
+    const int rows = M - r0 < RG ? M - r0 : RG;  // valid rows of this group (1 .. 16)
+    const int nks = K / 64;
+    const int lr = lane & 15, kg = lane >> 4;
+    const int ks0 = wave * kKsw;
+
+    // weight fragments (B operand): column n0 + lr, bytes [64 ks + 16 kg, +16)
+    const int wcol = n0 + lr < N ? n0 + lr : N - 1;
+    const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + kg * 16;
+    v4i wf[kKsw];
+#pragma unroll
+    for (int s = 0; s < kKsw; s++) {
+        const int ks = ks0 + s;
+        wf[s] = ks < nks ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64))
+                         : v4i{0, 0, 0, 0};
+    }
+    // activation chunks of the valid rows
+    const int nchunks = nks * 4 * rows;
+    float4 xv[kChunks][4];
+    int crow[kChunks], ck16[kChunks];
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int c = (int)threadIdx.x + j * nthreads;
+        crow[j] = c % rows;
+        ck16[j] = c / rows;
+        const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)(r0 + crow[j]) * K +
+                                                           (int64_t)ck16[j] * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            xv[j][q] = c < nchunks ? xp[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (threadIdx.x < 16) s_am[threadIdx.x] = 0u;
+    for (int i = threadIdx.x; i < 256; i += nthreads) s_acc[i] = 0;
+    __syncthreads();
+    // row absmax from 0 (engine.tkv:272-276: NaN never compares greater;
+    // fmaxf skips it, so the bits compared below are those of a finite or
+    // infinite non-negative value, ordered as unsigned integers)
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int c = (int)threadIdx.x + j * nthreads;
+        if (c < nchunks) {
+            float am = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) am = amax4(am, xv[j][q]);
+            atomicMax(&s_am[crow[j]], __float_as_uint(am));
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < rows) {
+        double dam = (double)__uint_as_float(s_am[threadIdx.x]);
+        if (dam < 0.00000001) dam = 0.00000001;
+        const double sc = dam / 127.0;  // unrounded f64 scale (engine.tkv:277-279)
+        s_inv[threadIdx.x] = 1.0 / sc;
+        s_sa[threadIdx.x] = (float)sc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int c = (int)threadIdx.x + j * nthreads;
+        if (c < nchunks) {
+            const double inv = s_inv[crow[j]];
+            const v4i q = {quant4(xv[j][0], inv), quant4(xv[j][1], inv), quant4(xv[j][2], inv),
+                           quant4(xv[j][3], inv)};
+            // ck16 = ks * 4 + kg
+            *reinterpret_cast<v4i*>(s_a + ((ck16[j] * 16 + crow[j]) << 4)) = q;
+        }
+    }
+    __syncthreads();
+
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < kKsw; s++) {
+        const int ks = ks0 + s;
+        if (ks < nks) {
+            const v4i af = lr < rows
+                               ? *reinterpret_cast<const v4i*>(s_a + (((ks * 4 + kg) * 16 + lr) << 4))
+                               : v4i{0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, wf[s], acc, 0, 0, 0);
+        }
+    }
+    // 16 x 16 result: lane holds column lane & 15, rows 4 (lane >> 4) + i
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (4 * kg + i < rows) atomicAdd(&s_acc[(4 * kg + i) * 16 + lr], acc[i]);
+    __syncthreads();
+    if (wave != 0) return;
+    const int col = n0 + lr;
+    if (col >= N) return;
+    const double swc = (double)sw[col];
+    const double bc = bias ? (double)bias[col] : 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * kg + i;
+        if (r < rows) {
+            double v = (double)s_acc[r * 16 + lr] * (double)s_sa[r];
+            v = v * swc;
+            v = v + bc;
+            __builtin_nontemporal_store((float)v, y + (int64_t)(r0 + r) * N + col);
+        }
+    }
+}
+
+}  // namespace
+
+// Tokens per row group: all of them up to 4; 4 up to 16 tokens, which keeps
+// a workgroup's activation bytes (RG K 4) at its weight bytes (16 K); 8
+// beyond, where more groups cost more in workgroup dispatch than their
+// bytes save (trace of the three decode shapes at M = 32, RG 4 / 8 / 16:
+// 7.7 / 7.0 / 7.4, 9.4 / 7.0 / 7.6, 11.4 / 9.6 / 12.7 us).  TKV_DECODE_RG
+// overrides it (sweeps).
+static int decode_rows_per_group(int64_t m) {
+    if (const char* v = getenv("TKV_DECODE_RG")) {
+        const int r = atoi(v);
+        if (r >= 1 && r <= 16) return r;
+    }
+    return m <= 4 ? (int)m : (m <= 16 ? 4 : 8);
+}
+
+int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t ldk,
+                     int64_t n, const float* scales_w, const float* bias, float* y) {
+    if (m < 1 || m > kDecodeMaxM || k % 64 != 0 || k / 64 > (int64_t)kMaxWaves * kKsw ||
+        ldk % 16 != 0 || ldk < k || !aligned(x, 16) || !aligned(w, 16) || n < 1 ||
+        n >= (1ll << 28))
+        return TKV_HIP_UNSUPPORTED;
+    const int rg = decode_rows_per_group(m);
+    const int64_t ncb = ceil_div(n, 16), ngr = ceil_div(m, (int64_t)rg);
+    const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
+    hipLaunchKernelGGL(k_decode_i8, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
+                       (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk, rg, (int)ncb, (int)ngr,
+                       scales_w, bias, y);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+}  // namespace tkv

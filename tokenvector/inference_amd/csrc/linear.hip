@@ -9,6 +9,7 @@
 // in HBM, as simd_gemm_packed_create keeps packed f32 tiles
 // (docs/HANDOFF.md:1675).
 #include <new>
+#include <string>
 
 #include "tkv_device.h"
 #include "tkv_internal.h"
@@ -80,6 +81,57 @@ static void weight_release(Weight* wt) {
     if (wt->scales) (void)hipFree(wt->scales);
     if (wt->bias) (void)hipFree(wt->bias);
     delete wt;
+}
+
+// The per-call part of CS1 on context c: activation calibrate + quantize
+// (per tensor or per token), GEMM, dequant + bias.
+static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t act_mode,
+                          float* y) {
+    if (!wt || !x || !y || m < 0) return set_error(TKV_HIP_BAD_ARG, "linear_forward: bad arguments");
+    if (m == 0) return TKV_HIP_OK;
+    const int64_t k = wt->k;
+    if (wt->format == TKV_HIP_WEIGHT_INT8 && act_mode == TKV_HIP_ACT_PER_TOKEN) {
+        // decode batches: quantize + GEMM + epilogue in one kernel, reading
+        // the weight through its padded row stride
+        const int rc = launch_decode_i8(c, x, m, k, static_cast<const uint8_t*>(wt->codes),
+                                        wt->ldk, wt->n, wt->scales, wt->bias, y);
+        if (rc != TKV_HIP_UNSUPPORTED) return rc;
+    }
+    if (wt->ldk != k)
+        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of the GEMM K step (128)");
+    void* qa;
+    TKV_RC_TRY(ctx_workspace(c, 0, (size_t)(m * k), &qa));
+    tkv_hip_qparams_dev* ap = c->params + 1;
+    if (wt->format == TKV_HIP_WEIGHT_INT8) {
+        I8Epilogue ep;
+        ep.mode = EPI_PER_CHANNEL;
+        ep.recipe = TKV_HIP_RECIPE_PRIMARY;
+        ep.scale_w = 0.0f;
+        ep.scales_w = wt->scales;
+        ep.bias = wt->bias;
+        if (act_mode == TKV_HIP_ACT_PER_TENSOR) {
+            TKV_RC_TRY(launch_quant_i8_dynamic(c, x, m * k, TKV_HIP_RECIPE_PRIMARY, ap, qa, false));
+            ep.scale_a = &ap->scale;
+            ep.scale_a_stride = 0;
+        } else if (act_mode == TKV_HIP_ACT_PER_TOKEN) {
+            void* sa;
+            TKV_RC_TRY(ctx_workspace(c, 1, (size_t)m * 4, &sa));
+            TKV_RC_TRY(launch_quant_rows(c, x, m, k, RM_DYNAMIC, nullptr, qa, false,
+                                         static_cast<float*>(sa), nullptr, 1));
+            ep.scale_a = static_cast<float*>(sa);
+            ep.scale_a_stride = 1;
+        } else {
+            return set_error(TKV_HIP_BAD_ARG, "linear_forward: unknown act_mode");
+        }
+        return launch_gemm_i8(c, static_cast<int8_t*>(qa), static_cast<int8_t*>(wt->codes), m,
+                              wt->n, k, ep, y);
+    }
+    if (act_mode != TKV_HIP_ACT_PER_TENSOR)
+        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: FP8 weights take per-tensor activations");
+    TKV_RC_TRY(launch_quant_fp8_dynamic(c, x, m * k, ap, qa, false));
+    return launch_gemm_f8(c, static_cast<uint8_t*>(qa), static_cast<uint8_t*>(wt->codes), m, wt->n,
+                          k, &ap->scale, 0, wt->scales, wt->bias, y,
+                          wt->format == TKV_HIP_WEIGHT_FP8_FAST);
 }
 
 }  // namespace tkv
@@ -189,45 +241,7 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
                                int32_t act_mode, float* y) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
-    Weight* wt = reinterpret_cast<Weight*>(weight);
-    if (!wt || !x || !y || m < 0) return set_error(TKV_HIP_BAD_ARG, "linear_forward: bad arguments");
-    if (m == 0) return TKV_HIP_OK;
-    if (wt->ldk != wt->k)
-        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of the GEMM K step (128)");
-    const int64_t k = wt->k;
-    void* qa;
-    TKV_RC_TRY(ctx_workspace(c, 0, (size_t)(m * k), &qa));
-    tkv_hip_qparams_dev* ap = c->params + 1;
-    if (wt->format == TKV_HIP_WEIGHT_INT8) {
-        I8Epilogue ep;
-        ep.mode = EPI_PER_CHANNEL;
-        ep.recipe = TKV_HIP_RECIPE_PRIMARY;
-        ep.scale_w = 0.0f;
-        ep.scales_w = wt->scales;
-        ep.bias = wt->bias;
-        if (act_mode == TKV_HIP_ACT_PER_TENSOR) {
-            TKV_RC_TRY(launch_quant_i8_dynamic(c, x, m * k, TKV_HIP_RECIPE_PRIMARY, ap, qa, false));
-            ep.scale_a = &ap->scale;
-            ep.scale_a_stride = 0;
-        } else if (act_mode == TKV_HIP_ACT_PER_TOKEN) {
-            void* sa;
-            TKV_RC_TRY(ctx_workspace(c, 1, (size_t)m * 4, &sa));
-            TKV_RC_TRY(launch_quant_rows(c, x, m, k, RM_DYNAMIC, nullptr, qa, false,
-                                         static_cast<float*>(sa), nullptr, 1));
-            ep.scale_a = static_cast<float*>(sa);
-            ep.scale_a_stride = 1;
-        } else {
-            return set_error(TKV_HIP_BAD_ARG, "linear_forward: unknown act_mode");
-        }
-        return launch_gemm_i8(c, static_cast<int8_t*>(qa), static_cast<int8_t*>(wt->codes), m,
-                              wt->n, k, ep, y);
-    }
-    if (act_mode != TKV_HIP_ACT_PER_TENSOR)
-        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: FP8 weights take per-tensor activations");
-    TKV_RC_TRY(launch_quant_fp8_dynamic(c, x, m * k, ap, qa, false));
-    return launch_gemm_f8(c, static_cast<uint8_t*>(qa), static_cast<uint8_t*>(wt->codes), m, wt->n,
-                          k, &ap->scale, 0, wt->scales, wt->bias, y,
-                          wt->format == TKV_HIP_WEIGHT_FP8_FAST);
+    return linear_forward(c, reinterpret_cast<Weight*>(weight), x, m, act_mode, y);
 }
 
 }  // extern "C"

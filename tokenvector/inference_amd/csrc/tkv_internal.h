@@ -197,6 +197,12 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
 // 32-element block (0 for any other dtype).
 int launch_gguf_blocks(Ctx* c, const uint8_t* raw, int64_t n, int dtype, float* out);
 int64_t gguf_block_bytes(int dtype);
+// decode.hip: the per-token W8A8 linear of decode batches in one kernel
+// (M <= 32, K % 64 == 0, K <= 3072, x 16-byte aligned; UNSUPPORTED
+// otherwise, with nothing launched): rowwise absmax + int8 quantize of x,
+// INT8 GEMM against W [n, ldk], y = fl32(fl64(fl64(acc * sa[m]) * sw[n]) + b[n]).
+int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t ldk,
+                     int64_t n, const float* scales_w, const float* bias, float* y);
 // K granularity of the GEMM main loop: operands whose row stride is a
 // multiple of it (and 16-byte aligned) run without repacking.
 int64_t gemm_k_align();
