@@ -368,6 +368,21 @@ int32_t tkv_hip_weight_info(int64_t handle, void** codes, float** scales, float*
 #define TKV_HIP_ACT_PER_TOKEN 1
 int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int64_t m,
                                int32_t act_mode, float* y);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tkv_hip_linear_forward on the caller's stream (NULL:
+ * the default stream) with every scratch buffer in one fixed area per GPU
+ * inside the library's code object -- activation codes up to
+ * TKV_HIP_STATIC_CODES_BYTES (m * k), per-token scales for up to 65536 rows,
+ * calibration partials and per-call parameters.  It calls no hipMalloc,
+ * hipFree or other allocating routine (the area is resolved once per device
+ * on the first call).  INT8 weights only (FP8: TKV_HIP_UNSUPPORTED); larger
+ * m * k or m: TKV_HIP_BAD_ARG.  Every call on a GPU shares that GPU's area,
+ * which keeps the last call's contents: calls that overlap on one GPU (other
+ * streams, other threads) race, so order them on one stream. */
+#define TKV_HIP_STATIC_CODES_BYTES (32ll << 20)
+int32_t tkv_hip_linear_forward_static(int64_t weight, const float* x, int64_t m,
+                                      int32_t act_mode, float* y, void* stream);
 
 /* ======================================================================== */
 /* Grouped INT4 weights (tv/quantization/int4.tkv) and GGUF block formats   */

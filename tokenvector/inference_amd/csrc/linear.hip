@@ -8,6 +8,7 @@
 // weight handle keeps the packed codes, per-channel scales and bias resident
 // in HBM, as simd_gemm_packed_create keeps packed f32 tiles
 // (docs/HANDOFF.md:1675).
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -134,6 +135,53 @@ static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t
                           wt->format == TKV_HIP_WEIGHT_FP8_FAST);
 }
 
+// ---------------------------------------------------------------------------
+// Fixed scratch of tkv_hip_linear_forward_static, for callers that cannot
+// allocate: one area per device, in the code object's own device memory, so
+// no call ever allocates.  Layout (256-byte aligned parts):
+//   activation codes   TKV_HIP_STATIC_CODES_BYTES
+//   per-token scales   kStaticMaxRows f32
+//   calibration partials, per-call params
+//   split-K partial sums and arrival counts (zero at load; every call that
+//   can use them clears them first)
+// Host code never names `scratch` directly as an address (on the host it is
+// a stand-in symbol): static_scratch() resolves each device's copy once with
+// hipGetSymbolAddress and every launch takes that pointer.
+// ---------------------------------------------------------------------------
+constexpr int64_t kStaticMaxRows = 65536;
+constexpr size_t kAlign256(size_t v) { return (v + 255) & ~size_t(255); }
+constexpr size_t kOffCodes = 0;
+constexpr size_t kOffScales = kAlign256(kOffCodes + (size_t)TKV_HIP_STATIC_CODES_BYTES);
+constexpr size_t kOffPartials = kAlign256(kOffScales + (size_t)kStaticMaxRows * 4);
+constexpr size_t kOffParams = kAlign256(kOffPartials + sizeof(RedPartial) * kMaxReduceBlocks);
+constexpr size_t kOffGemv = kAlign256(kOffParams + sizeof(tkv_hip_qparams_dev) * 64);
+constexpr size_t kOffArrivals = kOffGemv + (size_t)kGemvSplitBlocks * 1024 * sizeof(int32_t);
+constexpr size_t kOffScratchEnd = kAlign256(kOffArrivals + (size_t)kGemvSplitBlocks * sizeof(unsigned));
+
+static __device__ __align__(256) uint8_t scratch[kOffScratchEnd];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[kMaxDevices];
+static int g_scratch_cus[kMaxDevices];
+
+// The calling thread's current device must be `dev`.
+static int static_scratch(int dev, uint8_t** out, int* cus) {
+    if (dev < 0 || dev >= kMaxDevices) return set_error(TKV_HIP_NO_DEVICE, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        TKV_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        int n = 0;
+        TKV_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        g_scratch_cus[dev] = n;
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    *cus = g_scratch_cus[dev];
+    return TKV_HIP_OK;
+}
+
 }  // namespace tkv
 
 using namespace tkv;
@@ -242,6 +290,48 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
     return linear_forward(c, reinterpret_cast<Weight*>(weight), x, m, act_mode, y);
+}
+
+int32_t tkv_hip_linear_forward_static(int64_t weight, const float* x, int64_t m,
+                                      int32_t act_mode, float* y, void* stream) {
+    Weight* wt = reinterpret_cast<Weight*>(weight);
+    if (!wt || !x || !y || m < 0)
+        return set_error(TKV_HIP_BAD_ARG, "linear_forward_static: bad arguments");
+    if (wt->format != TKV_HIP_WEIGHT_INT8)
+        return set_error(TKV_HIP_UNSUPPORTED, "linear_forward_static: INT8 weights only");
+    if (m * wt->k > TKV_HIP_STATIC_CODES_BYTES || m > kStaticMaxRows)
+        return set_error(TKV_HIP_BAD_ARG,
+                         "linear_forward_static: m * k = " + std::to_string(m * wt->k) +
+                             " activation codes (or m = " + std::to_string(m) +
+                             " rows) exceed the static scratch (" +
+                             std::to_string(TKV_HIP_STATIC_CODES_BYTES) + " bytes, " +
+                             std::to_string(kStaticMaxRows) + " rows)");
+    if (m == 0) return TKV_HIP_OK;
+    TKV_HIP_TRY(hipSetDevice(wt->device));
+    uint8_t* base;
+    int cus;
+    TKV_RC_TRY(static_scratch(wt->device, &base, &cus));
+    Ctx c;
+    c.device = wt->device;
+    c.num_cus = cus;
+    c.stream = static_cast<hipStream_t>(stream);
+    c.own_stream = nullptr;
+    c.no_alloc = true;
+    c.partials = reinterpret_cast<RedPartial*>(base + kOffPartials);
+    c.params = reinterpret_cast<tkv_hip_qparams_dev*>(base + kOffParams);
+    c.gemv_part = reinterpret_cast<int32_t*>(base + kOffGemv);
+    c.gemv_arrivals = reinterpret_cast<unsigned*>(base + kOffArrivals);
+    c.ws[0] = base + kOffCodes;
+    c.ws_bytes[0] = (size_t)TKV_HIP_STATIC_CODES_BYTES;
+    c.ws[1] = base + kOffScales;
+    c.ws_bytes[1] = (size_t)kStaticMaxRows * 4;
+    // The split-K skinny GEMM (per-tensor activations, m <= 32) needs its
+    // partial sums and arrival counts at zero; its kernels leave them so,
+    // but this area is shared by every call on the device: clear them (a
+    // fill kernel, which a stream capture records as a kernel node).
+    if (act_mode == TKV_HIP_ACT_PER_TENSOR && m <= 32)
+        TKV_RC_TRY(launch_fill(&c, c.gemv_part, 0, kOffScratchEnd - kOffGemv));
+    return linear_forward(&c, wt, x, m, act_mode, y);
 }
 
 }  // extern "C"

@@ -134,6 +134,10 @@ int ctx_get(int64_t handle, Ctx** out) {
 
 int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out) {
     if (bytes == 0) bytes = 256;
+    if (c->ws_bytes[slot] < bytes && c->no_alloc)
+        return set_error(TKV_HIP_BAD_ARG, "workspace slot " + std::to_string(slot) + " needs " +
+                                              std::to_string(bytes) +
+                                              " bytes, beyond this call's fixed scratch");
     if (c->ws_bytes[slot] < bytes) {
         // growing synchronizes the stream and reallocates: not capturable
         if (c->capturing)

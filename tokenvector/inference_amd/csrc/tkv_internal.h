@@ -73,6 +73,9 @@ struct Ctx {
     // with the context) instead of freeing it.
     int live_graphs = 0;
     std::vector<void*> retired;
+    // A context over caller-fixed memory (the static-scratch entry point):
+    // its workspaces never grow; a call that would need more fails.
+    bool no_alloc = false;
 };
 
 int ctx_create(int device, Ctx** out);
