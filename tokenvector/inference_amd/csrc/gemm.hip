@@ -471,9 +471,9 @@ __device__ __forceinline__ void store_part_dyn(int part, const uint32_t (&v)[C::
     static_assert(C::TM * 16 <= 64, "parts");
     switch (part) {
 #define TKV_PART(p)                                                                      \
-    case p:                                                                              \
-        if constexpr (p < C::TM * 16) {                                                  \
-            constexpr int i = p / 16 < C::TM ? p / 16 : 0, r = p % 16;                  \
+    case (p):                                                                            \
+        if constexpr ((p) < C::TM * 16) {                                                \
+            constexpr int i = (p) / 16 < C::TM ? (p) / 16 : 0, r = (p) % 16;            \
             uint32_t* rowp = yw + (int64_t)(i * 32 + (r >> 2) * 8 + (r & 3)) * N;        \
             _Pragma("unroll") for (int j = 0; j < C::TN; j++)                            \
                 put(rowp + loff + j * 32, v[i][j][r]);                                   \

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void k_fp8_encode_rows(const float* __restrict
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
     const float mul = 1.0f / s[r];
-    for (int64_t c = lane; c < cols; c += 64) q[r * ldq + c] = (uint8_t)e4m3_encode(x[r * cols + c] * mul);
+    for (int64_t c = lane; c < cols; c += 64) q[r * ldq + c] = (uint8_t)e4m3_encode1(x[r * cols + c] * mul);
 }
 
 // FP8 per-channel scales: s[r] = fl32(max(|x[r,:]|, 1e-8) / kFp8Target).

@@ -580,14 +580,16 @@ int launch_dequant_i8(Ctx* c, const void* q, bool in_i32, int64_t rows, int64_t 
 // reference's int32 codes (byte - 128).  With `scaled` the input is first
 // multiplied by fl32(1 / scale) in f32 (extension for per-tensor FP8).
 // ---------------------------------------------------------------------------
+// Four packed e4m3 bytes (element 0 in bits 7:0) as raw bytes, or as the
+// reference's int32 codes (byte - 128).
 template <bool OUT_I32>
-__device__ __forceinline__ void store4_fp8(void* q, int64_t i4, uint32_t a, uint32_t b,
-                                           uint32_t c, uint32_t d) {
+__device__ __forceinline__ void store_fp8x4(void* q, int64_t i4, uint32_t w) {
     if (OUT_I32)
         reinterpret_cast<int4*>(q)[i4] =
-            make_int4((int)a - 128, (int)b - 128, (int)c - 128, (int)d - 128);
+            make_int4((int)(w & 0xffu) - 128, (int)((w >> 8) & 0xffu) - 128,
+                      (int)((w >> 16) & 0xffu) - 128, (int)(w >> 24) - 128);
     else
-        reinterpret_cast<uint32_t*>(q)[i4] = a | (b << 8) | (c << 16) | (d << 24);
+        reinterpret_cast<uint32_t*>(q)[i4] = w;
 }
 
 template <bool OUT_I32>
@@ -614,8 +616,7 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
                 v[u].z *= mul;
                 v[u].w *= mul;
             }
-            store4_fp8<OUT_I32>(q, i + u * stride, e4m3_encode(v[u].x), e4m3_encode(v[u].y),
-                                e4m3_encode(v[u].z), e4m3_encode(v[u].w));
+            store_fp8x4<OUT_I32>(q, i + u * stride, e4m3_encode4(v[u].x, v[u].y, v[u].z, v[u].w));
         }
     }
     for (; i < n4; i += stride) {
@@ -626,13 +627,12 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
             v.z *= mul;
             v.w *= mul;
         }
-        store4_fp8<OUT_I32>(q, i, e4m3_encode(v.x), e4m3_encode(v.y), e4m3_encode(v.z),
-                            e4m3_encode(v.w));
+        store_fp8x4<OUT_I32>(q, i, e4m3_encode4(v.x, v.y, v.z, v.w));
     }
     for (int64_t j = n4 * 4 + tid; j < n; j += stride) {
         float v = x[j];
         if (scaled) v *= mul;
-        uint32_t e = e4m3_encode(v);
+        uint32_t e = e4m3_encode1(v);
         if (OUT_I32)
             reinterpret_cast<int32_t*>(q)[j] = (int)e - 128;
         else
@@ -644,11 +644,13 @@ int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_d
                       void* q, bool out_i32) {
     if (n <= 0) return TKV_HIP_OK;
     int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
-    // The e4m3 encode is ALU-heavy (about 27 operations per element): six
-    // blocks per CU overlap it with the loads better than the light streams'
-    // two (46.6 against 50.9 us at 201 MB, same box, interleaved medians).
+    // The e4m3 encode costs more ALU work per element than the int8 quantize
+    // (the hardware conversion plus the reference's fix-ups, ~12 operations
+    // per element): three blocks per CU overlap it with the loads best (at
+    // 201 MB: 43.9 us against 46.7 / 48.2 / 46.0 / 46.4 us at 2 / 4 / 6 / 8,
+    // same box, medians of four interleaved rounds).
     int64_t blocks = ceil_div(vec ? n / 4 : n, (int64_t)kBlock * kUnroll);
-    const int64_t cap = (int64_t)c->num_cus * (vec ? 6 : 16);
+    const int64_t cap = (int64_t)c->num_cus * (vec ? 3 : 16);
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     if (out_i32)

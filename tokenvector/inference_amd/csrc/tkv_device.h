@@ -52,6 +52,46 @@ __device__ __forceinline__ uint32_t e4m3_encode(float x) {
     return mag > 0x7f800000u ? 0x38u : code;
 }
 
+// The same codes through the hardware conversion.  The reference encoder is
+// OCP e4m3 with round to nearest even everywhere except its three departures
+// and the non-finite inputs above (the integer form above checks that on all
+// 2^32 inputs), so the code of |x| comes from v_cvt_pk_fp8_f32 (OCP e4m3fn,
+// nearest even) and only those cases are patched, on the magnitude bits:
+//   |x| >= 248 -> 0x7E (the hardware gives 0x78 .. 0x7F there);
+//   |x| < 2^-6 -> at most 0x07 (the hardware rounds [7.5 * 2^-9, 2^-6) up to
+//                0x08, the reference clamps the subnormal round-up);
+//   the sign bit unless x is +-0 (-0.0 -> 0x00; a nonzero value that rounds
+//   to zero keeps its sign, 0x80, as in the reference);
+//   +-inf -> 0x7F|sign, NaN -> 0x38.
+// f32 subnormal inputs round to code 0 either way.
+__device__ __forceinline__ uint32_t e4m3_fix(uint32_t bits, uint32_t c) {
+    const uint32_t mag = bits & 0x7fffffffu, sign = (bits >> 24) & 0x80u;
+    c = mag >= 0x43780000u ? 0x7eu : c;
+    c = (mag < 0x3c800000u && c > 7u) ? 7u : c;
+    c |= mag != 0u ? sign : 0u;
+    c = mag == 0x7f800000u ? (sign | 0x7fu) : c;
+    return mag > 0x7f800000u ? 0x38u : c;
+}
+
+// Four codes packed little-endian (a in bits 7:0).
+__device__ __forceinline__ uint32_t e4m3_encode4(float a, float b, float c, float d) {
+    const uint32_t ba = __float_as_uint(a), bb = __float_as_uint(b);
+    const uint32_t bc = __float_as_uint(c), bd = __float_as_uint(d);
+    int hw = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(ba & 0x7fffffffu),
+                                             __uint_as_float(bb & 0x7fffffffu), 0, false);
+    hw = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(bc & 0x7fffffffu),
+                                         __uint_as_float(bd & 0x7fffffffu), hw, true);
+    const uint32_t h = (uint32_t)hw;
+    return e4m3_fix(ba, h & 0xffu) | (e4m3_fix(bb, (h >> 8) & 0xffu) << 8) |
+           (e4m3_fix(bc, (h >> 16) & 0xffu) << 16) | (e4m3_fix(bd, h >> 24) << 24);
+}
+
+__device__ __forceinline__ uint32_t e4m3_encode1(float a) {
+    const uint32_t ba = __float_as_uint(a);
+    const int hw = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(ba & 0x7fffffffu), 0.0f, 0, false);
+    return e4m3_fix(ba, (uint32_t)hw & 0xffu);
+}
+
 // e4m3 decode of the reference (types.tkv:193-226 through f32_bits_to_f64,
 // f32_bits.tkv:60-74), f32 result.  Differs from OCP in three places that the
 // reference fixes: subnormal m decodes to m * 2^-10 (normalisation uses
