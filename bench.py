@@ -395,6 +395,47 @@ def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
     out["config"] = f"M={m} x {cols} f32 (config 2, largest)"
     for b in xs:
         b.close()
+    out["activations"] = bench_act_quant(ctx, D, O)
+    return out
+
+
+def bench_act_quant(ctx, D, O, reps=24):
+    """Per-tensor calibrate + quantize of the step's activations (configs[2]:
+    8192 x 768 for qkv / attn_out / mlp_up, 8192 x 3072 for mlp_down).
+    `cold` rotates distinct inputs totalling more than the 256 MB Infinity
+    Cache, so x comes from HBM; `warm` repeats one input, as in the step,
+    where x was just written by the previous kernel.  Bytes are the HBM
+    algorithmic bytes: x once (4 B) + the codes (1 B) per element; the
+    two-kernel path reads x a second time, from the Infinity Cache when x
+    fits it, which these bytes do not count."""
+    out = {}
+    for rows, cols in ((8192, 768), (8192, 3072)):
+        n = rows * cols
+        x = O.add_outliers(O.gi_noise(n, 3, 1.0), 0.001, 3, 4, 20.0)
+        nbuf = max(2, -(-(320 << 20) // (4 * n)))
+        xs = [D.DeviceBuffer.from_host(ctx, x) for _ in range(nbuf)]
+        q8 = D.DeviceBuffer.empty(ctx, n, np.int8)
+        p = D.params_buffer(ctx)
+        res = {}
+        for label, pick in (("cold", lambda i: xs[i % nbuf]), ("warm", lambda i: xs[0])):
+            for i in range(3):
+                D.quantize_int8_dynamic_tensor(ctx, pick(i), n, q8, p)
+            e0, e1 = D.Event(), D.Event()
+            ctx.synchronize()
+            e0.record(ctx)
+            for i in range(reps):
+                D.quantize_int8_dynamic_tensor(ctx, pick(i), n, q8, p)
+            e1.record(ctx)
+            us = e0.elapsed_ms(e1) / reps * 1e3
+            res[f"{label}_us"] = round(us, 2)
+            res[f"{label}_GBps"] = round(5 * n / (us * 1e-6) / 1e9, 1)
+        res["cold_frac_of_hbm"] = round(res["cold_GBps"] / PEAK_HBM_GBPS, 3)
+        out[f"{rows}x{cols}"] = res
+        for b in xs:
+            b.close()
+        q8.close()
+    out["note"] = ("tkv_hip_dev_quantize_int8_dynamic_tensor; GB/s over 5 B/element (x read "
+                   "once + int8 codes); us per call over back-to-back calls")
     return out
 
 

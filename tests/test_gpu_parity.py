@@ -407,6 +407,95 @@ def test_int8_dynamic_tensor(ctx, n, offset):
                               O.quantize_int8_symmetric(x, want_p.scale))
 
 
+# Activation-sized tensors around 8192 x 768 and beyond (float4 tails of 0 and
+# 4 elements past multiples of 256 * 512 * 4).
+RES_UNIT = 256 * 512 * 4
+RES_SIZES = [RES_UNIT * r + d for r in (4, 8, 16, 24, 32) for d in (0, 4)] + [2 ** 20]
+
+
+def _res_input(n, seed):
+    x = _x(n, seed, 1.0)
+    return O.add_outliers(x, 0.001, 3, 4, 20.0)
+
+
+def _dyn_quant(ctx, x):
+    n = x.size
+    dx = D.DeviceBuffer.from_host(ctx, x)
+    dq = D.DeviceBuffer.empty(ctx, n, np.int8)
+    p = D.params_buffer(ctx)
+    D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
+    ctx.synchronize()
+    return D.read_params(p), dq.download().astype(np.int32)
+
+
+@pytest.mark.parametrize("n", RES_SIZES)
+def test_int8_dynamic_tensor_activation_sizes(ctx, n):
+    """calibrate + quantize on activation-sized tensors: QuantParams and codes
+    bit-exact against the oracle."""
+    say(f"int8 dynamic tensor activation size n={n}")
+    x = _res_input(n, 5 + n % 997)
+    got_p, got_q = _dyn_quant(ctx, x)
+    want_p = O.calibrate_minmax(x, 1)
+    assert _same_f32([got_p.scale, got_p.min_val, got_p.max_val],
+                     [want_p.scale, want_p.min_val, want_p.max_val])
+    assert np.array_equal(got_q, O.quantize_int8_symmetric(x, want_p.scale))
+
+
+@pytest.mark.parametrize("case", ["nan_first", "nan_inside", "inf", "zeros", "tiny", "ties",
+                                  "negative_extreme"])
+def test_int8_dynamic_tensor_specials(ctx, case):
+    """NaN (first element and inside), infinities, an all-zero tensor (the
+    1e-8 scale floor), values below the floor, exact .5 ties of x * inv and a
+    negative extreme, at an activation size: bit-exact against the oracle."""
+    n = 3 * RES_UNIT
+    say(f"int8 dynamic tensor special={case}")
+    x = _res_input(n, 77)
+    if case == "nan_first":
+        x[0] = np.nan
+    elif case == "nan_inside":
+        x[RNG.integers(1, n, 64)] = np.nan
+    elif case == "inf":
+        x[12345] = np.inf
+        x[n - 1] = -np.inf
+    elif case == "zeros":
+        x[:] = 0.0
+        x[7] = -0.0
+    elif case == "tiny":
+        x = (x * np.float32(1e-12)).astype(np.float32)
+    elif case == "ties":
+        # amax 127 gives scale 1 and inv 1: every k + 0.5 is an exact tie
+        x = (np.round(x * 20) / 2).astype(np.float32)
+        x[0] = 127.0
+        x = np.clip(x, -127.0, 127.0).astype(np.float32)
+    elif case == "negative_extreme":
+        x[999] = -50.0
+    got_p, got_q = _dyn_quant(ctx, x)
+    want_p = O.calibrate_minmax(x, 1)
+    assert _same_f32([got_p.scale, got_p.min_val, got_p.max_val],
+                     [want_p.scale, want_p.min_val, want_p.max_val])
+    assert np.array_equal(got_q, O.quantize_int8_symmetric(x, want_p.scale))
+
+
+def test_int8_dynamic_tensor_repeated(ctx):
+    """Back-to-back calls of different sizes on one context, no sync between
+    them (the context's partials are reused by every call)."""
+    sizes = [RES_SIZES[0], RES_SIZES[5], 2 ** 20, RES_SIZES[2]] * 3
+    xs = {n: _res_input(n, n % 101) for n in set(sizes)}
+    bufs = {n: (D.DeviceBuffer.from_host(ctx, xs[n]), D.DeviceBuffer.empty(ctx, n, np.int8))
+            for n in xs}
+    ps = [D.params_buffer(ctx) for _ in sizes]
+    for i, n in enumerate(sizes):
+        D.quantize_int8_dynamic_tensor(ctx, bufs[n][0], n, bufs[n][1], ps[i])
+    ctx.synchronize()
+    for i, n in enumerate(sizes):
+        want_p = O.calibrate_minmax(xs[n], 1)
+        assert _same_f32([D.read_params(ps[i]).scale], [want_p.scale])
+    for n in xs:
+        want_p = O.calibrate_minmax(xs[n], 1)
+        assert np.array_equal(bufs[n][1].download().astype(np.int32),
+                              O.quantize_int8_symmetric(xs[n], want_p.scale))
+
+
 @pytest.mark.parametrize("n", [1, 1000, 5 * GRID_CHUNK + 7, 8192 * 768, 32 * GRID_CHUNK,
                                8192 * 3072])
 def test_fp8_dynamic_tensor(ctx, n):
