@@ -158,9 +158,14 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
     return 2 * k * 2.0 ** -53 * s.reshape(-1) + np.spacing(np.abs(yref)).astype(np.float64)
 
 
+# 2 <= M <= 32 with K % 32 == 0 takes the decode kernel (16-column workgroups,
+# K split over workgroups when the column blocks are few: (16, 200, 256) in 2,
+# (32, 130, 512) in 4, (17, 1000, 1024) in 3); M = 1 and (3, 50, 80, 16), whose
+# K % 32 != 0, take the per-column kernel.
 GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 256, 64),
-               (32, 130, 512, 128), (70, 130, 256, 64), (33, 2304, 768, 128),
-               (300, 768, 768, 128), (129, 768, 3072, 32)]
+               (32, 130, 512, 128), (17, 1000, 1024, 128), (3, 50, 80, 16),
+               (70, 130, 256, 64), (33, 2304, 768, 128), (300, 768, 768, 128),
+               (129, 768, 3072, 32)]
 
 
 @pytest.mark.parametrize("m,n,k,gs", GEMM_SHAPES)
@@ -207,6 +212,48 @@ def test_int4_matmul_dyadic_exact_and_errors(hip):
         I4.matmul_int4_grouped(a, pk, b, y, m, n, k - 1, 51, sc)    # odd K
     with pytest.raises(_lib.TkvHipError):
         I4.matmul_int4_grouped_ordered(a, pk, b, y, m, n, k, gs, sc, np.full(k, k, np.int64))
+
+
+@pytest.mark.parametrize("m", [1, 4, 17, 32])
+@pytest.mark.parametrize("name,n,k", [("qkv", 2304, 768), ("attn_out", 768, 768),
+                                      ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)])
+def test_int4_decode_gpt2_shapes(ctx, name, n, k, m):
+    """Decode batches on the four GPT-2 shapes (group size 128), device
+    buffers: every output within the reordering bound of the oracle, and a
+    second launch bit-identical (the split-K reduction has a fixed order)."""
+    gs = 128
+    say(f"int4 decode {name} m={m}")
+    a = O.gi_noise(m * k, 31 + m, 1.0)
+    w = _weights(n, k, 37)
+    pk, sc = O.quantize_int4_grouped(w, n, k, gs)
+    b = O.gi_noise(n, 41, 0.01)
+    da, db = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, b)
+    dw = D.DeviceBuffer.from_host(ctx, pk.astype(np.uint8))
+    ds = D.DeviceBuffer.from_host(ctx, sc)
+    dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+    D.matmul_int4_grouped(ctx, da, dw, ds, db, None, dy, m, n, k, gs)
+    y = dy.download()
+    ref = O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc)
+    assert np.all(np.abs(y.astype(np.float64).reshape(-1) - ref) <=
+                  _gemm_bound(a, pk, sc, b, m, n, k, gs, ref))
+    for _ in range(2):
+        D.matmul_int4_grouped(ctx, da, dw, ds, db, None, dy, m, n, k, gs)
+        assert np.array_equal(dy.download(), y)
+
+
+def test_int4_decode_dyadic_exact(hip):
+    """Dyadic inputs through the decode kernel with a K split over
+    workgroups: every partial sum is exact, so the result is the reference's
+    bit for bit."""
+    for m, n, k, gs in ((32, 72, 512, 32), (9, 40, 256, 64)):
+        say(f"int4 decode dyadic {m}x{n}x{k}")
+        a = (RNG.integers(-64, 64, m * k) / 16.0).astype(np.float32)
+        pk = RNG.integers(0, 256, n * k // 2).astype(np.int32)
+        sc = (2.0 ** -RNG.integers(1, 6, n * k // gs)).astype(np.float32)
+        b = (RNG.integers(-8, 8, n) / 8.0).astype(np.float32)
+        y = np.zeros(m * n, np.float32)
+        I4.matmul_int4_grouped(a, pk, b, y, m, n, k, gs, sc)
+        assert np.array_equal(y, O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc))
 
 
 def test_int4_matmul_gpt2_full_size_rows(ctx):

@@ -18,6 +18,8 @@
 //
 // Codes are packed bytes on the device ([rows, cols / 2], low nibble = even
 // column); the host mirrors move the reference's int32-per-byte lists.
+#include <cstdlib>
+
 #include "tkv_device.h"
 #include "tkv_internal.h"
 
@@ -360,6 +362,154 @@ __global__ __launch_bounds__(256) void k_gemv_int4_f64(
         }
 }
 
+// Decode batches on the f64 MFMA (M <= 16 MB rows, K % 32 == 0, gs % 8 == 0,
+// no column permutation).  A workgroup of kDecWaves waves owns 16 output
+// columns and one of `splits` contiguous ranges of 32-deep k blocks; its waves
+// divide that range again.  Within a k block, lane group g = lane / 16 takes
+// k = 32 kb + 8 g + s at MFMA step s (the same permutation of k for A and W,
+// so every product x * w still meets its partner): one 16-byte A load per row
+// block and one 4-byte weight load (8 nibbles, one scale) per lane cover 8
+// steps.  w = (nibble - 8) * scale is formed once per lane and shared by all
+// rows through the MFMA, and the activations are read from L2 once per
+// 16-column workgroup instead of once per column.
+//   The waves' partial sums are added in LDS in wave order.  With splits > 1
+// each workgroup writes its partial tile to `part` and counts itself in on
+// arrivals[cb]; the workgroup that completes the count adds the splits' tiles
+// in split order, adds the bias, stores y and clears the count.  Every output
+// is therefore the same fixed-order f64 sum on every run.
+//   Ordering without cache maintenance: the tiles are written with agent-scope
+// atomic stores and read with agent-scope atomic loads, which gfx950 performs
+// at the device coherence point (sc1: not held in, or served from, an XCD's
+// L2).  Every wave waits for its own stores to complete (vmcnt(0): an atomic
+// store completes once it is performed there) before the workgroup barrier,
+// and the arrival add is issued after that barrier; the completing workgroup
+// issues its tile loads only after its arrival add has returned.  So every
+// tile is in place before any load of it is issued.  A release add with an
+// acquire fence would instead write back and invalidate a whole L2 per
+// workgroup: measured at ~20 us per call over ~500 workgroups.
+constexpr int kDecWaves = 4;
+
+template <int MB>
+__global__ __launch_bounds__(kDecWaves * 64) void k_gemv_int4_mfma(
+    const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
+    const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int gs,
+    int splits, double* __restrict__ part, unsigned* __restrict__ arrivals) {
+    __shared__ double sP[kDecWaves][MB * 16][17];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cb = (int)blockIdx.x / splits, sp = (int)blockIdx.x % splits;
+    const int n0 = cb * 16;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int nkb = K / 32;
+    const int lo = (int)((int64_t)nkb * sp / splits), hi = (int)((int64_t)nkb * (sp + 1) / splits);
+    const int wlo = lo + (hi - lo) * wave / kDecWaves, whi = lo + (hi - lo) * (wave + 1) / kDecWaves;
+    const int half = K / 2, ng = K / gs;
+    // rows past M and columns past N read row 0 / column N - 1; they are never stored
+    const float* __restrict__ arow[MB];
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+        const int r = 16 * i + l16;
+        arow[i] = A + (int64_t)(r < M ? r : 0) * K + 8 * g;
+    }
+    const int col = n0 + l16 < N ? n0 + l16 : N - 1;
+    const uint8_t* __restrict__ wrow = Wp + (int64_t)col * half + 4 * g;
+    const float* __restrict__ srow = scales + (int64_t)col * ng;
+    f64x4 acc[MB];
+#pragma unroll
+    for (int i = 0; i < MB; i++) acc[i] = f64x4{0.0, 0.0, 0.0, 0.0};
+    // each k block's operands are loaded one block ahead, so their latency
+    // overlaps the previous block's MFMAs
+    float4 an[MB][2];
+    uint32_t wn = 0;
+    float sn = 0.0f;
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            const float4* p = reinterpret_cast<const float4*>(arow[i] + 32 * kb);
+            an[i][0] = p[0];
+            an[i][1] = p[1];
+        }
+        wn = *reinterpret_cast<const uint32_t*>(wrow + 16 * kb);
+        sn = srow[(32 * kb + 8 * g) / gs];
+    };
+    if (wlo < whi) fetch(wlo);
+    for (int kb = wlo; kb < whi; kb++) {
+        float4 a[MB][2];
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            a[i][0] = an[i][0];
+            a[i][1] = an[i][1];
+        }
+        const uint32_t w8 = wn;
+        const double sc = (double)sn;
+        if (kb + 1 < whi) fetch(kb + 1);
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const double b = (double)((int)((w8 >> (4 * s)) & 15) - 8) * sc;
+#pragma unroll
+            for (int i = 0; i < MB; i++) {
+                const float4 q = a[i][s >> 2];
+                const float x = (s & 3) == 0 ? q.x : (s & 3) == 1 ? q.y : (s & 3) == 2 ? q.z : q.w;
+                acc[i] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)x, b, acc[i], 0, 0, 0);
+            }
+        }
+    }
+    // D layout: lane l, register v holds row l / 16 + 4 v, column l % 16
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) sP[wave][16 * i + g + 4 * v][l16] = acc[i][v];
+    __syncthreads();
+    constexpr int kT = MB * 16 * 16;  // outputs of the tile
+    double sum[(kT + kDecWaves * 64 - 1) / (kDecWaves * 64)];
+#pragma unroll
+    for (int e = 0; e < (kT + kDecWaves * 64 - 1) / (kDecWaves * 64); e++) {
+        const int t = threadIdx.x + e * kDecWaves * 64;
+        double v = 0.0;
+        if (t < kT) {
+            const int r = t / 16, c = t % 16;
+            v = sP[0][r][c];
+#pragma unroll
+            for (int w = 1; w < kDecWaves; w++) v = v + sP[w][r][c];
+        }
+        sum[e] = v;
+    }
+    if (splits > 1) {
+        double* mine = part + (int64_t)blockIdx.x * kT;
+#pragma unroll
+        for (int e = 0; e < (kT + kDecWaves * 64 - 1) / (kDecWaves * 64); e++) {
+            const int t = threadIdx.x + e * kDecWaves * 64;
+            if (t < kT) __hip_atomic_store(mine + t, sum[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_last = __hip_atomic_fetch_add(arrivals + cb, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(splits - 1);
+        __syncthreads();
+        if (!s_last) return;
+        double* tiles = part + (int64_t)cb * splits * kT;
+#pragma unroll
+        for (int e = 0; e < (kT + kDecWaves * 64 - 1) / (kDecWaves * 64); e++) {
+            const int t = threadIdx.x + e * kDecWaves * 64;
+            if (t < kT) {
+                double v = __hip_atomic_load(tiles + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int q = 1; q < splits; q++)
+                    v = v + __hip_atomic_load(tiles + (int64_t)q * kT + t, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                sum[e] = v;
+            }
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(arrivals + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int e = 0; e < (kT + kDecWaves * 64 - 1) / (kDecWaves * 64); e++) {
+        const int t = threadIdx.x + e * kDecWaves * 64;
+        const int r = t / 16, c = n0 + t % 16;
+        if (t < kT && r < M && c < N) Y[(int64_t)r * N + c] = (float)(sum[e] + (bias ? (double)bias[c] : 0.0));
+    }
+}
+
 // ---------------------------------------------------------------------------
 // GGUF Q8_0 / Q4_0 / Q4_1 blocks (gguf.tkv:284-313)
 // ---------------------------------------------------------------------------
@@ -480,6 +630,40 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX || (n + kGBN - 1) / kGBN > INT32_MAX ||
         (m + kGBM - 1) / kGBM > 65535)
         return set_error(TKV_HIP_UNSUPPORTED, "matmul_int4_grouped: sizes beyond the grid");
+    // Decode batches of 2..32 rows: 16-column workgroups on the f64 MFMA, K
+    // split over workgroups until the grid is about half the CUs (one
+    // counter per column block).  A single row keeps the per-column kernel.
+    // Sweep over the four GPT-2 shapes (us per call, HIP events, M = 1 / 4 /
+    // 16 / 32, per-column kernel first): qkv 4.6 / 8.2 / 21.7 / 40.4 against
+    // 6.3 / 6.5 / 7.2 / 10.3, mlp_down 8.7 / 20.0 / 55.6 / 108.4 against
+    // 9.2 / 9.3 / 10.0 / 13.9; a grid of about half the CUs was best for the
+    // N = 768 shapes (attn_out M = 32: 7.9 us against 10.1 / 12.4 us with
+    // twice / four times the workgroups).
+    if (m >= 2 && m <= kGemvRows && !perm && k % 32 == 0 && gs % 8 == 0 && aligned(a, 16) &&
+        aligned(wp, 4) && !getenv("TKV_INT4_GEMV_WAVE")) {
+        const int64_t ncb = (n + 15) / 16, nkb = k / 32;
+        int64_t splits = 1;
+        if (ncb <= kGemvSplitBlocks && 2 * ncb < (int64_t)c->num_cus) {
+            splits = ceil_div((int64_t)c->num_cus, 2 * ncb);
+            if (splits > nkb / kDecWaves) splits = nkb / kDecWaves;
+            if (splits < 1) splits = 1;
+        }
+        void* part = nullptr;
+        const int mb = m <= 16 ? 1 : 2;
+        if (splits > 1)
+            TKV_RC_TRY(ctx_workspace(c, 12, (size_t)(ncb * splits) * mb * 256 * sizeof(double), &part));
+        const unsigned grid = (unsigned)(ncb * splits);
+        if (mb == 1)
+            hipLaunchKernelGGL((k_gemv_int4_mfma<1>), dim3(grid), dim3(kDecWaves * 64), 0, c->stream, a,
+                               wp, scales, bias, y, (int)m, (int)n, (int)k, (int)gs, (int)splits,
+                               static_cast<double*>(part), c->gemv_arrivals);
+        else
+            hipLaunchKernelGGL((k_gemv_int4_mfma<2>), dim3(grid), dim3(kDecWaves * 64), 0, c->stream, a,
+                               wp, scales, bias, y, (int)m, (int)n, (int)k, (int)gs, (int)splits,
+                               static_cast<double*>(part), c->gemv_arrivals);
+        TKV_LAUNCH_CHECK();
+        return TKV_HIP_OK;
+    }
     if (m <= kGemvRows && (perm || aligned(a, 8))) {
         const unsigned g = (unsigned)((n + 3) / 4);
 #define TKV_GEMV(MM)                                                                              \

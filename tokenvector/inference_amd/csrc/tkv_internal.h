@@ -63,7 +63,7 @@ struct Ctx {
     int32_t* gemv_part = nullptr;
     unsigned* gemv_arrivals = nullptr;
     // grow-only workspaces
-    static constexpr int kSlots = 12;  // 10, 11: f16-decoded FP8 operands
+    static constexpr int kSlots = 13;  // 10, 11: f16-decoded FP8 operands; 12: INT4 split partials
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
     bool capturing = false;  // between capture_begin and capture_end
