@@ -660,8 +660,9 @@ constexpr int kGemvUnroll = 8;
 // SPLIT: workgroup b takes column block b % ncb and the K steps of split
 // b / ncb (of `splits`), so narrow N still spreads over the CUs.  Its INT32
 // partial sums go into part[block][1024] with device-scope atomic adds (exact
-// in any order); after a release fence it counts itself into
-// arrivals[block].  The workgroup that completes the count takes the sums
+// in any order); once those adds have completed (vmcnt(0); no cache
+// writeback, see below) it counts itself into arrivals[block] with another
+// device-scope atomic.  The workgroup that completes the count takes the sums
 // with an exchange that also clears them, clears the count, and runs the
 // epilogue: no workgroup ever waits for another, and part / arrivals are
 // zero again when the kernel ends (zeroed at context creation).
