@@ -408,9 +408,13 @@ def test_int8_dynamic_tensor(ctx, n, offset):
 
 
 # Activation-sized tensors around 8192 x 768 and beyond (float4 tails of 0 and
-# 4 elements past multiples of 256 * 512 * 4).
+# 4 elements past multiples of 256 * 512 * 4).  From 16 Mi elements on, the
+# single-pass kernel runs (one 768-thread workgroup per CU holding 32 float4
+# per thread on chip: 8192 x 3072 exactly fills 256 CUs, and 4 elements more
+# take the two-kernel path).
 RES_UNIT = 256 * 512 * 4
-RES_SIZES = [RES_UNIT * r + d for r in (4, 8, 16, 24, 32) for d in (0, 4)] + [2 ** 20]
+RES_SIZES = [RES_UNIT * r + d for r in (4, 8, 16, 24, 32) for d in (0, 4)] + [2 ** 20] + \
+    [8192 * 3072, 8192 * 3072 + 4, 2 ** 24 + 12]
 
 
 def _res_input(n, seed):
@@ -418,13 +422,19 @@ def _res_input(n, seed):
     return O.add_outliers(x, 0.001, 3, 4, 20.0)
 
 
-def _dyn_quant(ctx, x):
+def _dyn_quant(ctx, x, two_pass=False):
+    import os
     n = x.size
     dx = D.DeviceBuffer.from_host(ctx, x)
     dq = D.DeviceBuffer.empty(ctx, n, np.int8)
     p = D.params_buffer(ctx)
-    D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
-    ctx.synchronize()
+    if two_pass:
+        os.environ["TKV_QUANT_TWO_PASS"] = "1"
+    try:
+        D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
+        ctx.synchronize()
+    finally:
+        os.environ.pop("TKV_QUANT_TWO_PASS", None)
     return D.read_params(p), dq.download().astype(np.int32)
 
 
@@ -443,12 +453,14 @@ def test_int8_dynamic_tensor_activation_sizes(ctx, n):
 
 @pytest.mark.parametrize("case", ["nan_first", "nan_inside", "inf", "zeros", "tiny", "ties",
                                   "negative_extreme"])
-def test_int8_dynamic_tensor_specials(ctx, case):
+@pytest.mark.parametrize("n", [3 * RES_UNIT, 33 * RES_UNIT])
+def test_int8_dynamic_tensor_specials(ctx, case, n):
     """NaN (first element and inside), infinities, an all-zero tensor (the
     1e-8 scale floor), values below the floor, exact .5 ties of x * inv and a
-    negative extreme, at an activation size: bit-exact against the oracle."""
-    n = 3 * RES_UNIT
-    say(f"int8 dynamic tensor special={case}")
+    negative extreme, at an activation size for each path (two kernels, single
+    pass): bit-exact against the oracle, and the single-pass size also equal
+    to the two-kernel path's result."""
+    say(f"int8 dynamic tensor special={case} n={n}")
     x = _res_input(n, 77)
     if case == "nan_first":
         x[0] = np.nan
@@ -473,13 +485,19 @@ def test_int8_dynamic_tensor_specials(ctx, case):
     want_p = O.calibrate_minmax(x, 1)
     assert _same_f32([got_p.scale, got_p.min_val, got_p.max_val],
                      [want_p.scale, want_p.min_val, want_p.max_val])
-    assert np.array_equal(got_q, O.quantize_int8_symmetric(x, want_p.scale))
+    want_q = O.quantize_int8_symmetric(x, want_p.scale)
+    assert np.array_equal(got_q, want_q)
+    if n >= 2 ** 24:
+        two_p, two_q = _dyn_quant(ctx, x, two_pass=True)
+        assert _same_f32([two_p.scale, two_p.min_val, two_p.max_val],
+                         [got_p.scale, got_p.min_val, got_p.max_val])
+        assert np.array_equal(two_q, want_q)
 
 
 def test_int8_dynamic_tensor_repeated(ctx):
     """Back-to-back calls of different sizes on one context, no sync between
     them (the context's partials are reused by every call)."""
-    sizes = [RES_SIZES[0], RES_SIZES[5], 2 ** 20, RES_SIZES[2]] * 3
+    sizes = [RES_SIZES[0], 8192 * 3072, RES_SIZES[5], 2 ** 20, 2 ** 24 + 12, RES_SIZES[2]] * 2
     xs = {n: _res_input(n, n % 101) for n in set(sizes)}
     bufs = {n: (D.DeviceBuffer.from_host(ctx, xs[n]), D.DeviceBuffer.empty(ctx, n, np.int8))
             for n in xs}

@@ -143,7 +143,9 @@ static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t
 //   per-token scales   kStaticMaxRows f32
 //   calibration partials, per-call params
 //   split-K partial sums and arrival counts (zero at load; every call that
-//   can use them clears them first)
+//   can use them clears them first), the grid-barrier slots (zero at load;
+//   every launch advances each slot it uses by one generation, and the clear
+//   above resets all of them together)
 // Host code never names `scratch` directly as an address (on the host it is
 // a stand-in symbol): static_scratch() resolves each device's copy once with
 // hipGetSymbolAddress and every launch takes that pointer.
@@ -156,7 +158,8 @@ constexpr size_t kOffPartials = kAlign256(kOffScales + (size_t)kStaticMaxRows * 
 constexpr size_t kOffParams = kAlign256(kOffPartials + sizeof(RedPartial) * kMaxReduceBlocks);
 constexpr size_t kOffGemv = kAlign256(kOffParams + sizeof(tkv_hip_qparams_dev) * 64);
 constexpr size_t kOffArrivals = kOffGemv + (size_t)kGemvSplitBlocks * 1024 * sizeof(int32_t);
-constexpr size_t kOffScratchEnd = kAlign256(kOffArrivals + (size_t)kGemvSplitBlocks * sizeof(unsigned));
+constexpr size_t kOffGridSlots = kAlign256(kOffArrivals + (size_t)kGemvSplitBlocks * sizeof(unsigned));
+constexpr size_t kOffScratchEnd = kAlign256(kOffGridSlots + (size_t)kMaxGridSlots * 8);
 
 static __device__ __align__(256) uint8_t scratch[kOffScratchEnd];
 
@@ -321,6 +324,7 @@ int32_t tkv_hip_linear_forward_static(int64_t weight, const float* x, int64_t m,
     c.params = reinterpret_cast<tkv_hip_qparams_dev*>(base + kOffParams);
     c.gemv_part = reinterpret_cast<int32_t*>(base + kOffGemv);
     c.gemv_arrivals = reinterpret_cast<unsigned*>(base + kOffArrivals);
+    c.grid_slots = reinterpret_cast<unsigned long long*>(base + kOffGridSlots);
     c.ws[0] = base + kOffCodes;
     c.ws_bytes[0] = (size_t)TKV_HIP_STATIC_CODES_BYTES;
     c.ws[1] = base + kOffScales;

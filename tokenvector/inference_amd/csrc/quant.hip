@@ -22,6 +22,7 @@
 // products and reciprocals where the reference computes in f64, round half to
 // even, saturating clamp.  Compiled with -ffp-contract=off.
 #include <float.h>
+#include <cstdlib>
 
 #include "tkv_device.h"
 #include "tkv_internal.h"
@@ -287,12 +288,216 @@ int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qpar
     return TKV_HIP_OK;
 }
 
-// calibrate_minmax(x, 1) then quantize_int8_symmetric(x, q, scale) in two
-// kernels: per-CU partials, then the quantize kernel finalizing the scale in
-// every block.  *p receives the QuantParams.
+// ---------------------------------------------------------------------------
+// Single-pass per-tensor calibrate + quantize for large tensors
+// (calibrate_minmax(x, 1), then quantize_int8_symmetric: engine.tkv:13-36,
+// 216-226).  One workgroup per CU keeps its share of x on chip: kResRegs
+// float4 per thread in registers and kResLds in LDS (filled by direct-to-LDS
+// loads), up to 100.7 MB on 256 CUs.  The workgroups exchange their absmax
+// through a grid barrier and form the codes from the on-chip copy, so x
+// crosses HBM once.  The two-kernel path reads it twice: at 8192 x 3072 it
+// takes 17.9 + 20.7 us, this kernel ~26 us (timestamped probe: loads 15-16
+// us at 6.3-6.8 TB/s, barrier ~3 us, codes ~7 us).  For a 25 MB tensor the
+// two were equal, so the kernel is used from kResMinElems up.
+//
+// Symmetric calibration needs only max(|min|, |max|), the absmax of the
+// elements that are not NaN (fmaxf skips NaN, as the reference's strict
+// comparisons do); nan_first applies the reference's NaN-first-element rule,
+// so the QuantParams equal the two-kernel path's bit for bit.
+//
+// The barrier is a slot array in context memory: workgroup b owns the 64-bit
+// slot b = (generation << 32) | absmax bits.  It reads its own slot and
+// stores the next generation with its absmax (one relaxed agent-scope atomic
+// store).  Workgroup 0 polls every slot until all carry that generation,
+// takes the max of their absmaxes and stores it, with the generation, in the
+// result word (the last slot); the other workgroups poll only that word.
+// Every launch advances every slot by one, so the slots hold equal
+// generations whenever no launch is running, and a replayed graph needs
+// nothing from the host.  Data and flag are one atomic word, performed at
+// the device coherence point: no fences, no cache maintenance, and no shared
+// counter (256 agent-scope adds on one word serialize, ~10 us).  The grid is
+// one workgroup per CU (the LDS share leaves room for no second), so every
+// workgroup is resident once the CUs are free of earlier work.  The wait is
+// bounded all the same: a workgroup that gives up (kResSpin polls) takes the
+// absmax of the whole tensor itself, which gives the same scale (max is exact
+// in any order), so the result never depends on the barrier completing and
+// no workgroup can wait forever.
+// ---------------------------------------------------------------------------
+constexpr int kResBlock = 768;
+constexpr int kResRegs = 19;   // float4 per thread in registers (164 VGPRs in all)
+constexpr int kResLds = 13;    // float4 per thread in LDS (159,744 bytes)
+constexpr int kResSpin = 1 << 20;
+constexpr int64_t kResMinElems = 16ll << 20;  // 64 MB of f32
+
+__device__ __forceinline__ float absmax4(float m, const float4 v) {
+    return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+}
+
+// Block-wide max of a non-negative value, returned to every thread.
+__device__ __forceinline__ float block_max_res(float v, float* s) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max(v);
+    __syncthreads();  // s free from any earlier use
+    if (lane == 0) s[wave] = v;
+    __syncthreads();
+    float r = s[0];
+#pragma unroll
+    for (int w = 1; w < kResBlock / 64; w++) r = fmaxf(r, s[w]);
+    return r;
+}
+
+template <bool OUT_I32>
+__global__ __launch_bounds__(kResBlock, 3) void k_quant_i8_resident(
+    const float* __restrict__ x, int64_t n, tkv_hip_qparams_dev* __restrict__ p,
+    void* __restrict__ q, int recipe, unsigned long long* __restrict__ slots) {
+    __shared__ float4 s_x[kResLds * kResBlock];
+    __shared__ float s_red[kResBlock / 64];
+    __shared__ float s_all;
+    __shared__ int s_ok;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t n4 = n / 4;
+    const int64_t stride = (int64_t)gridDim.x * kResBlock;
+    const int64_t tid = (int64_t)blockIdx.x * kResBlock + threadIdx.x;
+    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
+    float4 v[kResRegs];
+#pragma unroll
+    for (int u = 0; u < kResRegs; u++) {
+        const int64_t i = tid + u * stride;
+        v[u] = i < n4 ? ld4<true>(x4 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    // the LDS share: lane l's 16 bytes land at s_x[u * kResBlock + 64 * wave + l]
+#pragma unroll
+    for (int u = 0; u < kResLds; u++) {
+        int64_t i = tid + (kResRegs + u) * stride;
+        if (i >= n4) i = n4 - 1;  // in bounds; the element is not used
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(x4 + i),
+            (__attribute__((address_space(3))) void*)(s_x + u * kResBlock + 64 * wave), 16, 0, 0);
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kResRegs; u++) am = absmax4(am, v[u]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS share has landed
+#pragma unroll
+    for (int u = 0; u < kResLds; u++)
+        if (tid + (kResRegs + u) * stride < n4) am = absmax4(am, s_x[u * kResBlock + threadIdx.x]);
+    am = block_max_res(am, s_red);
+    if (wave == 0) {
+        unsigned gen = 0;
+        if (lane == 0) {
+            unsigned long long* mine = slots + blockIdx.x;
+            gen = (unsigned)(__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) + 1u;
+            __hip_atomic_store(mine, ((unsigned long long)gen << 32) | __float_as_uint(am),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        gen = __shfl(gen, 0, 64);
+        unsigned long long* result = slots + (kMaxGridSlots - 1);
+        float g = 0.0f;
+        int ok = 0;
+        if (blockIdx.x == 0) {
+            // the leader gathers every slot, then publishes the max
+            for (int it = 0; it < kResSpin; it++) {
+                int ready = 1;
+                float gg = 0.0f;
+                for (int b = lane; b < (int)gridDim.x; b += 64) {
+                    const unsigned long long sv =
+                        __hip_atomic_load(slots + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ready &= (unsigned)(sv >> 32) == gen;
+                    gg = fmaxf(gg, __uint_as_float((unsigned)sv));
+                }
+                if (__all(ready)) {
+                    g = wave_max(gg);
+                    ok = 1;
+                    break;
+                }
+            }
+            if (ok && lane == 0)
+                __hip_atomic_store(result, ((unsigned long long)gen << 32) | __float_as_uint(g),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (lane == 0) {
+            for (int it = 0; it < kResSpin; it++) {
+                const unsigned long long rv =
+                    __hip_atomic_load(result, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((unsigned)(rv >> 32) == gen) {
+                    g = __uint_as_float((unsigned)rv);
+                    ok = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        if (lane == 0) {
+            s_all = g;
+            s_ok = ok;
+        }
+    }
+    __syncthreads();
+    float g = s_all;
+    if (!s_ok) {
+        // barrier gave up: the absmax of the whole tensor, read by this workgroup
+        g = 0.0f;
+        for (int64_t i = threadIdx.x; i < n4; i += kResBlock) g = absmax4(g, ld4<true>(x4 + i));
+        g = block_max_res(g, s_red);
+    }
+    double dmn = 0.0, dmx = (double)g;
+    nan_first(x, dmn, dmx);
+    tkv_hip_qparams_dev prm;
+    finalize_minmax(dmn, dmx, MM_SYMMETRIC, recipe, &prm);
+    const double inv = prm.inv;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *p = prm;
+#pragma unroll
+    for (int u = 0; u < kResRegs; u++) {
+        const int64_t i = tid + u * stride;
+        if (i < n4)
+            store4<OUT_I32>(q, i, rne_clamp((double)v[u].x * inv, -127.0, 127.0),
+                            rne_clamp((double)v[u].y * inv, -127.0, 127.0),
+                            rne_clamp((double)v[u].z * inv, -127.0, 127.0),
+                            rne_clamp((double)v[u].w * inv, -127.0, 127.0));
+    }
+#pragma unroll
+    for (int u = 0; u < kResLds; u++) {
+        const int64_t i = tid + (kResRegs + u) * stride;
+        if (i < n4) {
+            const float4 w = s_x[u * kResBlock + threadIdx.x];
+            store4<OUT_I32>(q, i, rne_clamp((double)w.x * inv, -127.0, 127.0),
+                            rne_clamp((double)w.y * inv, -127.0, 127.0),
+                            rne_clamp((double)w.z * inv, -127.0, 127.0),
+                            rne_clamp((double)w.w * inv, -127.0, 127.0));
+        }
+    }
+}
+
+// TKV_HIP_UNSUPPORTED when the tensor is outside the single-pass kernel's
+// range (size, alignment, a tail of fewer than 4 elements) or the context
+// has no barrier slots.
+static int launch_quant_i8_resident(Ctx* c, const float* x, int64_t n, int recipe,
+                                    tkv_hip_qparams_dev* p, void* q, bool out_i32) {
+    const int64_t g = c->num_cus;
+    if (!c->grid_slots || g > kMaxGridSlots - 1 || n < kResMinElems || n % 4 != 0 ||
+        !aligned(x, 16) || !aligned(q, out_i32 ? 16 : 4) ||
+        n / 4 > g * kResBlock * (kResRegs + kResLds))
+        return TKV_HIP_UNSUPPORTED;
+    if (out_i32)
+        hipLaunchKernelGGL((k_quant_i8_resident<true>), dim3((unsigned)g), dim3(kResBlock), 0,
+                           c->stream, x, n, p, q, recipe, c->grid_slots);
+    else
+        hipLaunchKernelGGL((k_quant_i8_resident<false>), dim3((unsigned)g), dim3(kResBlock), 0,
+                           c->stream, x, n, p, q, recipe, c->grid_slots);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+// calibrate_minmax(x, 1) then quantize_int8_symmetric(x, q, scale): the
+// single-pass kernel for large tensors that fit it, else two kernels
+// (per-CU partials, then the quantize kernel finalizing the scale in every
+// block).  *p receives the QuantParams.
 int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
                             tkv_hip_qparams_dev* p, void* q, bool out_i32) {
     if (n <= 0) return launch_minmax_tensor(c, x, n, MM_SYMMETRIC, recipe, p);
+    if (!getenv("TKV_QUANT_TWO_PASS")) {
+        const int rc = launch_quant_i8_resident(c, x, n, recipe, p, q, out_i32);
+        if (rc != TKV_HIP_UNSUPPORTED) return rc;
+    }
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
     launch_quant_kernel<true>(c, x, n, p, q, out_i32, (int)nparts, recipe);

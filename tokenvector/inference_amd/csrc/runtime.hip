@@ -71,7 +71,8 @@ int ctx_create(int device, Ctx** out) {
     c->stream = c->own_stream;
     const size_t gemv_bytes = (size_t)kGemvSplitBlocks * 1024 * sizeof(int32_t);
     size_t red_bytes = sizeof(RedPartial) * kMaxReduceBlocks + 256 + sizeof(tkv_hip_qparams_dev) * 64 +
-                       256 + gemv_bytes + (size_t)kGemvSplitBlocks * sizeof(unsigned);
+                       256 + gemv_bytes + (size_t)kGemvSplitBlocks * sizeof(unsigned) + 256 +
+                       (size_t)kMaxGridSlots * 8;
     void* red = nullptr;
     e = hipMalloc(&red, red_bytes);
     if (e != hipSuccess) {
@@ -84,6 +85,10 @@ int ctx_create(int device, Ctx** out) {
                                                        sizeof(RedPartial) * kMaxReduceBlocks + 256);
     c->gemv_part = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(c->params + 64) + 256);
     c->gemv_arrivals = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(c->gemv_part) + gemv_bytes);
+    {   // next 256-byte boundary past the arrival counts
+        const uintptr_t end = reinterpret_cast<uintptr_t>(c->gemv_arrivals + kGemvSplitBlocks);
+        c->grid_slots = reinterpret_cast<unsigned long long*>((end + 255) & ~uintptr_t(255));
+    }
     // One-time zeroing at creation, so params read before any calibration
     // are defined (never inside a caller's stream capture).
     e = hipMemset(red, 0, red_bytes);

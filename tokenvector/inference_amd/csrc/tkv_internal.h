@@ -41,6 +41,8 @@ int fail_hip(hipError_t e, const char* what, const char* file, int line);
 constexpr int kMaxReduceBlocks = 2048;
 // Column blocks (32 columns each) of the split-K skinny GEMM's partial sums.
 constexpr int kGemvSplitBlocks = 128;
+// Workgroups of a grid-barrier kernel (one per CU) plus its result word.
+constexpr int kMaxGridSlots = 1024;
 
 struct RedPartial {
     float mn;
@@ -62,6 +64,11 @@ struct Ctx {
     // by the kernel that uses them.
     int32_t* gemv_part = nullptr;
     unsigned* gemv_arrivals = nullptr;
+    // Grid-barrier slots of the single-pass calibrate + quantize kernel: one
+    // 64-bit word per workgroup and the result word (the last of
+    // kMaxGridSlots), zero at creation; every launch advances each slot it
+    // uses, and the result word, by one generation.
+    unsigned long long* grid_slots = nullptr;
     // grow-only workspaces
     static constexpr int kSlots = 13;  // 10, 11: f16-decoded FP8 operands; 12: INT4 split partials
     void* ws[kSlots] = {};
