@@ -642,7 +642,7 @@ __device__ __forceinline__ void quant_row(const float4 (&v)[C4], int64_t r, int6
     double am = (double)wave_max(al);
     if (am < 0.00000001) am = 0.00000001;
     const double sc = am / 127.0;
-    scales_out[r] = (float)sc;
+    if (lane == 0) scales_out[r] = (float)sc;
     const double inv = 1.0 / sc;
     const int64_t base4 = r * cols4;
 #pragma unroll
@@ -696,6 +696,8 @@ static bool launch_rows_dynamic(Ctx* c, const float* x, int64_t rows, int64_t co
                                 float* scales_out) {
     const int64_t per_lane = ceil_div(cols / 4, 64);
     int64_t blocks = ceil_div(rows, kBlock / 64);
+    // 2 to 24 blocks per CU all measured 42.2-44.5 us at 65536 x 768 (one
+    // box, three interleaved rounds): the grid is not what limits it
     const int64_t cap = (int64_t)c->num_cus * 8;
     if (blocks > cap) blocks = cap;
     const dim3 grid((unsigned)blocks), block(kBlock);
