@@ -1065,6 +1065,50 @@ def test_graph_capture_replays(hip):
     ctx.close()
 
 
+def test_graph_replays_single_pass_quantize(hip):
+    """The single-pass calibrate + quantize (a 100 MB activation: one
+    workgroup per CU and a grid barrier whose slots advance by one generation
+    per launch) inside a captured graph: three replays over new inputs, with
+    eager single-pass calls of another size between them, each equal to the
+    eager result bit for bit."""
+    say("graph replays of the single-pass quantize")
+    ctx = D.Context(0)
+    n = 8192 * 3072
+    dx = D.DeviceBuffer.empty(ctx, n, np.float32)
+    dq = D.DeviceBuffer.empty(ctx, n, np.int8)
+    p = D.params_buffer(ctx)
+    other = _res_input(2 ** 24 + 12, 91)
+    dox = D.DeviceBuffer.from_host(ctx, other)
+    doq = D.DeviceBuffer.empty(ctx, other.size, np.int8)
+    dop = D.params_buffer(ctx)
+    inputs = [_res_input(n, 80 + i) for i in range(3)]
+    want = []
+    for x in inputs:
+        dx.upload(x)
+        D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
+        ctx.synchronize()
+        want.append((D.read_params(p).scale, dq.download()))
+    wp = O.calibrate_minmax(inputs[0], 1)
+    assert _same_f32([want[0][0]], [wp.scale])
+    assert np.array_equal(want[0][1].astype(np.int32), O.quantize_int8_symmetric(inputs[0], wp.scale))
+    with D.Graph(ctx) as g:
+        D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
+    for x, (ws, wq) in zip(inputs, want):
+        dx.upload(x)
+        D.quantize_int8_dynamic_tensor(ctx, dox, other.size, doq, dop)
+        D.memset(ctx, dq, 0, n)
+        ctx.synchronize()
+        g.launch()
+        ctx.synchronize()
+        assert _same_f32([D.read_params(p).scale], [ws])
+        assert np.array_equal(dq.download(), wq)
+    g.close()
+    op = O.calibrate_minmax(other, 1)
+    assert _same_f32([D.read_params(dop).scale], [op.scale])
+    assert np.array_equal(doq.download().astype(np.int32), O.quantize_int8_symmetric(other, op.scale))
+    ctx.close()
+
+
 def test_graph_survives_workspace_growth(hip):
     """A graph captured over a call that repacks its operands into workspace
     still replays correctly after a larger eager call has grown those
