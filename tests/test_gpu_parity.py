@@ -106,11 +106,33 @@ def test_calibrate_kl(hip, n):
     x = _x(n, 41 + n % 97, 1.0)
     if n > 100:
         x = O.add_outliers(x, 0.001, 3, 4, 20.0)
-    for bins, target in [(2048, 128), (512, 32), (64, 8), (4096, 4000)]:
+    for bins, target in [(2048, 128), (512, 32), (64, 8), (4096, 4000), (4096, 4096), (100, 7)]:
         g, o = Q.calibrate_kl(x, bins, target), O.calibrate_kl(x, bins, target)
         assert _same_qp(g, o), (bins, target, g, o)
     z = np.zeros(max(n, 2), np.float32)
     assert _same_qp(Q.calibrate_kl(z), O.calibrate_kl(z))
+
+
+@pytest.mark.parametrize("bins, target", [(2048, 128), (100, 7), (4096, 16)])
+def test_calibrate_kl_bin_edges(hip, bins, target):
+    """Elements on the histogram's bin edges: f32(k * bw) and its two f32
+    neighbours for every k, where |x| / bw rounds to k or just below it.  The
+    kernel's two-sided f32 estimate cannot place these, so every one of them
+    takes the f64-division path (per element, inside otherwise fast waves);
+    NaN, inf and zeros go the same way.  Compared with the oracle's loop."""
+    say(f"calibrate_kl bin edges bins={bins}")
+    am = np.float32(3.7)
+    bw = float(am) / bins
+    k = np.arange(bins + 1, dtype=np.float64)
+    e = (k * bw).astype(np.float32)
+    x = np.concatenate([e, np.nextafter(e, np.float32(np.inf)), np.nextafter(e, np.float32(0))])
+    x = np.minimum(x, am).astype(np.float32)
+    rng = np.random.default_rng(bins)
+    x = np.concatenate([x, -x, rng.uniform(-3.7, 3.7, 200000).astype(np.float32)])
+    rng.shuffle(x)
+    x = np.concatenate([x, np.float32([np.nan, 0.0, -0.0])]).astype(np.float32)
+    g, o = Q.calibrate_kl(x, bins, target), O.calibrate_kl(x, bins, target)
+    assert _same_qp(g, o), (bins, target, g, o)
 
 
 @pytest.mark.parametrize("n", CAL_SIZES)

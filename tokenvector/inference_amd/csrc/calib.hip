@@ -4,17 +4,23 @@
 //   calibrate_kl          max|x| from the min / max partials, a num_bins
 //                         histogram of |x| (LDS per block, 64-bit global
 //                         atomics), then the threshold search: one candidate
-//                         threshold per wave, its kl sum added in the
-//                         reference's sequential order.
+//                         threshold per block, its kl sum added in the
+//                         reference's sequential order; the last block to
+//                         finish picks the threshold.
 //   calibrate_percentile  the k-th smallest |x| by radix select on its f32 bit
 //                         pattern (non-negative floats order as integers):
-//                         three histogram passes of 11 / 11 / 10 bits, each
-//                         followed by a one-block digit pick; the asymmetric
-//                         form clips the min / max partials.
+//                         three histogram passes of 11 / 11 / 10 bits, the
+//                         last block of each picking the digit; the
+//                         asymmetric form clips the min / max partials.
 //   calibrate_mse         passes over x of 16 candidate thresholds each,
 //                         summing squared quantization errors per block
 //                         (f64), one block per candidate reducing those
-//                         sums, then the reference's first-minimum pick.
+//                         sums, the last of them making the reference's
+//                         first-minimum pick.
+//
+// The histogram and the "last block" arrival counts are the context's
+// calibration scratch (cal_hist, cal_arrivals): zero at creation, and each
+// call's last block clears what it used.
 //
 // Numerics follow the reference's f64 locals.  Sums whose order the
 // reference fixes are reproduced in that order where they decide the result
@@ -22,6 +28,7 @@
 // (a different order than the reference's single loop), which can only
 // matter for candidates within rounding of each other.
 #include <float.h>
+#include <limits.h>
 
 #include <utility>
 
@@ -58,32 +65,6 @@ __device__ __forceinline__ void write_sym(double thr, tkv_hip_qparams_dev* out) 
     *out = p;
 }
 
-// Shared first step: reduce the min / max partials, keep max|x| and bw.
-__global__ __launch_bounds__(kBlock) void k_cal_prep(const float* __restrict__ x, int nparts,
-                                                     int track_zero,
-                                                     const RedPartial* __restrict__ partials,
-                                                     int64_t num_bins, CalibState* st,
-                                                     unsigned long long* __restrict__ hist,
-                                                     int64_t hist_len, int64_t rank) {
-    double dmn, dmx;
-    reduce_partials(x, nparts, track_zero, partials, dmn, dmx);
-    for (int64_t i = threadIdx.x; i < hist_len; i += kBlock) hist[i] = 0;
-    if (threadIdx.x == 0) {
-        // max|x| from 0 (engine.tkv:45-49, 170-174) skips NaN; all NaN gives
-        // 0 (the partials then hold min +inf > max -inf).  mn / mx feed the
-        // calibrate_minmax fallback, seeded by x[0].
-        const double am = dmn <= dmx ? fmax(fabs(dmn), fabs(dmx)) : 0.0;
-        nan_first(x, dmn, dmx);
-        st->am = am;
-        st->bw = num_bins > 0 ? am / (double)num_bins : 0.0;
-        st->mn = dmn;
-        st->mx = dmx;
-        st->prefix = 0;
-        st->pad = 0;
-        st->rank = rank;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // calibrate_kl (engine.tkv:42-123)
 // ---------------------------------------------------------------------------
@@ -103,213 +84,328 @@ __device__ __forceinline__ int kl_bin(float xv, double bw, double inv_bw, int nu
     return (int)q;
 }
 
-// Each wave counts into its own LDS histogram (num_bins x 4 waves), merged
-// into the 64-bit global one at the end.
+constexpr int kKlVec = 4;     // float4 loads per lane per trip, all issued before any count
+constexpr int kKlCopies = 2;  // LDS histogram copies per block (copy = lane parity)
+
+// The |x| histogram: kKlCopies LDS histograms per block, pitch num_bins + 1
+// (a bin's copies in different banks), merged into the 64-bit global one at
+// the end.  Each element's bin comes from two f32 quotients that bracket
+// |x| / bw: |x| * fl(inv_bw (1 - 2^-22)) and |x| * fl(inv_bw (1 + 2^-22)) lie
+// below and above the exact quotient by more than 2^-23 of it (two f32
+// roundings of 2^-24 at most), so equal truncations below num_bins are the
+// bin of the exact quotient and of its f64 rounding alike.  An element whose
+// truncations differ (a bin edge within ~2^-22 of it, the clamp at num_bins,
+// NaN or inf) takes kl_bin instead, each on its own branch, which a wave
+// skips unless one of its lanes needs it; so does every element when 1 / bw
+// is outside the f32 normal range.
+//   Every block reduces the min / max partials itself for max|x| and bw (a
+// few KB from L2); block 0 also records them, with the first-element NaN rule
+// for the calibrate_minmax fallback, in st.
 __global__ __launch_bounds__(kCalBlock) void k_kl_hist(const float* __restrict__ x, int64_t n,
-                                                       int vec, int num_bins,
-                                                       const CalibState* __restrict__ st,
+                                                       int vec, int num_bins, int nparts,
+                                                       const RedPartial* __restrict__ partials,
+                                                       CalibState* __restrict__ st,
                                                        unsigned long long* __restrict__ hist) {
-    extern __shared__ unsigned int s_hist[];  // [kCalBlock / 64][num_bins]
-    for (int i = threadIdx.x; i < num_bins * (kCalBlock / 64); i += kCalBlock) s_hist[i] = 0;
-    __syncthreads();
-    unsigned int* wh = s_hist + (threadIdx.x >> 6) * num_bins;
-    const double bw = st->bw, inv_bw = 1.0 / bw;
+    extern __shared__ unsigned int s_hist[];  // [kKlCopies][num_bins + 1]
+    const int pitch = num_bins + 1;
+    for (int i = threadIdx.x; i < pitch * kKlCopies; i += kCalBlock) s_hist[i] = 0;
+    double dmn, dmx;
+    reduce_partials(x, nparts, 0, partials, dmn, dmx);  // its barrier also orders the clear
+    // max|x| from 0 (engine.tkv:45-49, 170-174) skips NaN; all NaN gives 0
+    // (the partials then hold min +inf > max -inf)
+    const double am = dmn <= dmx ? fmax(fabs(dmn), fabs(dmx)) : 0.0;
+    const double bw = am / (double)num_bins, inv_bw = 1.0 / bw;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        nan_first(x, dmn, dmx);
+        st->am = am;
+        st->bw = bw;
+        st->mn = dmn;
+        st->mx = dmx;
+    }
+    unsigned int* h = s_hist + (threadIdx.x % kKlCopies) * pitch;
+    const bool fast = inv_bw >= 0x1p-125 && inv_bw <= 0x1p+125;
+    const float inv_lo = (float)(inv_bw * (1.0 - 0x1p-22));
+    const float inv_hi = (float)(inv_bw * (1.0 + 0x1p-22));
+    const float fbins = (float)num_bins;
     const int64_t stride = (int64_t)gridDim.x * kCalBlock;
     const int64_t tid = (int64_t)blockIdx.x * kCalBlock + threadIdx.x;
     const int64_t n4 = vec ? n / 4 : 0;
     const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
     int64_t i = tid;
-    for (; i + stride < n4; i += 2 * stride) {
-        const float4 u = x4[i], v = x4[i + stride];
-        atomicAdd(&wh[kl_bin(u.x, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(u.y, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(u.z, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(u.w, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(v.x, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(v.y, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(v.z, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(v.w, bw, inv_bw, num_bins)], 1u);
+    for (; i + (kKlVec - 1) * stride < n4; i += kKlVec * stride) {
+        float v[kKlVec * 4];
+#pragma unroll
+        for (int k = 0; k < kKlVec; k++) {
+            const float4 u = x4[i + k * stride];
+            v[4 * k] = u.x;
+            v[4 * k + 1] = u.y;
+            v[4 * k + 2] = u.z;
+            v[4 * k + 3] = u.w;
+        }
+        int b[kKlVec * 4];
+        unsigned slow = fast ? 0u : ~0u;
+#pragma unroll
+        for (int e = 0; e < kKlVec * 4; e++) {
+            const float a = fabsf(v[e]);
+            const float tl = __builtin_truncf(a * inv_lo), qh = a * inv_hi;
+            const bool ok = tl == __builtin_truncf(qh) && qh < fbins;
+            slow |= ok ? 0u : 1u << e;
+            b[e] = ok ? (int)tl : 0;
+        }
+        if (slow) {
+#pragma unroll
+            for (int e = 0; e < kKlVec * 4; e++)
+                if (slow & (1u << e)) b[e] = kl_bin(v[e], bw, inv_bw, num_bins);
+        }
+#pragma unroll
+        for (int e = 0; e < kKlVec * 4; e++) atomicAdd(&h[b[e]], 1u);
     }
     for (; i < n4; i += stride) {
         const float4 u = x4[i];
-        atomicAdd(&wh[kl_bin(u.x, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(u.y, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(u.z, bw, inv_bw, num_bins)], 1u);
-        atomicAdd(&wh[kl_bin(u.w, bw, inv_bw, num_bins)], 1u);
+        atomicAdd(&h[kl_bin(u.x, bw, inv_bw, num_bins)], 1u);
+        atomicAdd(&h[kl_bin(u.y, bw, inv_bw, num_bins)], 1u);
+        atomicAdd(&h[kl_bin(u.z, bw, inv_bw, num_bins)], 1u);
+        atomicAdd(&h[kl_bin(u.w, bw, inv_bw, num_bins)], 1u);
     }
     for (int64_t j = n4 * 4 + tid; j < n; j += stride)
-        atomicAdd(&wh[kl_bin(x[j], bw, inv_bw, num_bins)], 1u);
+        atomicAdd(&h[kl_bin(x[j], bw, inv_bw, num_bins)], 1u);
     __syncthreads();
     for (int b = threadIdx.x; b < num_bins; b += kCalBlock) {
         unsigned int c = 0;
-        for (int w = 0; w < kCalBlock / 64; w++) c += s_hist[w * num_bins + b];
+#pragma unroll
+        for (int w = 0; w < kKlCopies; w++) c += s_hist[w * pitch + b];
         if (c) atomicAdd(&hist[b], (unsigned long long)c);
     }
 }
 
-// Candidate th = target + 16 * blockIdx.x, one wave each.  Every candidate's
+static_assert(kMaxKlBins <= kCalHistBins && kRadixBins <= kCalHistBins,
+              "the context's calibration histogram holds every histogram");
+constexpr int kKlCandBlock = 256;
+constexpr int kKlHistPerThread = (int)(kMaxKlBins / kKlCandBlock);
+static_assert(kKlCandBlock == kBlock, "block_first_min runs on kBlock threads");
+
+// kl of candidate threshold th (returned in thread 0).  Every candidate's
 // total s equals the histogram total (the tail is merged into p[th - 1]), so
 // p[i] = hist[i] / s for i < th - 1 and p[th - 1] = (tail sum) / s, as the
 // reference's own arithmetic gives; the total and the tail are integer sums,
-// exact in f64 in any order.  Lanes form the block shares (each block's mass
-// summed in index order) and the kl terms in parallel; lane 0 adds the terms
-// in index order, so kl is the reference's sequential sum bit for bit (terms
-// the reference skips are +0.0).
-__global__ __launch_bounds__(64) void k_kl_candidate(int num_bins, int target_bins,
-                                                     const unsigned long long* __restrict__ hist,
-                                                     double* __restrict__ kl_out) {
-    extern __shared__ double s_dyn[];  // [num_bins] p, then [target_bins] shares
+// exact in f64 in any order.  Threads form the block shares (each block's
+// mass summed in index order) and the kl terms in parallel, the terms
+// overwriting p in LDS; thread 0 then adds them in index order, so kl is the
+// reference's sequential sum bit for bit (terms the reference skips, and the
+// padding to a multiple of 64, are +0.0, which leaves a sum that started at
+// +0.0 unchanged).
+//   s_dyn: [num_bins rounded up to 64] p, then [max(target_bins, 8)] shares;
+// the wave totals sit in the shares' place until those are formed, so the
+// largest call (4096 bins and targets) stays within 64 KB of LDS.
+__device__ double candidate_kl(int num_bins, int target_bins, int th,
+                               const unsigned long long* __restrict__ hist, double* s_dyn) {
+    const int tid = threadIdx.x;
+    const int nb64 = (num_bins + 63) & ~63;
     double* s_p = s_dyn;
-    double* s_share = s_dyn + num_bins;
-    __shared__ double s_t[64];
-    const int lane = threadIdx.x;
-    const int th = target_bins + 16 * (int)blockIdx.x;
+    double* s_share = s_dyn + nb64;
+    unsigned long long(*s_red)[kKlCandBlock / 64] =
+        reinterpret_cast<unsigned long long(*)[kKlCandBlock / 64]>(s_share);
+    unsigned long long h[kKlHistPerThread];
+#pragma unroll
+    for (int k = 0; k < kKlHistPerThread; k++) {
+        const int i = tid + k * kKlCandBlock;
+        h[k] = i < num_bins ? hist[i] : 0ull;
+    }
     unsigned long long tot = 0, tail = 0;
-    for (int i = lane; i < num_bins; i += 64) {
-        const unsigned long long h = hist[i];
-        tot += h;
-        if (i >= th - 1) tail += h;
+#pragma unroll
+    for (int k = 0; k < kKlHistPerThread; k++) {
+        tot += h[k];
+        tail += tid + k * kKlCandBlock >= th - 1 ? h[k] : 0ull;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         tot += __shfl_xor(tot, o, 64);
         tail += __shfl_xor(tail, o, 64);
     }
+    if ((tid & 63) == 0) {
+        s_red[0][tid >> 6] = tot;
+        s_red[1][tid >> 6] = tail;
+    }
+    __syncthreads();
+    tot = 0;
+    tail = 0;
+#pragma unroll
+    for (int w = 0; w < kKlCandBlock / 64; w++) {
+        tot += s_red[0][w];
+        tail += s_red[1][w];
+    }
     const double total = (double)tot;
-    for (int i = lane; i < th - 1; i += 64) s_p[i] = (double)hist[i] / total;
-    if (lane == 0) s_p[th - 1] = (double)tail / total;
+#pragma unroll
+    for (int k = 0; k < kKlHistPerThread; k++) {
+        const int i = tid + k * kKlCandBlock;
+        if (i < th - 1) s_p[i] = (double)h[k] / total;
+    }
+    if (tid == 0) s_p[th - 1] = (double)tail / total;
     __syncthreads();
     const int per = th / target_bins;
-    for (int b = lane; b < target_bins; b += 64) {
+    for (int b = tid; b < target_bins; b += kKlCandBlock) {
         const int start = b * per;
         const int end = (b == target_bins - 1) ? th : start + per;
         double mass = 0.0;
-        for (int i = start; i < end; i++) mass = mass + s_p[i];
+        int i = start;
+        for (; i + 8 <= end; i += 8) {
+            double v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = s_p[i + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) mass = mass + v[k];
+        }
+        for (; i < end; i++) mass = mass + s_p[i];
         int span = end - start;
         if (span < 1) span = 1;
         s_share[b] = mass / (double)span;
     }
     __syncthreads();
-    double kl = 0.0;
-    for (int i0 = 0; i0 < th; i0 += 64) {
-        const int i = i0 + lane;
+    const int th64 = (th + 63) & ~63;
+    for (int i = tid; i < th64; i += kKlCandBlock) {
         double t = 0.0;
         if (i < th) {
             const int b = i / per < target_bins - 1 ? i / per : target_bins - 1;
             const double pi = s_p[i], sh = s_share[b];
             if (pi > 0.000000000001 && sh > 0.000000000001) t = pi * log(pi / sh);
         }
-        s_t[lane] = t;
-        __syncthreads();
-        if (lane == 0) {
-            const int cnt = th - i0 < 64 ? th - i0 : 64;
-            for (int l = 0; l < cnt; l++) kl = kl + s_t[l];
-        }
-        __syncthreads();
+        s_p[i] = t;
     }
-    if (lane == 0) kl_out[blockIdx.x] = kl;
+    __syncthreads();
+    double kl = 0.0;
+    if (tid == 0) {
+        const double2* t2 = reinterpret_cast<const double2*>(s_p);
+        for (int j = 0; j < th64 / 2; j += 16) {
+            double2 v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = t2[j + k];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                kl = kl + v[k].x;
+                kl = kl + v[k].y;
+            }
+        }
+    }
+    return kl;
 }
 
-// The first strict minimum over th ascending (the reference's loop), then the
-// parameters: thr = best_bin * bw, or calibrate_minmax below max|x| 1e-8.
-__global__ void k_kl_select(int ncand, int num_bins, int target_bins,
-                            const double* __restrict__ kl, const CalibState* __restrict__ st,
-                            tkv_hip_qparams_dev* __restrict__ out) {
-    double best = 1e45;
-    int best_bin = num_bins;
-    for (int c = 0; c < ncand; c++)
-        if (kl[c] < best) {
-            best = kl[c];
-            best_bin = target_bins + 16 * c;
-        }
-    if (st->am < 0.00000001)
-        finalize_minmax(st->mn, st->mx, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
-    else
-        write_sym((double)best_bin * st->bw, out);
+// Candidate th = target + 16 * blockIdx.x, one block each.  The block that
+// arrives last (arrive_last) makes the selection, writes the parameters and
+// clears the histogram for the next call; with no candidate (num_bins <
+// target_bins) a single block only does that.
+__global__ __launch_bounds__(kKlCandBlock) void k_kl_candidate(
+    int num_bins, int target_bins, int ncand, unsigned long long* __restrict__ hist,
+    double* __restrict__ kl_out, const CalibState* __restrict__ st, unsigned* __restrict__ arrivals,
+    tkv_hip_qparams_dev* __restrict__ out) {
+    extern __shared__ double s_dyn[];
+    if (ncand > 0) {
+        const double kl =
+            candidate_kl(num_bins, target_bins, target_bins + 16 * (int)blockIdx.x, hist, s_dyn);
+        if (threadIdx.x == 0)
+            __hip_atomic_store(kl_out + blockIdx.x, kl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!arrive_last(arrivals, gridDim.x)) return;
+    // the first strict minimum over th ascending (the reference's loop), then
+    // thr = best_bin * bw, or calibrate_minmax below max|x| 1e-8
+    const int pick = block_first_min(kl_out, ncand);
+    for (int i = threadIdx.x; i < num_bins; i += kKlCandBlock) hist[i] = 0;
+    if (threadIdx.x == 0) {
+        const int best_bin = pick < 0 ? num_bins : target_bins + 16 * pick;
+        if (st->am < 0.00000001)
+            finalize_minmax(st->mn, st->mx, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
+        else
+            write_sym((double)best_bin * st->bw, out);
+    }
+    arrive_clear(arrivals);
 }
 
 // ---------------------------------------------------------------------------
 // calibrate_percentile (engine.tkv:126-162)
 // ---------------------------------------------------------------------------
 
-// Histogram of digit (bits(|x|) >> shift) & (bins - 1) over the elements
-// whose bits above the digit equal the prefix found so far; per-wave LDS
-// histograms, 16-byte loads.
-__device__ __forceinline__ void radix_count(unsigned int* wh, float xv, uint32_t prefix,
+// One radix pass: the digit (bits(|x|) >> shift) & (2^bits - 1) counted over
+// the elements whose higher bits equal the prefix found so far (one LDS
+// histogram per block, kKlVec float4 per lane per trip), merged into the
+// global histogram.  The block that arrives last (arrive_last) finds the
+// digit holding the element of the wanted rank (block prefix sum over the
+// 2048 digit counts, 8 per thread), records prefix and rank in st, clears
+// the histogram, and after the last pass writes the parameters.
+__device__ __forceinline__ void radix_count(unsigned int* h, float xv, uint32_t prefix,
                                             uint32_t hi_mask, int shift, uint32_t dmask) {
     const uint32_t v = __float_as_uint(xv) & 0x7fffffffu;
-    if (((v ^ prefix) & hi_mask) == 0) atomicAdd(&wh[(v >> shift) & dmask], 1u);
+    if (((v ^ prefix) & hi_mask) == 0) atomicAdd(&h[(v >> shift) & dmask], 1u);
 }
 
-__global__ __launch_bounds__(kCalBlock) void k_radix_hist(const float* __restrict__ x, int64_t n,
-                                                          int vec, int shift, int bits,
-                                                          const CalibState* __restrict__ st,
-                                                          unsigned long long* __restrict__ hist) {
-    __shared__ unsigned int s_hist[kCalBlock / 64][kRadixBins];
-    for (int i = threadIdx.x; i < kRadixBins * (kCalBlock / 64); i += kCalBlock)
-        (&s_hist[0][0])[i] = 0;
+__global__ __launch_bounds__(kCalBlock) void k_radix_pass(
+    const float* __restrict__ x, int64_t n, int vec, int shift, int bits, int first, int last,
+    int64_t rank0, int symmetric, int nparts, const RedPartial* __restrict__ partials,
+    CalibState* __restrict__ st, unsigned long long* __restrict__ hist,
+    unsigned* __restrict__ arrivals, tkv_hip_qparams_dev* __restrict__ out) {
+    __shared__ unsigned int s_h[kRadixBins];
+    for (int i = threadIdx.x; i < kRadixBins; i += kCalBlock) s_h[i] = 0;
     __syncthreads();
-    unsigned int* wh = s_hist[threadIdx.x >> 6];
     const uint32_t hi_mask = (shift + bits >= 32) ? 0u : ~((1u << (shift + bits)) - 1u);
-    const uint32_t prefix = st->prefix;
+    const uint32_t prefix = first ? 0u : st->prefix;
     const uint32_t dmask = (1u << bits) - 1u;
     const int64_t stride = (int64_t)gridDim.x * kCalBlock;
     const int64_t tid = (int64_t)blockIdx.x * kCalBlock + threadIdx.x;
     const int64_t n4 = vec ? n / 4 : 0;
     const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
     int64_t i = tid;
-    for (; i + stride < n4; i += 2 * stride) {
-        const float4 u = x4[i], v = x4[i + stride];
-        radix_count(wh, u.x, prefix, hi_mask, shift, dmask);
-        radix_count(wh, u.y, prefix, hi_mask, shift, dmask);
-        radix_count(wh, u.z, prefix, hi_mask, shift, dmask);
-        radix_count(wh, u.w, prefix, hi_mask, shift, dmask);
-        radix_count(wh, v.x, prefix, hi_mask, shift, dmask);
-        radix_count(wh, v.y, prefix, hi_mask, shift, dmask);
-        radix_count(wh, v.z, prefix, hi_mask, shift, dmask);
-        radix_count(wh, v.w, prefix, hi_mask, shift, dmask);
+    for (; i + (kKlVec - 1) * stride < n4; i += kKlVec * stride) {
+        float4 u[kKlVec];
+#pragma unroll
+        for (int k = 0; k < kKlVec; k++) u[k] = x4[i + k * stride];
+#pragma unroll
+        for (int k = 0; k < kKlVec; k++) {
+            radix_count(s_h, u[k].x, prefix, hi_mask, shift, dmask);
+            radix_count(s_h, u[k].y, prefix, hi_mask, shift, dmask);
+            radix_count(s_h, u[k].z, prefix, hi_mask, shift, dmask);
+            radix_count(s_h, u[k].w, prefix, hi_mask, shift, dmask);
+        }
     }
     for (; i < n4; i += stride) {
         const float4 u = x4[i];
-        radix_count(wh, u.x, prefix, hi_mask, shift, dmask);
-        radix_count(wh, u.y, prefix, hi_mask, shift, dmask);
-        radix_count(wh, u.z, prefix, hi_mask, shift, dmask);
-        radix_count(wh, u.w, prefix, hi_mask, shift, dmask);
+        radix_count(s_h, u.x, prefix, hi_mask, shift, dmask);
+        radix_count(s_h, u.y, prefix, hi_mask, shift, dmask);
+        radix_count(s_h, u.z, prefix, hi_mask, shift, dmask);
+        radix_count(s_h, u.w, prefix, hi_mask, shift, dmask);
     }
-    for (int64_t j = n4 * 4 + tid; j < n; j += stride) radix_count(wh, x[j], prefix, hi_mask, shift, dmask);
+    for (int64_t j = n4 * 4 + tid; j < n; j += stride)
+        radix_count(s_h, x[j], prefix, hi_mask, shift, dmask);
     __syncthreads();
     for (int b = threadIdx.x; b < kRadixBins; b += kCalBlock) {
-        unsigned int c = 0;
-        for (int w = 0; w < kCalBlock / 64; w++) c += s_hist[w][b];
+        const unsigned int c = s_h[b];
         if (c) atomicAdd(&hist[b], (unsigned long long)c);
     }
-}
+    if (!arrive_last(arrivals, gridDim.x)) return;
 
-// Digit holding the element of rank st->rank (block prefix sum over the
-// 2048 digit counts, 8 per thread); clears the histogram after.
-__global__ __launch_bounds__(kCalBlock) void k_radix_pick(int shift, CalibState* st,
-                                                          unsigned long long* __restrict__ hist) {
     constexpr int kPer = kRadixBins / kCalBlock;
-    __shared__ unsigned long long s_scan[kCalBlock];
+    __shared__ unsigned long long s_wsum[kCalBlock / 64];
+    __shared__ uint32_t s_prefix;
     unsigned long long h[kPer], sum = 0;
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
-        h[j] = hist[threadIdx.x * kPer + j];
-        hist[threadIdx.x * kPer + j] = 0;
+        h[j] = __hip_atomic_load(hist + threadIdx.x * kPer + j, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
         sum += h[j];
     }
-    s_scan[threadIdx.x] = sum;
-    __syncthreads();
-    for (int o = 1; o < kCalBlock; o <<= 1) {  // inclusive scan
-        const unsigned long long v = threadIdx.x >= o ? s_scan[threadIdx.x - o] : 0ull;
-        __syncthreads();
-        s_scan[threadIdx.x] += v;
-        __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; j++) hist[threadIdx.x * kPer + j] = 0;
+    // inclusive scan of the per-thread sums: within each wave by shuffles,
+    // then the totals of the waves before
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned long long upto = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long v = __shfl_up(upto, o, 64);
+        if (lane >= o) upto += v;
     }
-    const int64_t rank = st->rank;
-    const unsigned long long before = threadIdx.x ? s_scan[threadIdx.x - 1] : 0ull;
-    const unsigned long long upto = s_scan[threadIdx.x];
-    __syncthreads();  // every thread has read st->rank before it is rewritten
+    if (lane == 63) s_wsum[wave] = upto;
+    const int64_t rank = first ? rank0 : st->rank;
+    __syncthreads();  // also: every thread has read st->rank before it is rewritten
+    for (int w = 0; w < wave; w++) upto += s_wsum[w];
+    const unsigned long long before = upto - sum;
     // a rank past the total lands in the last digit, as a sequential walk ends
     if ((unsigned long long)rank >= before &&
         ((unsigned long long)rank < upto || threadIdx.x == kCalBlock - 1)) {
@@ -319,33 +415,41 @@ __global__ __launch_bounds__(kCalBlock) void k_radix_pick(int shift, CalibState*
             if (r < (int64_t)h[d]) break;
             r -= (int64_t)h[d];
         }
+        const uint32_t np = prefix | ((uint32_t)(threadIdx.x * kPer + d) << shift);
         st->rank = r;
-        st->prefix |= (uint32_t)(threadIdx.x * kPer + d) << shift;
+        st->prefix = np;
+        s_prefix = np;
     }
-}
-
-// clip = the selected |x| (>= 1e-8); symmetric, or the reference's
-// asymmetric loop: data[0] unclipped, every later value clipped, so
-// min = data[0] < clip(min x) ? ... with the first-minimum rule (the partials
-// keep the sign of the first zero in index order).
-__global__ void k_pct_final(const float* __restrict__ x, int symmetric,
-                            const CalibState* __restrict__ st,
-                            tkv_hip_qparams_dev* __restrict__ out) {
-    double clip = (double)__uint_as_float(st->prefix);
-    if (clip <= 0.00000001) clip = 0.00000001;
-    if (symmetric) {
-        write_sym(clip, out);
-        return;
+    if (last) {
+        // clip = the selected |x| (>= 1e-8); symmetric, or the reference's
+        // asymmetric loop: data[0] unclipped, every later value clipped, so
+        // min = data[0] < clip(min x) ? ... with the first-minimum rule (the
+        // partials keep the sign of the first zero in index order).
+        __syncthreads();
+        double dmn = 0.0, dmx = 0.0;
+        if (!symmetric) {
+            reduce_partials(x, nparts, 1, partials, dmn, dmx);
+            nan_first(x, dmn, dmx);
+        }
+        if (threadIdx.x == 0) {
+            double clip = (double)__uint_as_float(s_prefix);
+            if (clip <= 0.00000001) clip = 0.00000001;
+            if (symmetric) {
+                write_sym(clip, out);
+            } else {
+                const double d0 = (double)x[0];
+                double vmn = dmn, vmx = dmx;
+                if (vmn < -clip) vmn = -clip;
+                if (vmn > clip) vmn = clip;
+                if (vmx < -clip) vmx = -clip;
+                if (vmx > clip) vmx = clip;
+                const double mn = vmn < d0 ? vmn : d0;
+                const double mx = vmx > d0 ? vmx : d0;
+                finalize_minmax(mn, mx, MM_ASYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
+            }
+        }
     }
-    const double d0 = (double)x[0];
-    double vmn = st->mn, vmx = st->mx;
-    if (vmn < -clip) vmn = -clip;
-    if (vmn > clip) vmn = clip;
-    if (vmx < -clip) vmx = -clip;
-    if (vmx > clip) vmx = clip;
-    const double mn = vmn < d0 ? vmn : d0;
-    const double mx = vmx > d0 ? vmx : d0;
-    finalize_minmax(mn, mx, MM_ASYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
+    arrive_clear(arrivals);
 }
 
 // ---------------------------------------------------------------------------
@@ -355,12 +459,25 @@ __global__ void k_pct_final(const float* __restrict__ x, int symmetric,
 // Candidate c (1-based) of num_candidates: thr = am * c / nc, scale = thr /
 // 127, inv = 1 / scale (f64, as the reference's locals).  Entries up to npad
 // (whole chunks) past nc repeat the last candidate; their sums are dropped.
-__global__ __launch_bounds__(kCalBlock) void k_mse_table(int nc, int npad,
-                                                         const CalibState* __restrict__ st,
+// The block first reduces the min / max partials to max|x| (NaN skipped, 0
+// when all are NaN) and records them in st for the selection.
+__global__ __launch_bounds__(kCalBlock) void k_mse_table(const float* __restrict__ x, int nparts,
+                                                         const RedPartial* __restrict__ partials,
+                                                         int nc, int npad,
+                                                         CalibState* __restrict__ st,
                                                          double* __restrict__ table) {
+    double dmn, dmx;
+    reduce_partials(x, nparts, 0, partials, dmn, dmx);
+    const double am = dmn <= dmx ? fmax(fabs(dmn), fabs(dmx)) : 0.0;
+    if (threadIdx.x == 0) {
+        nan_first(x, dmn, dmx);
+        st->am = am;
+        st->mn = dmn;
+        st->mx = dmx;
+    }
     for (int c = threadIdx.x; c < npad; c += kCalBlock) {
         const int cc = c < nc ? c : nc - 1;
-        const double thr = st->am * (double)(cc + 1) / (double)nc;
+        const double thr = am * (double)(cc + 1) / (double)nc;
         const double scale = thr / 127.0;
         table[3 * c + 0] = thr;
         table[3 * c + 1] = scale;
@@ -442,10 +559,16 @@ constexpr MsePartialsFn mse_partials_for(int ch, std::integer_sequence<int, CH..
     return fns[ch - 1];
 }
 
-// mse[c] = (sum over the per-block partials, a fixed tree order) / n.
+// mse[c] = (sum over the per-block partials, a fixed tree order) / n.  The
+// block that arrives last (arrive_last) makes the reference's first-minimum
+// pick over c ascending and writes the parameters.
 __global__ __launch_bounds__(kCalBlock) void k_mse_reduce(int64_t n, int nc, int nblocks,
                                                           const double* __restrict__ partial,
-                                                          double* __restrict__ mse) {
+                                                          double* __restrict__ mse,
+                                                          const double* __restrict__ table,
+                                                          const CalibState* __restrict__ st,
+                                                          unsigned* __restrict__ arrivals,
+                                                          tkv_hip_qparams_dev* __restrict__ out) {
     __shared__ double s_red[kCalBlock / 64];
     const int c = blockIdx.x;
     double a = 0.0;
@@ -457,29 +580,24 @@ __global__ __launch_bounds__(kCalBlock) void k_mse_reduce(int64_t n, int nc, int
     if (threadIdx.x == 0) {
         double t = 0.0;
         for (int w = 0; w < kCalBlock / 64; w++) t = t + s_red[w];
-        mse[c] = t / (double)n;
+        __hip_atomic_store(mse + c, t / (double)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (!arrive_last(arrivals, gridDim.x)) return;
+    const int bc = block_first_min(mse, nc);
+    if (threadIdx.x == 0) {
+        if (st->am < 0.00000001)
+            finalize_minmax(st->mn, st->mx, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
+        else
+            write_sym(bc >= 0 ? table[3 * bc] : st->am, out);
+    }
+    arrive_clear(arrivals);
 }
 
-// The first strict minimum over c ascending, as in the reference's loop.
-__global__ void k_mse_select(int nc, const double* __restrict__ table,
-                             const double* __restrict__ mse, const CalibState* __restrict__ st,
-                             tkv_hip_qparams_dev* __restrict__ out) {
-    double best = 1e45;
-    int bc = -1;
-    for (int c = 0; c < nc; c++)
-        if (mse[c] < best) {
-            best = mse[c];
-            bc = c;
-        }
-    if (st->am < 0.00000001)
-        finalize_minmax(st->mn, st->mx, MM_SYMMETRIC, TKV_HIP_RECIPE_PRIMARY, out);
-    else
-        write_sym(bc >= 0 ? table[3 * bc] : st->am, out);
-}
-
-int64_t cal_grid(Ctx* c, int64_t n) {
-    int64_t blocks = ceil_div(n, (int64_t)kCalBlock * 4);
+// Histogram passes (KL, radix), each lane taking kKlVec float4 per trip: two
+// blocks per CU, the fastest shape measured on MI355X for the LDS-atomic-bound
+// passes and for the stream-bound ones alike.
+int64_t hist_grid(Ctx* c, int64_t n) {
+    int64_t blocks = ceil_div(n, (int64_t)kCalBlock * 4 * kKlVec);
     const int64_t cap = (int64_t)c->num_cus * 2;
     if (blocks > cap) blocks = cap;
     return blocks < 1 ? 1 : blocks;
@@ -496,36 +614,37 @@ int cal_workspace(Ctx* c, size_t extra, CalibState** st, void** rest) {
 
 }  // namespace
 
+// The calibrators finish inside their last kernels (arrive_last), on the
+// context's calibration histogram and counters.
+static int need_cal_scratch(Ctx* c, const char* what) {
+    if (c->cal_hist && c->cal_arrivals) return TKV_HIP_OK;
+    return set_error(TKV_HIP_UNSUPPORTED,
+                     std::string(what) + ": this context has no calibration scratch");
+}
+
 int launch_calibrate_kl(Ctx* c, const float* x, int64_t n, int64_t num_bins, int64_t target_bins,
                         tkv_hip_qparams_dev* out) {
     if (n <= 0 || num_bins < 1 || num_bins > kMaxKlBins || target_bins < 1 ||
         target_bins > kMaxKlBins)
         return set_error(TKV_HIP_BAD_ARG,
                          "calibrate_kl: needs n > 0, 1 <= num_bins <= 4096, target_bins >= 1");
+    TKV_RC_TRY(need_cal_scratch(c, "calibrate_kl"));
     CalibState* st;
     void* rest;
     const int ncand = num_bins >= target_bins ? (int)((num_bins - target_bins) / 16 + 1) : 0;
-    TKV_RC_TRY(cal_workspace(c, (size_t)num_bins * 16 + (size_t)ncand * 8 + 8, &st, &rest));
-    auto* hist = static_cast<unsigned long long*>(rest);
-    double* kl = reinterpret_cast<double*>(hist + num_bins);
+    TKV_RC_TRY(cal_workspace(c, (size_t)(ncand > 0 ? ncand : 1) * 8, &st, &rest));
+    double* kl = static_cast<double*>(rest);
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
-    hipLaunchKernelGGL(k_cal_prep, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts, 0,
-                       c->partials, num_bins, st, hist, num_bins, (int64_t)0);
-    TKV_LAUNCH_CHECK();
     const int vec = aligned(x, 16) ? 1 : 0;
-    hipLaunchKernelGGL(k_kl_hist, dim3((unsigned)cal_grid(c, n)), dim3(kCalBlock),
-                       (size_t)num_bins * 4 * (kCalBlock / 64), c->stream, x, n, vec,
-                       (int)num_bins, st, hist);
+    hipLaunchKernelGGL(k_kl_hist, dim3((unsigned)hist_grid(c, n)), dim3(kCalBlock),
+                       (size_t)(num_bins + 1) * 4 * kKlCopies, c->stream, x, n, vec,
+                       (int)num_bins, (int)nparts, c->partials, st, c->cal_hist);
     TKV_LAUNCH_CHECK();
-    if (ncand > 0) {
-        hipLaunchKernelGGL(k_kl_candidate, dim3((unsigned)ncand), dim3(64),
-                           (size_t)(num_bins + target_bins) * 8, c->stream, (int)num_bins,
-                           (int)target_bins, hist, kl);
-        TKV_LAUNCH_CHECK();
-    }
-    hipLaunchKernelGGL(k_kl_select, dim3(1), dim3(1), 0, c->stream, ncand, (int)num_bins,
-                       (int)target_bins, kl, st, out);
+    const size_t lds = (size_t)(((num_bins + 63) & ~63) + (target_bins > 8 ? target_bins : 8)) * 8;
+    hipLaunchKernelGGL(k_kl_candidate, dim3((unsigned)(ncand > 0 ? ncand : 1)),
+                       dim3(kKlCandBlock), ncand > 0 ? lds : 0, c->stream, (int)num_bins,
+                       (int)target_bins, ncand, c->cal_hist, kl, st, c->cal_arrivals + 1, out);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
@@ -542,29 +661,24 @@ int launch_calibrate_percentile(Ctx* c, const float* x, int64_t n, float percent
     if (n <= 0) return set_error(TKV_HIP_BAD_ARG, "calibrate_percentile: empty input");
     if (!(percentile > 0.0f && percentile <= 100.0f))
         return set_error(TKV_HIP_BAD_ARG, "percentile must be in (0, 100]");
+    TKV_RC_TRY(need_cal_scratch(c, "calibrate_percentile"));
     CalibState* st;
     void* rest;
-    TKV_RC_TRY(cal_workspace(c, (size_t)kRadixBins * 8, &st, &rest));
-    auto* hist = static_cast<unsigned long long*>(rest);
-    int64_t nparts;
-    TKV_RC_TRY(launch_partials(c, x, n, symmetric ? 0 : 1, &nparts));
-    hipLaunchKernelGGL(k_cal_prep, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts,
-                       symmetric ? 0 : 1, c->partials, (int64_t)0, st, hist, (int64_t)kRadixBins,
-                       percentile_rank(n, percentile));
-    TKV_LAUNCH_CHECK();
-    const int grid = (int)cal_grid(c, n);
+    TKV_RC_TRY(cal_workspace(c, 0, &st, &rest));
+    // the min / max partials only feed the asymmetric parameters
+    int64_t nparts = 0;
+    if (!symmetric) TKV_RC_TRY(launch_partials(c, x, n, 1, &nparts));
+    const int grid = (int)hist_grid(c, n);
     const int vec = aligned(x, 16) ? 1 : 0;
+    const int64_t rank = percentile_rank(n, percentile);
     const int shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
     for (int r = 0; r < 3; r++) {
-        hipLaunchKernelGGL(k_radix_hist, dim3((unsigned)grid), dim3(kCalBlock), 0, c->stream, x,
-                           n, vec, shifts[r], widths[r], st, hist);
-        TKV_LAUNCH_CHECK();
-        hipLaunchKernelGGL(k_radix_pick, dim3(1), dim3(kCalBlock), 0, c->stream, shifts[r], st,
-                           hist);
+        hipLaunchKernelGGL(k_radix_pass, dim3((unsigned)grid), dim3(kCalBlock), 0, c->stream, x,
+                           n, vec, shifts[r], widths[r], r == 0 ? 1 : 0, r == 2 ? 1 : 0, rank,
+                           symmetric ? 1 : 0, (int)nparts, c->partials, st, c->cal_hist,
+                           c->cal_arrivals + 2, out);
         TKV_LAUNCH_CHECK();
     }
-    hipLaunchKernelGGL(k_pct_final, dim3(1), dim3(1), 0, c->stream, x, symmetric, st, out);
-    TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
 
@@ -572,6 +686,7 @@ int launch_calibrate_mse(Ctx* c, const float* x, int64_t n, int64_t num_candidat
                          tkv_hip_qparams_dev* out) {
     if (n <= 0 || num_candidates > kMaxMseCandidates)
         return set_error(TKV_HIP_BAD_ARG, "calibrate_mse: needs n > 0, num_candidates <= 4096");
+    TKV_RC_TRY(need_cal_scratch(c, "calibrate_mse"));
     const int nc = (int)(num_candidates < 4 ? 4 : num_candidates);
     // passes of ch <= kMseChunk candidates, as even as whole passes allow
     const int passes = (int)ceil_div((int64_t)nc, (int64_t)kMseChunk);
@@ -591,11 +706,8 @@ int launch_calibrate_mse(Ctx* c, const float* x, int64_t n, int64_t num_candidat
     double* partial = mse + nc;
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, 0, &nparts));
-    hipLaunchKernelGGL(k_cal_prep, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts, 0,
-                       c->partials, (int64_t)0, st, (unsigned long long*)nullptr, (int64_t)0,
-                       (int64_t)0);
-    TKV_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_mse_table, dim3(1), dim3(kCalBlock), 0, c->stream, nc, npad, st, table);
+    hipLaunchKernelGGL(k_mse_table, dim3(1), dim3(kCalBlock), 0, c->stream, x, (int)nparts,
+                       c->partials, nc, npad, st, table);
     TKV_LAUNCH_CHECK();
     const MsePartialsFn fn = mse_partials_for(ch, std::make_integer_sequence<int, kMseChunk>());
     for (int c0 = 0; c0 < nc; c0 += ch) {
@@ -604,9 +716,7 @@ int launch_calibrate_mse(Ctx* c, const float* x, int64_t n, int64_t num_candidat
         TKV_LAUNCH_CHECK();
     }
     hipLaunchKernelGGL(k_mse_reduce, dim3((unsigned)nc), dim3(kCalBlock), 0, c->stream, n, nc,
-                       grid, partial, mse);
-    TKV_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_mse_select, dim3(1), dim3(1), 0, c->stream, nc, table, mse, st, out);
+                       grid, partial, mse, table, st, c->cal_arrivals + 3, out);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -48,16 +48,26 @@ __device__ __forceinline__ float4 ld4(const float4* p) {
     }
 }
 
-// Per-tensor min / max (+ first zero): one partial per block, then a
-// one-block finalize kernel.  The kernel boundary orders the partial stores
-// before the finalize reads, across XCDs and their separate L2s, without
-// device-scope fences in the streaming kernel.
-template <bool TRACK_ZERO, bool NT>
+// Per-tensor min / max (+ first zero): one partial per block.  Consumers
+// either reduce the partials themselves (the quantize kernels, every block),
+// or (FIN) the last block to arrive reduces them and writes the QuantParams:
+// the partials then go through the device coherence point (store_partial_sc1,
+// arrive_last), so no finalize kernel and no cache maintenance is needed.
+// Without FIN the kernel boundary orders the partial stores before the
+// consumer's reads.
+template <bool TRACK_ZERO, bool NT, bool FIN = false>
 __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __restrict__ x,
                                                                int64_t n, int vec,
-                                                               RedPartial* __restrict__ partials) {
+                                                               RedPartial* __restrict__ partials,
+                                                               unsigned* __restrict__ arrivals = nullptr,
+                                                               int mode = 0, int recipe = 0,
+                                                               tkv_hip_qparams_dev* __restrict__ out = nullptr) {
     float mn = __builtin_inff(), mx = -__builtin_inff();
     unsigned long long zi = ~0ull;
+    // x[0] for the first-element NaN rule, loaded early: the last block's
+    // finalize would otherwise wait for it at the end of the kernel
+    float x0 = 0.0f;
+    if (FIN && threadIdx.x == 0) x0 = x[0];
     const int64_t stride = (int64_t)gridDim.x * kRedBlock;
     const int64_t tid = (int64_t)blockIdx.x * kRedBlock + threadIdx.x;
     int64_t n4 = vec ? n / 4 : 0;
@@ -103,11 +113,25 @@ __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __re
             mx = fmaxf(mx, s_mx[w]);
             zi = s_zi[w] < zi ? s_zi[w] : zi;
         }
-        RedPartial p;
-        p.mn = mn;
-        p.mx = mx;
-        p.zidx = zi;
-        partials[blockIdx.x] = p;
+        if constexpr (FIN) {
+            store_partial_sc1(partials + blockIdx.x, mn, mx, zi);
+        } else {
+            RedPartial p;
+            p.mn = mn;
+            p.mx = mx;
+            p.zidx = zi;
+            partials[blockIdx.x] = p;
+        }
+    }
+    if constexpr (FIN) {
+        if (!arrive_last(arrivals, gridDim.x)) return;
+        double dmn, dmx;
+        reduce_partials<true>(x, (int)gridDim.x, TRACK_ZERO, partials, dmn, dmx);
+        if (threadIdx.x == 0) {
+            if (x0 != x0) dmn = dmx = (double)x0;  // nan_first
+            finalize_minmax(dmn, dmx, mode, recipe, out);
+        }
+        arrive_clear(arrivals);
     }
 }
 
@@ -156,6 +180,26 @@ int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe
                          tkv_hip_qparams_dev* out) {
     // Only the asymmetric QuantParams expose the sign of a zero extreme.
     const int track_zero = (mode == MM_ASYMMETRIC) ? 1 : 0;
+    if (c->cal_arrivals) {  // one kernel: its last block finalizes
+        const int vec = aligned(x, 16) ? 1 : 0;
+        const int64_t blocks = partial_blocks(c, vec ? n / 4 : n, vec);
+        const bool nt = n * 4 > kCacheableBytes;
+        unsigned* arr = c->cal_arrivals + 0;
+#define TKV_PARTIALS_FIN(TZ, NT)                                                           \
+    hipLaunchKernelGGL((k_minmax_partials<TZ, NT, true>), dim3((unsigned)blocks),         \
+                       dim3(kRedBlock), 0, c->stream, x, n, vec, c->partials, arr, mode, \
+                       recipe, out)
+        if (track_zero) {
+            if (nt) TKV_PARTIALS_FIN(true, true);
+            else TKV_PARTIALS_FIN(true, false);
+        } else {
+            if (nt) TKV_PARTIALS_FIN(false, true);
+            else TKV_PARTIALS_FIN(false, false);
+        }
+#undef TKV_PARTIALS_FIN
+        TKV_LAUNCH_CHECK();
+        return TKV_HIP_OK;
+    }
     int64_t nparts;
     TKV_RC_TRY(launch_partials(c, x, n, track_zero, &nparts));
     hipLaunchKernelGGL(k_minmax_finalize, dim3(1), dim3(kBlock), 0, c->stream, x, (int)nparts,

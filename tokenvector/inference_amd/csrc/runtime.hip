@@ -72,7 +72,8 @@ int ctx_create(int device, Ctx** out) {
     const size_t gemv_bytes = (size_t)kGemvSplitBlocks * 1024 * sizeof(int32_t);
     size_t red_bytes = sizeof(RedPartial) * kMaxReduceBlocks + 256 + sizeof(tkv_hip_qparams_dev) * 64 +
                        256 + gemv_bytes + (size_t)kGemvSplitBlocks * sizeof(unsigned) + 256 +
-                       (size_t)kMaxGridSlots * 8;
+                       (size_t)kMaxGridSlots * 8 + (size_t)kCalHistBins * 8 +
+                       (size_t)kCalCounters * sizeof(unsigned);
     void* red = nullptr;
     e = hipMalloc(&red, red_bytes);
     if (e != hipSuccess) {
@@ -89,6 +90,8 @@ int ctx_create(int device, Ctx** out) {
         const uintptr_t end = reinterpret_cast<uintptr_t>(c->gemv_arrivals + kGemvSplitBlocks);
         c->grid_slots = reinterpret_cast<unsigned long long*>((end + 255) & ~uintptr_t(255));
     }
+    c->cal_hist = c->grid_slots + kMaxGridSlots;
+    c->cal_arrivals = reinterpret_cast<unsigned*>(c->cal_hist + kCalHistBins);
     // One-time zeroing at creation, so params read before any calibration
     // are defined (never inside a caller's stream capture).
     e = hipMemset(red, 0, red_bytes);

@@ -43,6 +43,10 @@ constexpr int kMaxReduceBlocks = 2048;
 constexpr int kGemvSplitBlocks = 128;
 // Workgroups of a grid-barrier kernel (one per CU) plus its result word.
 constexpr int kMaxGridSlots = 1024;
+// Arrival counts of the calibration kernels whose last workgroup finishes
+// the call: 0 calibrate_minmax, 1 KL candidates, 2 radix passes, 3 MSE sums.
+constexpr int kCalCounters = 4;
+constexpr int64_t kCalHistBins = 4096;  // the largest KL histogram
 
 struct RedPartial {
     float mn;
@@ -69,6 +73,12 @@ struct Ctx {
     // kMaxGridSlots), zero at creation; every launch advances each slot it
     // uses, and the result word, by one generation.
     unsigned long long* grid_slots = nullptr;
+    // Calibration histogram (kCalHistBins 64-bit counts) and kCalCounters
+    // arrival counts: zero at creation, and every calibration call that uses
+    // them leaves them zero (its last workgroup clears what it used).
+    // Contexts that do not run the calibrators leave them null.
+    unsigned long long* cal_hist = nullptr;
+    unsigned* cal_arrivals = nullptr;
     // grow-only workspaces
     static constexpr int kSlots = 13;  // 10, 11: f16-decoded FP8 operands; 12: INT4 split partials
     void* ws[kSlots] = {};

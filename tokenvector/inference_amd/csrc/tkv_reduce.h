@@ -93,18 +93,72 @@ __device__ __forceinline__ void nan_first(const float* x, double& dmn, double& d
     if (x0 != x0) dmn = dmx = (double)x0;
 }
 
+// Cross-workgroup hand-off inside one kernel, without cache maintenance:
+// values another workgroup will read are written with agent-scope atomic
+// stores or device atomics and read with agent-scope atomic loads, which
+// gfx950 performs at the device coherence point (sc1: not held in, or served
+// from, an XCD's L2).  Every wave waits for its own writes to complete
+// (vmcnt(0): such a write completes once it is performed there) before the
+// workgroup barrier, and one arrival add on `counter` (zero on entry) follows
+// that barrier.  Returns true in every thread of the workgroup that completes
+// the count of `total`; its loads are issued after its arrival add returned,
+// so every other workgroup's writes are in place.  That workgroup clears the
+// counter (arrive_clear) for the next call.  A release add with an acquire
+// fence would instead write back and invalidate a whole L2 per workgroup.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned total) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 total - 1;
+    __syncthreads();
+    return s_last != 0;
+}
+
+__device__ __forceinline__ void arrive_clear(unsigned* counter) {
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One partial as two agent-scope 8-byte stores / loads ({mn, mx}, zidx).
+__device__ __forceinline__ void store_partial_sc1(RedPartial* p, float mn, float mx,
+                                                  unsigned long long zi) {
+    const unsigned long long w = (unsigned long long)__float_as_uint(mn) |
+                                 ((unsigned long long)__float_as_uint(mx) << 32);
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&p->zidx, zi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool SC1>
+__device__ __forceinline__ RedPartial load_partial(const RedPartial* p) {
+    if constexpr (SC1) {
+        const unsigned long long w = __hip_atomic_load(
+            reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        RedPartial r;
+        r.mn = __uint_as_float((uint32_t)w);
+        r.mx = __uint_as_float((uint32_t)(w >> 32));
+        r.zidx = __hip_atomic_load(&p->zidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return r;
+    } else {
+        return *p;
+    }
+}
+
 // Reduces the per-block partials (every thread of a kBlock-thread block
 // takes part; the result is returned to all of them) to the reference's f64
 // min / max locals.  The reference keeps the first element reaching an
 // extreme; values that compare equal are bit-identical except +-0, so a zero
-// extreme takes the sign of the first zero in index order.
+// extreme takes the sign of the first zero in index order.  SC1: partials
+// written by other workgroups of the running kernel (store_partial_sc1).
+template <bool SC1 = false>
 __device__ inline void reduce_partials(const float* __restrict__ x, int nparts, int track_zero,
                                        const RedPartial* __restrict__ partials, double& dmn,
                                        double& dmx) {
     float mn = __builtin_inff(), mx = -__builtin_inff();
     unsigned long long zi = ~0ull;
     for (int b = threadIdx.x; b < nparts; b += kBlock) {
-        RedPartial p = partials[b];
+        const RedPartial p = load_partial<SC1>(partials + b);
         mn = fminf(mn, p.mn);
         mx = fmaxf(mx, p.mx);
         zi = p.zidx < zi ? p.zidx : zi;
@@ -136,6 +190,50 @@ __device__ inline void reduce_partials(const float* __restrict__ x, int nparts, 
         if (mn == 0.0f) dmn = z;
         if (mx == 0.0f) dmx = z;
     }
+}
+
+// The reference's selection loop `if v[c] < best: best = v[c]; pick c` over
+// c ascending from best = 1e45, on a kBlock-thread block (every thread calls
+// it; the pick, or -1 for none, is returned to all).  Its pick is the
+// smallest index holding the least value below 1e45 (`<`, so NaN never
+// counts and +-0 tie): each thread takes the first strict minimum of its
+// indices c = tid (mod kBlock), and pairs combine to the smaller value, or on
+// == values to the smaller index.  The values are read with agent-scope
+// loads (written by other workgroups of the running kernel).
+__device__ inline int block_first_min(const double* v, int count) {
+    __shared__ double s_b[kBlock / 64];
+    __shared__ int s_i[kBlock / 64];
+    double best = 1e45;
+    int bi = 0x7fffffff;
+    for (int c = threadIdx.x; c < count; c += kBlock) {
+        const double x = __hip_atomic_load(v + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (x < best) {
+            best = x;
+            bi = c;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const double ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ob < best || (ob == best && oi < bi)) {
+            best = ob;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_b[threadIdx.x >> 6] = best;
+        s_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    best = s_b[0];
+    bi = s_i[0];
+    for (int w = 1; w < kBlock / 64; w++)
+        if (s_b[w] < best || (s_b[w] == best && s_i[w] < bi)) {
+            best = s_b[w];
+            bi = s_i[w];
+        }
+    return bi == 0x7fffffff ? -1 : bi;
 }
 
 }  // namespace tkv
