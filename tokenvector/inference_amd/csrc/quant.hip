@@ -859,6 +859,8 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
         float4 v[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) v[u] = ld4(x4 + i + u * stride);
+        uint32_t w[kUnroll];
+        bool special = false;
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             if (scaled) {
@@ -867,8 +869,16 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
                 v[u].z *= mul;
                 v[u].w *= mul;
             }
-            store_fp8x4<OUT_I32>(q, i + u * stride, e4m3_encode4(v[u].x, v[u].y, v[u].z, v[u].w));
+            special = special | e4m3_special(v[u].x) | e4m3_special(v[u].y) |
+                      e4m3_special(v[u].z) | e4m3_special(v[u].w);
+            w[u] = e4m3_encode4_finite(v[u].x, v[u].y, v[u].z, v[u].w);
         }
+        if (special) {  // +-inf or NaN in this lane's trip: the patched form
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) w[u] = e4m3_encode4(v[u].x, v[u].y, v[u].z, v[u].w);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) store_fp8x4<OUT_I32>(q, i + u * stride, w[u]);
     }
     for (; i < n4; i += stride) {
         float4 v = ld4(x4 + i);
@@ -896,10 +906,10 @@ int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_d
     if (n <= 0) return TKV_HIP_OK;
     int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
     // The e4m3 encode costs more ALU work per element than the int8 quantize
-    // (the hardware conversion plus the reference's fix-ups, ~12 operations
-    // per element): three blocks per CU overlap it with the loads best (at
-    // 201 MB: 43.9 us against 46.7 / 48.2 / 46.0 / 46.4 us at 2 / 4 / 6 / 8,
-    // same box, medians of four interleaved rounds).
+    // (~11 operations per element: the magnitude clamps in front of the
+    // hardware conversion): three blocks per CU overlap it with the loads at
+    // least as well as two, and better than four (at 201 MB: 41.6-42.7 us
+    // against 41.4-43.6 / 46.2-47.0 us, three interleaved rounds on one box).
     int64_t blocks = ceil_div(vec ? n / 4 : n, (int64_t)kBlock * kUnroll);
     const int64_t cap = (int64_t)c->num_cus * (vec ? 3 : 16);
     if (blocks > cap) blocks = cap;

@@ -86,6 +86,28 @@ __device__ __forceinline__ uint32_t e4m3_encode4(float a, float b, float c, floa
            (e4m3_fix(bc, (h >> 16) & 0xffu) << 16) | (e4m3_fix(bd, h >> 24) << 24);
 }
 
+// The same codes for finite x with the fix-ups moved in front of the
+// conversion: the magnitude is clamped where the reference departs from OCP
+// (|x| >= 248 -> 448, coded 0x7E; |x| < 2^-6 -> at most 7 * 2^-9, coded at
+// most 0x07) and +-0 becomes +0 (code 0x00), so the hardware code of the
+// signed result is the reference's, sign included (a nonzero value that
+// rounds to zero keeps 0x80).  +-inf and NaN are not covered: callers test
+// for them (e4m3_special) and take e4m3_encode4 instead.
+__device__ __forceinline__ float e4m3_pre(float x) {
+    const float a = fabsf(x);
+    float m = a < 0x1p-6f ? fminf(a, 0x1.cp-7f) : a;  // 0x1.cp-7 = 7 * 2^-9
+    m = a >= 248.0f ? 448.0f : m;
+    return a == 0.0f ? 0.0f : __builtin_copysignf(m, x);
+}
+
+__device__ __forceinline__ bool e4m3_special(float x) { return !(fabsf(x) < __builtin_inff()); }
+
+__device__ __forceinline__ uint32_t e4m3_encode4_finite(float a, float b, float c, float d) {
+    int hw = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_pre(a), e4m3_pre(b), 0, false);
+    hw = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_pre(c), e4m3_pre(d), hw, true);
+    return (uint32_t)hw;
+}
+
 __device__ __forceinline__ uint32_t e4m3_encode1(float a) {
     const uint32_t ba = __float_as_uint(a);
     const int hw = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(ba & 0x7fffffffu), 0.0f, 0, false);
