@@ -247,23 +247,82 @@ __global__ __launch_bounds__(kBlock) void k_quant_i8_tensor(const float* __restr
                                                             void* __restrict__ q, int nparts,
                                                             int recipe,
                                                             const RedPartial* __restrict__ partials) {
-    double inv;
-    if constexpr (FUSED) {
-        double dmn, dmx;
-        reduce_partials(x, nparts, 0, partials, dmn, dmx);
-        nan_first(x, dmn, dmx);
-        tkv_hip_qparams_dev prm;
-        finalize_minmax(dmn, dmx, MM_SYMMETRIC, recipe, &prm);
-        inv = prm.inv;
-        if (blockIdx.x == 0 && threadIdx.x == 0) *p = prm;
-    } else {
-        inv = p->inv;
-    }
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     int64_t n4 = vec ? n / 4 : 0;
     const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
     int64_t i = tid;
+    double inv;
+    if constexpr (FUSED) {
+        // The partials are loaded first and the first trip of x right after;
+        // loads complete in issue order, so waiting for the partials leaves
+        // the x loads in flight and the two latencies overlap.  The reduction
+        // is reduce_partials' (exact min / max, so its order does not matter).
+        // Both groups of loads are issued unconditionally (indices clamped:
+        // a repeated partial leaves min / max unchanged; past the float4s of
+        // x, or with none, the x loads read a valid dummy), because a branch
+        // around either would make the wait for the partials drain both.
+        const float x0 = x[0];  // the first-element NaN rule (nan_first)
+        constexpr int kPp = kMaxReduceBlocks / kBlock;
+        float pmn[kPp], pmx[kPp];
+#pragma unroll
+        for (int j = 0; j < kPp; j++) {
+            const int b = (int)threadIdx.x + j * kBlock;
+            const RedPartial* pp = partials + (b < nparts ? b : nparts - 1);
+            pmn[j] = pp->mn;
+            pmx[j] = pp->mx;
+        }
+        float4 v0[kUnroll];
+        const bool pre = i + (kUnroll - 1) * stride < n4;
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t j = i + u * stride < n4 ? i + u * stride : n4 - 1;
+            v0[u] = ld4<NT>(n4 > 0 ? x4 + j : reinterpret_cast<const float4*>(partials));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the reduction
+        float mn = pmn[0], mx = pmx[0];
+#pragma unroll
+        for (int j = 1; j < kPp; j++) {
+            mn = fminf(mn, pmn[j]);
+            mx = fmaxf(mx, pmx[j]);
+        }
+        __shared__ float s_mn[kBlock / 64], s_mx[kBlock / 64];
+        mn = wave_min(mn);
+        mx = wave_max(mx);
+        if ((threadIdx.x & 63) == 0) {
+            s_mn[threadIdx.x >> 6] = mn;
+            s_mx[threadIdx.x >> 6] = mx;
+        }
+        __syncthreads();
+        mn = s_mn[0];
+        mx = s_mx[0];
+        for (int w = 1; w < kBlock / 64; w++) {
+            mn = fminf(mn, s_mn[w]);
+            mx = fmaxf(mx, s_mx[w]);
+        }
+        double dmn = mn, dmx = mx;
+        if (x0 != x0) dmn = dmx = (double)x0;
+        tkv_hip_qparams_dev prm;
+        finalize_minmax(dmn, dmx, MM_SYMMETRIC, recipe, &prm);
+        inv = prm.inv;
+        if (blockIdx.x == 0 && threadIdx.x == 0) *p = prm;
+        if (pre) {
+            // pins the first use of the early loads here, so the compiler
+            // cannot convert them (and wait for them) before the reduction
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++)
+                asm volatile("" : "+v"(v0[u].x), "+v"(v0[u].y), "+v"(v0[u].z), "+v"(v0[u].w));
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++)
+                store4<OUT_I32>(q, i + u * stride, rne_clamp((double)v0[u].x * inv, -127.0, 127.0),
+                                rne_clamp((double)v0[u].y * inv, -127.0, 127.0),
+                                rne_clamp((double)v0[u].z * inv, -127.0, 127.0),
+                                rne_clamp((double)v0[u].w * inv, -127.0, 127.0));
+            i += kUnroll * stride;
+        }
+    } else {
+        inv = p->inv;
+    }
     for (; i + (kUnroll - 1) * stride < n4; i += kUnroll * stride) {
         float4 v[kUnroll];
 #pragma unroll
@@ -860,7 +919,7 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) v[u] = ld4(x4 + i + u * stride);
         uint32_t w[kUnroll];
-        bool special = false;
+        int special = 0;
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             if (scaled) {
@@ -869,8 +928,8 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
                 v[u].z *= mul;
                 v[u].w *= mul;
             }
-            special = special | e4m3_special(v[u].x) | e4m3_special(v[u].y) |
-                      e4m3_special(v[u].z) | e4m3_special(v[u].w);
+            special |= (int)e4m3_special(v[u].x) | (int)e4m3_special(v[u].y) |
+                       (int)e4m3_special(v[u].z) | (int)e4m3_special(v[u].w);
             w[u] = e4m3_encode4_finite(v[u].x, v[u].y, v[u].z, v[u].w);
         }
         if (special) {  // +-inf or NaN in this lane's trip: the patched form
