@@ -990,11 +990,18 @@ def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
     GEMM configuration, including the skinny kernel (M <= 32; at N = 768
     with K split over workgroups), bit-exact."""
     gemm_cfg(cfg)
-    for (m, n, k) in [(37, 100, 200), (1024, 768, 768), (16, 2304, 768), (16, 768, 3072)]:
-        say(f"dev qlinear cfg={cfg} {m}x{n}x{k}")
+    # zero points: both set; zpa = 0 (no W sums needed); zpw = 0 (no A sums);
+    # both 0 (no pre-pass at all); zpw = 0 with |zpa| large enough for the f64
+    # correction path at K = 768
+    cases = [((37, 100, 200), (-3, 5, 7)), ((1024, 768, 768), (-3, 5, 7)),
+             ((16, 2304, 768), (-3, 5, 7)), ((16, 768, 3072), (-3, 5, 7)),
+             ((37, 100, 200), (0, 5, 7)), ((37, 100, 200), (-3, 0, 7)),
+             ((1024, 768, 768), (0, 0, -2)), ((64, 96, 768), (30000, 0, 3)),
+             ((64, 96, 768), (0, -30000, 3))]
+    for (m, n, k), (zpa, zpw, zpy) in cases:
+        say(f"dev qlinear cfg={cfg} {m}x{n}x{k} zp={zpa},{zpw},{zpy}")
         a = RNG.integers(-128, 128, m * k).astype(np.int8)
         w = RNG.integers(-128, 128, n * k).astype(np.int8)   # [N, K] = B transposed
-        zpa, zpw, zpy = -3, 5, 7
         sa, sw = np.float32(0.02), np.float32(0.003)
         sy = np.float32(np.sqrt(k) * 128 * 128 * sa * sw / 90.0)
         da, dw = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, w)

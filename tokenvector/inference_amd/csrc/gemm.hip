@@ -954,7 +954,10 @@ static int check_sizes(int64_t m, int64_t n, int64_t k, const char* what) {
 int64_t gemm_k_align() { return gemm::kBK; }
 
 // QLinearMatMul: row sums of A and W first (zero padding past k adds
-// nothing), then the GEMM with the requantizing epilogue.
+// nothing), then the GEMM with the requantizing epilogue.  The sums enter the
+// corrections only through zpw * sum(a) and zpa * sum(w), so the rows of A are
+// summed only for zpw != 0 and those of W only for zpa != 0; the epilogue
+// reads the others (any int32 value) and multiplies them by zero.
 int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n,
                         int64_t k, const QLinearParams& q, int8_t* y) {
     if (m <= 0 || n <= 0) return TKV_HIP_OK;
@@ -965,7 +968,8 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
     void* sums;
     TKV_RC_TRY(ctx_workspace(c, 8, (size_t)(m + n) * 4, &sums));
     int32_t* ra = static_cast<int32_t*>(sums);
-    TKV_RC_TRY(launch_row_sums_i8(c, a, m, w, n, k, ra));
+    TKV_RC_TRY(launch_row_sums_i8(c, a, q.zpw != 0 ? m : 0, w, q.zpa != 0 ? n : 0, k, ra,
+                                  ra + m));
     const void *pa = a, *pw = w;
     int64_t ldk;
     TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));

@@ -1018,7 +1018,8 @@ int launch_fp8_decode(Ctx* c, const void* q, bool in_i32, int64_t n, float* y) {
 
 // ---------------------------------------------------------------------------
 // Row sums of int8 codes (the zero-point corrections of QLinearMatMul): rows
-// [0, rows_a) of A, then rows [0, rows_w) of W, in one launch.  With 16-byte
+// [0, rows_a) of A into out_a, then rows [0, rows_w) of W into out_w, in one
+// launch.  With 16-byte
 // rows (cols % 16 == 0, aligned) a wave64 sums R rows, 64 / R lanes each;
 // each lane issues up to four 16-byte loads at once and adds their bytes with
 // v_dot4_i32_i8 against 0x01010101.  Otherwise one wave per row, byte by
@@ -1029,7 +1030,8 @@ __global__ __launch_bounds__(kBlock) void k_row_sums_i8(const int8_t* __restrict
                                                         int64_t rows_a,
                                                         const int8_t* __restrict__ w,
                                                         int64_t rows_w, int64_t cols, int vec,
-                                                        int32_t* __restrict__ out) {
+                                                        int32_t* __restrict__ out_a,
+                                                        int32_t* __restrict__ out_w) {
     constexpr int L = 64 / R;
     const int lane = threadIdx.x & 63;
     const int64_t wave = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
@@ -1060,18 +1062,18 @@ __global__ __launch_bounds__(kBlock) void k_row_sums_i8(const int8_t* __restrict
         }
 #pragma unroll
         for (int o = L / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-        if (live && lane % L == 0) out[r] = sum;
+        if (live && lane % L == 0) (r < rows_a ? out_a + r : out_w + (r - rows_a))[0] = sum;
     } else {
         if (!live) return;
         for (int64_t c = lane; c < cols; c += 64) sum += row[c];
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-        if (lane == 0) out[r] = sum;
+        if (lane == 0) (r < rows_a ? out_a + r : out_w + (r - rows_a))[0] = sum;
     }
 }
 
 int launch_row_sums_i8(Ctx* c, const int8_t* a, int64_t rows_a, const int8_t* w, int64_t rows_w,
-                       int64_t cols, int32_t* out) {
+                       int64_t cols, int32_t* out_a, int32_t* out_w) {
     const int64_t rows = rows_a + rows_w;
     if (rows <= 0) return TKV_HIP_OK;
     const int vec = (cols % 16 == 0 && aligned(a, 16) && aligned(w, 16)) ? 1 : 0;
@@ -1084,13 +1086,13 @@ int launch_row_sums_i8(Ctx* c, const int8_t* a, int64_t rows_a, const int8_t* w,
     const dim3 grid((unsigned)ceil_div(waves, kBlock / 64)), block(kBlock);
     if (R == 4)
         hipLaunchKernelGGL(k_row_sums_i8<4>, grid, block, 0, c->stream, a, rows_a, w, rows_w, cols,
-                           vec, out);
+                           vec, out_a, out_w);
     else if (R == 2)
         hipLaunchKernelGGL(k_row_sums_i8<2>, grid, block, 0, c->stream, a, rows_a, w, rows_w, cols,
-                           vec, out);
+                           vec, out_a, out_w);
     else
         hipLaunchKernelGGL(k_row_sums_i8<1>, grid, block, 0, c->stream, a, rows_a, w, rows_w, cols,
-                           vec, out);
+                           vec, out_a, out_w);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -195,10 +195,10 @@ struct QLinearParams {
 };
 int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n,
                         int64_t k, const QLinearParams& q, int8_t* y);
-// out[r] = sum of row r's `cols` int8 codes: rows of A [rows_a, cols], then
-// rows of W [rows_w, cols] (both compact).
+// Sums of each row's `cols` int8 codes: out_a[r] for the rows of A
+// [rows_a, cols], out_w[r] for the rows of W [rows_w, cols] (both compact).
 int launch_row_sums_i8(Ctx* c, const int8_t* a, int64_t rows_a, const int8_t* w, int64_t rows_w,
-                       int64_t cols, int32_t* out);
+                       int64_t cols, int32_t* out_a, int32_t* out_w);
 
 // Grouped INT4 (int4.hip).  packed: bytes, or int32 per byte (out32 / in32,
 // the reference's list format); zps NULL selects the symmetric form.
