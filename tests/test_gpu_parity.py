@@ -150,6 +150,34 @@ def test_calibrate_percentile(hip, n):
         Q.calibrate_percentile(x, 0.0)
 
 
+@pytest.mark.parametrize("kind", ["constant", "cluster", "two_values", "ties"])
+def test_calibrate_percentile_staging(hip, kind):
+    """The second radix pass stages the elements that share the first digit,
+    up to 2048 per workgroup, and the third reads only those; a workgroup
+    with more sets the spill flag and the third pass reads all of x.  Data
+    that overflows the staging everywhere (constant), in some workgroups
+    (a dense cluster in one stretch of the tensor), or nowhere (two values,
+    exact ties across digits) must all give the oracle's parameters."""
+    say(f"calibrate_percentile staging {kind}")
+    n = 1 << 22
+    rng = np.random.default_rng(11)
+    if kind == "constant":
+        x = np.full(n, 1.5, np.float32)
+    elif kind == "cluster":
+        x = rng.standard_normal(n).astype(np.float32)
+        x[n // 3: n // 3 + (1 << 20)] = np.float32(0.75) + rng.uniform(0, 1e-6, 1 << 20).astype(
+            np.float32)
+    elif kind == "two_values":
+        x = np.where(rng.uniform(size=n) < 0.5, np.float32(-2.0), np.float32(0.25)).astype(
+            np.float32)
+    else:
+        x = (rng.integers(-1000, 1001, n) / np.float32(64.0)).astype(np.float32)
+    for pct in (99.99, 50.0, 3.0):
+        for sym in (1, 0):
+            g, o = Q.calibrate_percentile(x, pct, sym), O.calibrate_percentile(x, pct, sym)
+            assert _same_qp(g, o), (kind, pct, sym, g, o)
+
+
 @pytest.mark.parametrize("n", [1, 7, 1000, 65539, 786432])
 def test_calibrate_mse(hip, n):
     say(f"calibrate_mse n={n}")

@@ -49,7 +49,7 @@ constexpr int kMseChunk = 16;  // most candidates per pass: their scale / inv pa
 struct CalibState {
     double am, bw, mn, mx;  // max|x|, bin width; min / max (f64 locals)
     uint32_t prefix;        // radix select: bits of the k-th |x| found so far
-    uint32_t pad;
+    uint32_t spill;         // radix select: a workgroup's staged elements overflowed
     int64_t rank;           // radix select: rank within the current prefix
 };
 
@@ -323,6 +323,9 @@ __global__ __launch_bounds__(kKlCandBlock) void k_kl_candidate(
 // calibrate_percentile (engine.tkv:126-162)
 // ---------------------------------------------------------------------------
 
+// Elements a workgroup of the second radix pass stages for the third.
+constexpr int kPctStage = 2048;
+
 // One radix pass: the digit (bits(|x|) >> shift) & (2^bits - 1) counted over
 // the elements whose higher bits equal the prefix found so far (one LDS
 // histogram per block, kKlVec float4 per lane per trip), merged into the
@@ -330,55 +333,112 @@ __global__ __launch_bounds__(kKlCandBlock) void k_kl_candidate(
 // digit holding the element of the wanted rank (block prefix sum over the
 // 2048 digit counts, 8 per thread), records prefix and rank in st, clears
 // the histogram, and after the last pass writes the parameters.
+//   The second pass also stages the bits of every element it counts (those
+// whose top 11 bits match) in LDS and writes them to its own kPctStage-entry
+// region of `stage`, with their number in `staged`; the third pass then reads
+// only those, block for block on the same grid, instead of all of x.  A
+// workgroup with more than kPctStage of them sets st->spill, and the third
+// pass reads x as the others do (the first pass's last block clears it).
 __device__ __forceinline__ void radix_count(unsigned int* h, float xv, uint32_t prefix,
                                             uint32_t hi_mask, int shift, uint32_t dmask) {
     const uint32_t v = __float_as_uint(xv) & 0x7fffffffu;
     if (((v ^ prefix) & hi_mask) == 0) atomicAdd(&h[(v >> shift) & dmask], 1u);
 }
 
+__device__ __forceinline__ void radix_count_stage(unsigned int* h, uint32_t* stage,
+                                                  unsigned int* n_staged, float xv,
+                                                  uint32_t prefix, uint32_t hi_mask, int shift,
+                                                  uint32_t dmask) {
+    const uint32_t v = __float_as_uint(xv) & 0x7fffffffu;
+    if (((v ^ prefix) & hi_mask) == 0) {
+        atomicAdd(&h[(v >> shift) & dmask], 1u);
+        const unsigned int i = atomicAdd(n_staged, 1u);
+        if (i < (unsigned)kPctStage) stage[i] = v;
+    }
+}
+
+template <int PASS>  // 0, 1, 2
 __global__ __launch_bounds__(kCalBlock) void k_radix_pass(
-    const float* __restrict__ x, int64_t n, int vec, int shift, int bits, int first, int last,
-    int64_t rank0, int symmetric, int nparts, const RedPartial* __restrict__ partials,
-    CalibState* __restrict__ st, unsigned long long* __restrict__ hist,
-    unsigned* __restrict__ arrivals, tkv_hip_qparams_dev* __restrict__ out) {
+    const float* __restrict__ x, int64_t n, int vec, int64_t rank0, int symmetric, int nparts,
+    const RedPartial* __restrict__ partials, CalibState* __restrict__ st,
+    unsigned long long* __restrict__ hist, uint32_t* __restrict__ stage,
+    uint32_t* __restrict__ staged, unsigned* __restrict__ arrivals,
+    tkv_hip_qparams_dev* __restrict__ out) {
+    constexpr int shift = PASS == 0 ? 21 : (PASS == 1 ? 10 : 0);
+    constexpr int bits = PASS == 2 ? 10 : 11;
+    constexpr uint32_t hi_mask = (shift + bits >= 32) ? 0u : ~((1u << (shift + bits)) - 1u);
+    constexpr uint32_t dmask = (1u << bits) - 1u;
     __shared__ unsigned int s_h[kRadixBins];
+    __shared__ uint32_t s_stage[PASS == 1 ? kPctStage : 1];
+    __shared__ unsigned int s_nst;
     for (int i = threadIdx.x; i < kRadixBins; i += kCalBlock) s_h[i] = 0;
+    if (threadIdx.x == 0) s_nst = 0;
     __syncthreads();
-    const uint32_t hi_mask = (shift + bits >= 32) ? 0u : ~((1u << (shift + bits)) - 1u);
-    const uint32_t prefix = first ? 0u : st->prefix;
-    const uint32_t dmask = (1u << bits) - 1u;
+    const uint32_t prefix = PASS == 0 ? 0u : st->prefix;
     const int64_t stride = (int64_t)gridDim.x * kCalBlock;
     const int64_t tid = (int64_t)blockIdx.x * kCalBlock + threadIdx.x;
-    const int64_t n4 = vec ? n / 4 : 0;
-    const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
-    int64_t i = tid;
-    for (; i + (kKlVec - 1) * stride < n4; i += kKlVec * stride) {
-        float4 u[kKlVec];
+    auto count = [&](float v) {
+        if constexpr (PASS == 1)
+            radix_count_stage(s_h, s_stage, &s_nst, v, prefix, hi_mask, shift, dmask);
+        else
+            radix_count(s_h, v, prefix, hi_mask, shift, dmask);
+    };
+    // arrivals expected at the end: the whole grid, or in the third pass on
+    // staged elements only its first kStagedBlocks workgroups, each taking
+    // every kStagedBlocks-th region (a few elements each, typically: the
+    // others return at once, so the arrival adds do not pile up behind them)
+    unsigned int arriving = gridDim.x;
+    if (PASS == 2 && st->spill == 0) {
+        constexpr unsigned int kStagedBlocks = 64;
+        arriving = gridDim.x < kStagedBlocks ? gridDim.x : kStagedBlocks;
+        if (blockIdx.x >= arriving) return;
+        for (unsigned int g = blockIdx.x; g < gridDim.x; g += arriving) {
+            const uint32_t* __restrict__ mine = stage + (int64_t)g * kPctStage;
+            const unsigned int cnt = staged[g];
+            for (unsigned int i = threadIdx.x; i < cnt; i += kCalBlock)
+                radix_count(s_h, __uint_as_float(mine[i]), prefix, hi_mask, shift, dmask);
+        }
+    } else {
+        const int64_t n4 = vec ? n / 4 : 0;
+        const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x);
+        int64_t i = tid;
+        for (; i + (kKlVec - 1) * stride < n4; i += kKlVec * stride) {
+            float4 u[kKlVec];
 #pragma unroll
-        for (int k = 0; k < kKlVec; k++) u[k] = x4[i + k * stride];
+            for (int k = 0; k < kKlVec; k++) u[k] = x4[i + k * stride];
 #pragma unroll
-        for (int k = 0; k < kKlVec; k++) {
-            radix_count(s_h, u[k].x, prefix, hi_mask, shift, dmask);
-            radix_count(s_h, u[k].y, prefix, hi_mask, shift, dmask);
-            radix_count(s_h, u[k].z, prefix, hi_mask, shift, dmask);
-            radix_count(s_h, u[k].w, prefix, hi_mask, shift, dmask);
+            for (int k = 0; k < kKlVec; k++) {
+                count(u[k].x);
+                count(u[k].y);
+                count(u[k].z);
+                count(u[k].w);
+            }
+        }
+        for (; i < n4; i += stride) {
+            const float4 u = x4[i];
+            count(u.x);
+            count(u.y);
+            count(u.z);
+            count(u.w);
+        }
+        for (int64_t j = n4 * 4 + tid; j < n; j += stride) count(x[j]);
+    }
+    __syncthreads();
+    if constexpr (PASS == 1) {
+        const unsigned int cnt = s_nst;
+        const unsigned int keep = cnt < (unsigned)kPctStage ? cnt : (unsigned)kPctStage;
+        uint32_t* __restrict__ mine = stage + (int64_t)blockIdx.x * kPctStage;
+        for (unsigned int i = threadIdx.x; i < keep; i += kCalBlock) mine[i] = s_stage[i];
+        if (threadIdx.x == 0) {
+            staged[blockIdx.x] = cnt;
+            if (cnt > (unsigned)kPctStage) st->spill = 1;
         }
     }
-    for (; i < n4; i += stride) {
-        const float4 u = x4[i];
-        radix_count(s_h, u.x, prefix, hi_mask, shift, dmask);
-        radix_count(s_h, u.y, prefix, hi_mask, shift, dmask);
-        radix_count(s_h, u.z, prefix, hi_mask, shift, dmask);
-        radix_count(s_h, u.w, prefix, hi_mask, shift, dmask);
-    }
-    for (int64_t j = n4 * 4 + tid; j < n; j += stride)
-        radix_count(s_h, x[j], prefix, hi_mask, shift, dmask);
-    __syncthreads();
     for (int b = threadIdx.x; b < kRadixBins; b += kCalBlock) {
         const unsigned int c = s_h[b];
         if (c) atomicAdd(&hist[b], (unsigned long long)c);
     }
-    if (!arrive_last(arrivals, gridDim.x)) return;
+    if (!arrive_last(arrivals, arriving)) return;
 
     constexpr int kPer = kRadixBins / kCalBlock;
     __shared__ unsigned long long s_wsum[kCalBlock / 64];
@@ -402,7 +462,7 @@ __global__ __launch_bounds__(kCalBlock) void k_radix_pass(
         if (lane >= o) upto += v;
     }
     if (lane == 63) s_wsum[wave] = upto;
-    const int64_t rank = first ? rank0 : st->rank;
+    const int64_t rank = PASS == 0 ? rank0 : st->rank;
     __syncthreads();  // also: every thread has read st->rank before it is rewritten
     for (int w = 0; w < wave; w++) upto += s_wsum[w];
     const unsigned long long before = upto - sum;
@@ -420,7 +480,8 @@ __global__ __launch_bounds__(kCalBlock) void k_radix_pass(
         st->prefix = np;
         s_prefix = np;
     }
-    if (last) {
+    if (PASS == 0 && threadIdx.x == 0) st->spill = 0;
+    if constexpr (PASS == 2) {
         // clip = the selected |x| (>= 1e-8); symmetric, or the reference's
         // asymmetric loop: data[0] unclipped, every later value clipped, so
         // min = data[0] < clip(min x) ? ... with the first-minimum rule (the
@@ -664,21 +725,24 @@ int launch_calibrate_percentile(Ctx* c, const float* x, int64_t n, float percent
     TKV_RC_TRY(need_cal_scratch(c, "calibrate_percentile"));
     CalibState* st;
     void* rest;
-    TKV_RC_TRY(cal_workspace(c, 0, &st, &rest));
+    const int grid = (int)hist_grid(c, n);
+    TKV_RC_TRY(cal_workspace(c, (size_t)grid * (kPctStage + 1) * 4, &st, &rest));
+    uint32_t* staged = static_cast<uint32_t*>(rest);
+    uint32_t* stage = staged + grid;
     // the min / max partials only feed the asymmetric parameters
     int64_t nparts = 0;
     if (!symmetric) TKV_RC_TRY(launch_partials(c, x, n, 1, &nparts));
-    const int grid = (int)hist_grid(c, n);
     const int vec = aligned(x, 16) ? 1 : 0;
     const int64_t rank = percentile_rank(n, percentile);
-    const int shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
-    for (int r = 0; r < 3; r++) {
-        hipLaunchKernelGGL(k_radix_pass, dim3((unsigned)grid), dim3(kCalBlock), 0, c->stream, x,
-                           n, vec, shifts[r], widths[r], r == 0 ? 1 : 0, r == 2 ? 1 : 0, rank,
-                           symmetric ? 1 : 0, (int)nparts, c->partials, st, c->cal_hist,
-                           c->cal_arrivals + 2, out);
-        TKV_LAUNCH_CHECK();
-    }
+#define TKV_RADIX(PASS)                                                                          \
+    hipLaunchKernelGGL(k_radix_pass<PASS>, dim3((unsigned)grid), dim3(kCalBlock), 0, c->stream, \
+                       x, n, vec, rank, symmetric ? 1 : 0, (int)nparts, c->partials, st,        \
+                       c->cal_hist, stage, staged, c->cal_arrivals + 2, out);                   \
+    TKV_LAUNCH_CHECK()
+    TKV_RADIX(0);
+    TKV_RADIX(1);
+    TKV_RADIX(2);
+#undef TKV_RADIX
     return TKV_HIP_OK;
 }
 
