@@ -387,13 +387,14 @@ def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
         lambda xb: D.quantize_dynamic_int8_rowwise(ctx, xb, m, cols, q8, sc), 5 * n + 4 * m)
     out["quantize_fp8"] = timeit(lambda xb: D.quantize_fp8_e4m3(ctx, xb, n, q8), 5 * n)
     # heavier calibrators (engine.tkv:42-197); bytes = the passes over x they
-    # need: KL min/max + histogram, percentile 3 radix passes (+ min/max when
+    # need: KL min/max + histogram, percentile 2 radix passes over x (the
+    # third reads the elements the second staged; + min/max when
     # asymmetric), MSE min/max + one pass evaluating all 50 candidates (f64
     # ALU-bound)
     out["calibrate_kl"] = timeit(lambda xb: D.calibrate_kl(ctx, xb, n, p), 8 * n)
-    out["calibrate_percentile"] = timeit(lambda xb: D.calibrate_percentile(ctx, xb, n, p), 12 * n)
+    out["calibrate_percentile"] = timeit(lambda xb: D.calibrate_percentile(ctx, xb, n, p), 8 * n)
     out["calibrate_percentile_asym"] = timeit(
-        lambda xb: D.calibrate_percentile(ctx, xb, n, p, symmetric=0), 16 * n)
+        lambda xb: D.calibrate_percentile(ctx, xb, n, p, symmetric=0), 12 * n)
     out["calibrate_mse"] = timeit(lambda xb: D.calibrate_mse(ctx, xb, n, p), 8 * n)
     out["config"] = f"M={m} x {cols} f32 (config 2, largest)"
     for b in xs:
