@@ -1122,6 +1122,61 @@ def test_graph_capture_replays(hip):
     ctx.close()
 
 
+def test_graph_replays_calibrators(hip):
+    """calibrate_minmax (finalized by its last partials workgroup), KL,
+    percentile (symmetric, with the staged third radix pass, and asymmetric)
+    and MSE captured in one graph.  Each finishes in its last workgroup, on
+    arrival counters and a histogram that every call leaves zero, so replays
+    after new input values, eager calibrator calls on other data and
+    synchronizations give the eager results, which equal the oracle's."""
+    say("graph replays calibrators")
+    ctx = D.Context(0)
+    n = 8192 * 96
+    dx = D.DeviceBuffer.empty(ctx, n, np.float32)
+    ps = [D.params_buffer(ctx) for _ in range(5)]
+
+    def calib():
+        D.calibrate_minmax(ctx, dx, n, 1, ps[0])
+        D.calibrate_kl(ctx, dx, n, ps[1])
+        D.calibrate_percentile(ctx, dx, n, ps[2], 99.9, 1)
+        D.calibrate_percentile(ctx, dx, n, ps[3], 50.0, 0)
+        D.calibrate_mse(ctx, dx, n, ps[4], 20)
+
+    inputs = [O.add_outliers(_x(n, 80 + i, 1.0 + i), 0.001, 3, 4, 20.0) for i in range(3)]
+    want = []
+    for x in inputs:
+        dx.upload(x)
+        calib()
+        ctx.synchronize()
+        want.append([p.download().tobytes() for p in ps])
+    x = inputs[0]
+    dx.upload(x)
+    calib()
+    assert _same_qp(D.read_params(ps[0]), O.calibrate_minmax(x, 1))
+    assert _same_qp(D.read_params(ps[1]), O.calibrate_kl(x))
+    assert _same_qp(D.read_params(ps[2]), O.calibrate_percentile(x, 99.9, 1))
+    assert _same_qp(D.read_params(ps[3]), O.calibrate_percentile(x, 50.0, 0))
+    assert _same_qp(D.read_params(ps[4]), O.calibrate_mse(x, 20))
+
+    other = D.DeviceBuffer.from_host(ctx, _x(5000, 90, 1.0))
+    op = D.params_buffer(ctx)
+    with D.Graph(ctx) as g:
+        calib()
+    for rep in range(2):
+        for x, w in zip(inputs, want):
+            dx.upload(x)
+            D.calibrate_kl(ctx, other, 5000, op)
+            D.calibrate_percentile(ctx, other, 5000, op, 99.0, 1)
+            D.calibrate_minmax(ctx, other, 5000, 0, op)
+            ctx.synchronize()
+            for p in ps:
+                D.memset(ctx, p, 0, p.nbytes)
+            g.launch()
+            ctx.synchronize()
+            assert [p.download().tobytes() for p in ps] == w, rep
+    g.close()
+
+
 def test_graph_replays_single_pass_quantize(hip):
     """The single-pass calibrate + quantize (a 100 MB activation: one
     workgroup per CU and a grid barrier whose slots advance by one generation
