@@ -1020,12 +1020,15 @@ def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
     gemm_cfg(cfg)
     # zero points: both set; zpa = 0 (no W sums needed); zpw = 0 (no A sums);
     # both 0 (no pre-pass at all); zpw = 0 with |zpa| large enough for the f64
-    # correction path at K = 768
+    # correction path at K = 768.  M > 32 with few K slices per workgroup
+    # forms the row sums inside the GEMM; K = 3072 at M = 1024 takes the
+    # pre-pass.
     cases = [((37, 100, 200), (-3, 5, 7)), ((1024, 768, 768), (-3, 5, 7)),
              ((16, 2304, 768), (-3, 5, 7)), ((16, 768, 3072), (-3, 5, 7)),
              ((37, 100, 200), (0, 5, 7)), ((37, 100, 200), (-3, 0, 7)),
              ((1024, 768, 768), (0, 0, -2)), ((64, 96, 768), (30000, 0, 3)),
-             ((64, 96, 768), (0, -30000, 3))]
+             ((64, 96, 768), (0, -30000, 3)), ((1024, 768, 3072), (-3, 5, 7)),
+             ((1024, 768, 3072), (0, 5, 7))]
     for (m, n, k), (zpa, zpw, zpy) in cases:
         say(f"dev qlinear cfg={cfg} {m}x{n}x{k} zp={zpa},{zpw},{zpy}")
         a = RNG.integers(-128, 128, m * k).astype(np.int8)

@@ -324,7 +324,15 @@ struct EpiF8 {
 //        clamped.
 //   else: the same correction in f64, exact because the launcher keeps
 //        |zp| <= 2^15 and K < 2^17 (every term below 2^53).
-template <bool I32>
+//   SUMS: ra / cw come from the accumulators of PolicyI8Q (each wave's own
+//        per-lane partial sums of the fragments it multiplied, combined over
+//        the two k-halves and moved into the accumulator layout with lane
+//        shuffles at the tile's end) instead of a pre-pass; row_sums /
+//        col_sums are not read.
+__device__ __forceinline__ int32_t acc_int(const v16i& a, int r) { return a[r]; }
+__device__ __forceinline__ int32_t acc_int(const AccQ& a, int r) { return a.v[r]; }
+
+template <bool I32, bool SUMS = false>
 struct EpiQL {
     static constexpr bool kOut32 = false;  // int8 outputs: stored at the tile's end
     const int32_t* row_sums;  // [M]
@@ -354,6 +362,7 @@ struct EpiQL {
     template <class C>
     __device__ __forceinline__ Operands<C> load(int m0, int n0, int M, int N) const {
         Operands<C> o;
+        if constexpr (SUMS) return o;
         const int lane = threadIdx.x & 63, wave = wave_id();
         const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
 #pragma unroll
@@ -373,18 +382,47 @@ struct EpiQL {
         return o;
     }
 
+    // The row / column terms from PolicyI8Q's partial sums (SUMS).
+    template <class C, class P>
+    __device__ __forceinline__ Operands<C> from_sums(
+        const typename P::Acc (&acc)[C::TM][C::TN]) const {
+        Operands<C> o;
+        const int khalf = (threadIdx.x & 63) >> 5;
+#pragma unroll
+        for (int i = 0; i < C::TM; i++) {
+            const int part = acc[i][0].rs;
+            const int full = part + __shfl_xor(part, 32, 64);  // row (lane % 32), all of K
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int32_t ra = __shfl(full, acc_row(r, khalf), 64);
+                o.rt[i][r] = I32 ? (int32_t)((uint32_t)kzz - (uint32_t)zpw * (uint32_t)ra) : ra;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int part = acc[0][j].cs;
+            const int32_t cw = part + __shfl_xor(part, 32, 64);
+            o.ct[j] = I32 ? (int32_t)((uint32_t)zpa * (uint32_t)cw) : cw;
+        }
+        return o;
+    }
+
     template <class C, class P, class F>
     __device__ __forceinline__ void with_value(const typename P::Acc (&acc)[C::TM][C::TN],
                                                const Operands<C>& o_in, F&& f) const {
-        const Operands<C> o = o_in.pinned();
+        Operands<C> o;
+        if constexpr (SUMS)
+            o = from_sums<C, P>(acc);
+        else
+            o = o_in.pinned();
         if constexpr (I32) {
             // clamp(rint(p) + zpy) == clamp(rint(p), -128 - zpy, 127 - zpy) + zpy for an
             // integer zpy; the launcher takes this path only for a finite mult, so p
             // is never NaN
             const double lo = -128.0 - (double)zpy, hi = 127.0 - (double)zpy;
             f([&](int i, int j, int r) {
-                const int32_t a = (int32_t)((uint32_t)pin(acc[i][j][r]) + (uint32_t)o.rt[i][r] -
-                                            (uint32_t)o.ct[j]);
+                const int32_t a = (int32_t)((uint32_t)pin(acc_int(acc[i][j], r)) +
+                                            (uint32_t)o.rt[i][r] - (uint32_t)o.ct[j]);
                 double v = __builtin_rint((double)a * mult);
                 v = v < lo ? lo : (v > hi ? hi : v);
                 return (uint32_t)((int32_t)v + zpy);
@@ -393,7 +431,8 @@ struct EpiQL {
             const double kzz_d = (double)kzz, zpw_d = (double)zpw, zpa_d = (double)zpa;
             f([&](int i, int j, int r) {
                 const double row = kzz_d - zpw_d * (double)o.rt[i][r];
-                const double a = ((double)pin(acc[i][j][r]) + row) - zpa_d * (double)o.ct[j];
+                const double a =
+                    ((double)pin(acc_int(acc[i][j], r)) + row) - zpa_d * (double)o.ct[j];
                 double v = __builtin_rint(a * mult);
                 if (v != v) v = 0.0;
                 v = v + (double)zpy;
@@ -438,9 +477,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm(const uint8_t* __restrict__
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
-            for (int j = 0; j < C::TN; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+            for (int j = 0; j < C::TN; j++) P::zero(acc[i][j]);
         const auto eo = ep.template load<C>(m0, n0, M, N);
         mainloop<C, P>(A, W, M, N, ldk, m0, n0, smem, acc);
         const int vn = v + (int)gridDim.x;
@@ -584,9 +621,7 @@ __global__ __launch_bounds__(C::THREADS, C::MIN_WAVES_EU) void k_gemm_ws(const u
 #pragma unroll
             for (int i = 0; i < C::TM; i++)
 #pragma unroll
-                for (int j = 0; j < C::TN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+                for (int j = 0; j < C::TN; j++) P::zero(acc[i][j]);
             const auto eo = ep.template load<C>(m0, n0, M, N);
             for (int kt = 0; kt < nk; kt++, s++) {
                 const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
@@ -616,9 +651,7 @@ __global__ __launch_bounds__(C::THREADS, C::MIN_WAVES_EU) void k_gemm_ws(const u
 #pragma unroll
             for (int i = 0; i < C::TM; i++)
 #pragma unroll
-                for (int j = 0; j < C::TN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+                for (int j = 0; j < C::TN; j++) P::zero(acc[i][j]);
             const auto eo = ep.template load<C>(m0, n0, M, N);
             for (int kt = 0; kt < nk; kt++, s++) {
                 const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
@@ -965,11 +998,6 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
     auto small = [](int32_t v) { return v >= -32768 && v <= 32767; };
     if (!small(q.zpa) || !small(q.zpw))
         return set_error(TKV_HIP_UNSUPPORTED, "QLinearMatMul: input zero points beyond +-2^15");
-    void* sums;
-    TKV_RC_TRY(ctx_workspace(c, 8, (size_t)(m + n) * 4, &sums));
-    int32_t* ra = static_cast<int32_t*>(sums);
-    TKV_RC_TRY(launch_row_sums_i8(c, a, q.zpw != 0 ? m : 0, w, q.zpa != 0 ? n : 0, k, ra,
-                                  ra + m));
     const void *pa = a, *pw = w;
     int64_t ldk;
     TKV_RC_TRY(gemm::prepare_operands(c, &pa, &pw, m, n, k, &ldk));
@@ -977,7 +1005,29 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
     const int64_t bound = k * (128 + (int64_t)std::abs(q.zpa)) * (128 + (int64_t)std::abs(q.zpw));
     const auto* ua = static_cast<const uint8_t*>(pa);
     const auto* uw = static_cast<const uint8_t*>(pw);
-    if (bound < (1ll << 31) && std::isfinite(q.mult))
+    const bool i32 = bound < (1ll << 31) && std::isfinite(q.mult);
+    // Tiled kernels can form the sums themselves (PolicyI8Q): that costs
+    // ~0.3 us per 128-deep K slice a workgroup runs, against ~4.5-6 us for
+    // the pre-pass at M = 8192 (traces of both on one box: attn_out 15.0
+    // against 13.3 + 4.4 us; qkv, mlp_up and mlp_down, at 18-24 slices per
+    // workgroup, 1.5-3.4 us slower).  So they do it up to 12 slices.
+    const int64_t slices = ceil_div(gemm::tiles_of<gemm::Cfg2>(m, n), (int64_t)c->num_cus) *
+                           (ldk / gemm::kBK);
+    if (m > gemm::kGemvMaxM && slices <= 12) {
+        if (i32)
+            return gemm::launch_any<gemm::PolicyI8Q>(
+                c, ua, uw, m, n, ldk,
+                gemm::EpiQL<true, true>{nullptr, nullptr, q.zpa, q.zpw, q.zpy, kzz, q.mult}, y);
+        return gemm::launch_any<gemm::PolicyI8Q>(
+            c, ua, uw, m, n, ldk,
+            gemm::EpiQL<false, true>{nullptr, nullptr, q.zpa, q.zpw, q.zpy, kzz, q.mult}, y);
+    }
+    void* sums;
+    TKV_RC_TRY(ctx_workspace(c, 8, (size_t)(m + n) * 4, &sums));
+    int32_t* ra = static_cast<int32_t*>(sums);
+    TKV_RC_TRY(launch_row_sums_i8(c, a, q.zpw != 0 ? m : 0, w, q.zpa != 0 ? n : 0, k, ra,
+                                  ra + m));
+    if (i32)
         return gemm::launch_any<gemm::PolicyI8>(
             c, ua, uw, m, n, ldk, gemm::EpiQL<true>{ra, ra + m, q.zpa, q.zpw, q.zpy, kzz, q.mult},
             y);

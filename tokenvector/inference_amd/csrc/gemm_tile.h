@@ -299,6 +299,10 @@ __device__ __forceinline__ void mainloop(const uint8_t* __restrict__ A,
 // INT8: v_mfma_i32_32x32x32_i8, 16 K-bytes per lane per 32-K step.
 struct PolicyI8 {
     typedef v16i Acc;
+    __device__ __forceinline__ static void zero(Acc& a) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) a[r] = 0;
+    }
     // Fragments are read C::FRAG_DEPTH k-steps ahead of the MFMAs that use
     // them, with scheduling barriers between the groups: ds_read returns in
     // order, so each MFMA waits only for its own operands (lgkmcnt(n), n =
@@ -336,11 +340,76 @@ struct PolicyI8 {
     }
 };
 
+// PolicyI8 plus the operands' row sums, for QLinearMatMul's zero-point
+// corrections: every consumer wave adds the bytes of the A and W fragments it
+// holds anyway (v_dot4_i32_i8 against 0x01010101, exact) into per-lane
+// partial sums.  acc[i][0].rs: lane l's row a_row[i] (l % 32) over k-half
+// l / 32; acc[0][j].cs: likewise for column w_row[j].  Waves sharing rows or
+// columns repeat the sums, which keeps every wave's epilogue self-contained.
+struct AccQ {
+    v16i v;
+    int rs, cs;
+};
+
+__device__ __forceinline__ int byte_sum4(const v4i& f, int s) {
+    s = __builtin_amdgcn_sdot4(f.x, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(f.y, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(f.z, 0x01010101, s, false);
+    return __builtin_amdgcn_sdot4(f.w, 0x01010101, s, false);
+}
+
+struct PolicyI8Q {
+    typedef AccQ Acc;
+    __device__ __forceinline__ static void zero(Acc& a) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) a.v[r] = 0;
+        a.rs = 0;
+        a.cs = 0;
+    }
+    template <class C>
+    __device__ __forceinline__ static void slice(const uint8_t* sa, const uint8_t* sw,
+                                                 const int (&a_row)[C::TM],
+                                                 const int (&w_row)[C::TN], int khalf,
+                                                 Acc (&acc)[C::TM][C::TN]) {
+        constexpr int KS = C::BK / 32, D = C::FRAG_DEPTH;
+        v4i af[KS][C::TM], bf[KS][C::TN];
+        auto load = [&](int ks) {
+            const int ch = ks * 2 + khalf;
+#pragma unroll
+            for (int i = 0; i < C::TM; i++) af[ks][i] = lds_chunk<C>(sa, a_row[i], ch);
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) bf[ks][j] = lds_chunk<C>(sw, w_row[j], ch);
+        };
+#pragma unroll
+        for (int ks = 0; ks < D - 1 && ks < KS; ks++) load(ks);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks + D - 1 < KS) load(ks + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++)
+                    acc[i][j].v = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j],
+                                                                        acc[i][j].v, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < C::TM; i++) acc[i][0].rs = byte_sum4(af[ks][i], acc[i][0].rs);
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) acc[0][j].cs = byte_sum4(bf[ks][j], acc[0][j].cs);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
 // FP8 full rate: v_mfma_scale_f32_32x32x64_f8f6f4 (both operands e4m3,
 // E8M0 scales 2^0), 32 K-bytes per lane per 64-K step.  Hardware decode is
 // OCP e4m3fn and the dot product is accumulated at reduced precision.
 struct PolicyF8 {
     typedef v16f Acc;
+    __device__ __forceinline__ static void zero(Acc& a) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) a[r] = 0.0f;
+    }
     static constexpr float kAccScale = 1.0f;
     template <class C>
     __device__ __forceinline__ static void slice(const uint8_t* sa, const uint8_t* sw,
@@ -418,6 +487,10 @@ __device__ __forceinline__ uint32_t dec2_f16(uint32_t x) {
 // 2^-8 pre-scale on both operands.
 struct PolicyF16 {
     typedef v16f Acc;
+    __device__ __forceinline__ static void zero(Acc& a) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) a[r] = 0.0f;
+    }
     static constexpr float kAccScale = 65536.0f;
     template <class C>
     __device__ __forceinline__ static void slice(const uint8_t* sa, const uint8_t* sw,
