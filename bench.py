@@ -256,10 +256,11 @@ def bench_qlinear(ctx, D, m=M, reps=20):
     return out
 
 
-def bench_int4(ctx, D, O, ms=(1, 32, 8192), gs=128):
+def bench_int4(ctx, D, O, ms=(1, 32, 256, 8192), gs=128):
     """Grouped INT4 (int4.tkv) on the four GPT-2 shapes: the GEMM with f64
     accumulation (exact products; v_mfma_f64_16x16x4_f64, peak 78.6 TFLOP/s)
-    at decode and prefill batches, the symmetric weight quantizer, and GGUF
+    at decode, small-prefill (K split over workgroups) and prefill batches,
+    the symmetric weight quantizer, and GGUF
     Q8_0 decoding of the same weights.  Weights are quantized once, outside
     the timed launches; 12 layers' weights are cycled so decode batches stream
     them from HBM."""

@@ -161,11 +161,18 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
 # 2 <= M <= 32 with K % 32 == 0 takes the decode kernel (16-column workgroups,
 # K split over workgroups when the column blocks are few: (16, 200, 256) in 2,
 # (32, 130, 512) in 4, (17, 1000, 1024) in 3); M = 1 and (3, 50, 80, 16), whose
-# K % 32 != 0, take the per-column kernel.
+# K % 32 != 0, take the per-column kernel.  Larger M takes the 64 x 64 tile
+# kernel, with K split over workgroups when the tiles are few for the CUs (256
+# CUs): (70, 130, 256) in 2, (300, 768, 768) in 4, (128, 768, 3072) in 20 (the
+# last split shorter), (100, 60, 522, 18) in 4 with scalar loads (K % 8 != 0),
+# (1100, 1100, 256) in 2 with more tiles than CUs; (520, 1040, 128) has too few
+# slices and no split.
 GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 256, 64),
                (32, 130, 512, 128), (17, 1000, 1024, 128), (3, 50, 80, 16),
                (70, 130, 256, 64), (33, 2304, 768, 128), (300, 768, 768, 128),
-               (129, 768, 3072, 32)]
+               (129, 768, 3072, 32), (64, 768, 768, 128), (128, 768, 3072, 128),
+               (200, 100, 512, 32), (100, 60, 522, 18), (520, 1040, 128, 32),
+               (1100, 1100, 256, 32)]
 
 
 @pytest.mark.parametrize("m,n,k,gs", GEMM_SHAPES)
@@ -191,8 +198,9 @@ def test_int4_matmul(hip, m, n, k, gs):
 
 
 def test_int4_matmul_dyadic_exact_and_errors(hip):
-    """Dyadic inputs: every partial sum exact, so the GPU result is the
-    reference's bit for bit; then the ValueError / unsupported cases."""
+    """Dyadic inputs (K split in 2 over the tile kernel's workgroups): every
+    partial sum exact, so the GPU result is the reference's bit for bit; then
+    the ValueError / unsupported cases."""
     m, n, k, gs = 40, 72, 256, 32
     say("int4 matmul dyadic")
     a = (RNG.integers(-64, 64, m * k) / 16.0).astype(np.float32)

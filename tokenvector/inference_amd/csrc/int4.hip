@@ -198,11 +198,15 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // slice's MFMAs, so their latency overlaps the matrix work.  VEC: A rows and W
 // rows allow 16-byte / 4-byte loads (K % 8 == 0, aligned bases, no perm) and
 // every 8-element run of k lies in one group (gs % 8 == 0).
-template <bool PERM, bool VEC>
+//   SPLIT (few tiles for the CUs): workgroup z of the grid's third dimension
+// takes K range [z kchunk, (z + 1) kchunk) (kchunk a multiple of the slice)
+// and writes its f64 partial tile to part[z] ([gridDim.y * 64, gridDim.x *
+// 64], every element); k_int4_split_sum then adds the partials in z order.
+template <bool PERM, bool VEC, bool SPLIT = false>
 __global__ __launch_bounds__(256) void k_matmul_int4_f64(
     const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
     const float* __restrict__ bias, const int64_t* __restrict__ perm, float* __restrict__ Y,
-    int M, int N, int K, int gs) {
+    int M, int N, int K, int gs, int kchunk = 0, double* __restrict__ part = nullptr) {
     __shared__ double sA[kGBK][kGPitch];
     __shared__ double sW[kGBK][kGPitch];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -263,8 +267,10 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
             }
         }
     };
-    fetch(0);
-    for (int k0 = 0; k0 < K; k0 += kGBK) {
+    const int kbeg = SPLIT ? (int)blockIdx.z * kchunk : 0;
+    const int kend = SPLIT ? min(K, kbeg + kchunk) : K;
+    fetch(kbeg);
+    for (int k0 = kbeg; k0 < kend; k0 += kGBK) {
 #pragma unroll
         for (int i = 0; i < 8; i++) sA[sk + i][sr] = (double)ra[i];
 #pragma unroll
@@ -273,7 +279,7 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
             sW[sk + 2 * i + 1][sr] = (double)(((rb[i] >> 4) & 15) - 8) * (double)rs[2 * i + 1];
         }
         __syncthreads();
-        if (k0 + kGBK < K) fetch(k0 + kGBK);
+        if (k0 + kGBK < kend) fetch(k0 + kGBK);
 #pragma unroll
         for (int kk = 0; kk < kGBK; kk += 4) {
             const int kr = kk + (lane >> 4), l16 = lane & 15;
@@ -285,6 +291,22 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
             acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
         }
         __syncthreads();
+    }
+    if constexpr (SPLIT) {
+        const int64_t nt = (int64_t)gridDim.x * kGBN;
+        double* __restrict__ mine = part + (int64_t)blockIdx.z * gridDim.y * kGBM * nt;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int col = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = m0 + wm * 32 + i * 16 + (lane >> 4) + 4 * v;
+                    mine[(int64_t)row * nt + col] = acc[i][j][v];
+                }
+            }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -299,6 +321,25 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
                 if (row < M) Y[(int64_t)row * N + col] = (float)(acc[i][j][v] + b);
             }
         }
+}
+
+// y[row, col] = fl32((part[0] + part[1] + ... + part[S - 1]) + bias[col]),
+// the split partials added in split order (a fixed order: launches repeat
+// bit for bit).
+__global__ __launch_bounds__(256) void k_int4_split_sum(const double* __restrict__ part, int S,
+                                                         int64_t mt, int64_t nt,
+                                                         const float* __restrict__ bias,
+                                                         float* __restrict__ Y, int M, int N) {
+    const int64_t total = (int64_t)M * N;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int64_t row = e / N, col = e - row * N;
+        const double* __restrict__ p = part + row * nt + col;
+        double acc = p[0];
+        for (int s = 1; s < S; s++) acc = acc + p[(int64_t)s * mt * nt];
+        const double b = bias ? (double)bias[col] : 0.0;
+        Y[e] = (float)(acc + b);
+    }
 }
 
 // Decode batches (M <= MM <= kGemvRows, MM a power of two): one wave per
@@ -687,6 +728,63 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     }
     const dim3 grid((unsigned)((n + kGBN - 1) / kGBN), (unsigned)((m + kGBM - 1) / kGBM));
     const bool vec = !perm && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4);
+    // K split over workgroups (f64 partial tiles that k_int4_split_sum adds
+    // in split order), at least 4 slices per split.  The kernel holds 3
+    // workgroups per CU (132 VGPRs, 40 KB LDS) and one workgroup alone on a CU
+    // waits on its loads (2.0 us per slice against 0.85 us of MFMA work), so:
+    //  - at most one tile per CU: about 3 workgroups per CU, trimmed to a
+    //    whole number of workgroups per CU (288 workgroups on 256 CUs ran
+    //    mlp_down M = 64 in 27.3 us, 240 in 22.8 us);
+    //  - more tiles: the split count minimising rounds of 3 workgroups per CU
+    //    times slices per workgroup, +2% per split for the partial traffic.
+    // Sweep of forced split counts over the four GPT-2 shapes (group size
+    // 128, M = 33 .. 4096): this rule is within 1.5% of the best count on
+    // average; M = 64 mlp_down 188.9 -> 22.8 us, attn_out 48.6 -> 14.7 us,
+    // M = 1024 mlp_down 213.4 -> 120.3 us, M = 4096 unsplit (qkv, mlp_up).
+    const int64_t tiles = (int64_t)grid.x * grid.y, nslices = ceil_div(k, (int64_t)kGBK);
+    const int64_t ncu = c->num_cus, smax = nslices / 4;
+    const int64_t mt = (int64_t)grid.y * kGBM, nt = (int64_t)grid.x * kGBN;
+    int64_t splits = 1;
+    if (smax >= 2 && tiles <= ncu) {
+        splits = std::min(ceil_div(3 * ncu, tiles), smax);
+        if (tiles * splits > ncu) splits = std::min(splits, tiles * splits / ncu * ncu / tiles);
+    } else if (smax >= 2 && tiles < 16 * ncu) {
+        double best = 1e300;
+        for (int64_t s = 1; s <= std::min<int64_t>(smax, 16); s++) {
+            const int64_t q = ceil_div(nslices, s), s2 = ceil_div(nslices, q);
+            const double est = (double)ceil_div(tiles * s2, 3 * ncu) * (double)q * (1.0 + 0.02 * s2);
+            if (est < best) best = est, splits = s2;
+        }
+    }
+    // partial tiles beyond 256 MiB: fewer splits
+    while (splits >= 2 && splits * mt * nt * (int64_t)sizeof(double) > ((int64_t)256 << 20)) splits--;
+    if (splits >= 2) {
+        const int64_t kchunk = ceil_div(nslices, splits) * kGBK;
+        splits = ceil_div(k, kchunk);
+        void* part;
+        TKV_RC_TRY(ctx_workspace(c, 12, (size_t)(splits * mt * nt) * sizeof(double), &part));
+        double* dp = static_cast<double*>(part);
+        const dim3 sgrid(grid.x, grid.y, (unsigned)splits);
+        if (perm)
+            hipLaunchKernelGGL((k_matmul_int4_f64<true, false, true>), sgrid, dim3(256), 0,
+                               c->stream, a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k,
+                               (int)gs, (int)kchunk, dp);
+        else if (vec)
+            hipLaunchKernelGGL((k_matmul_int4_f64<false, true, true>), sgrid, dim3(256), 0,
+                               c->stream, a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k,
+                               (int)gs, (int)kchunk, dp);
+        else
+            hipLaunchKernelGGL((k_matmul_int4_f64<false, false, true>), sgrid, dim3(256), 0,
+                               c->stream, a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k,
+                               (int)gs, (int)kchunk, dp);
+        TKV_LAUNCH_CHECK();
+        int64_t rblocks = ceil_div(m * n, (int64_t)256);
+        if (rblocks > (int64_t)c->num_cus * 8) rblocks = (int64_t)c->num_cus * 8;
+        hipLaunchKernelGGL(k_int4_split_sum, dim3((unsigned)rblocks), dim3(256), 0, c->stream, dp,
+                           (int)splits, mt, nt, bias, y, (int)m, (int)n);
+        TKV_LAUNCH_CHECK();
+        return TKV_HIP_OK;
+    }
     if (perm)
         hipLaunchKernelGGL((k_matmul_int4_f64<true, false>), grid, dim3(256), 0, c->stream, a, wp,
                            scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);

@@ -80,7 +80,7 @@ struct Ctx {
     unsigned long long* cal_hist = nullptr;
     unsigned* cal_arrivals = nullptr;
     // grow-only workspaces
-    static constexpr int kSlots = 13;  // 10, 11: f16-decoded FP8 operands; 12: INT4 split partials
+    static constexpr int kSlots = 13;  // 10, 11: f16-decoded FP8 operands; 12: INT4 split-K partials (either kernel)
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
     bool capturing = false;  // between capture_begin and capture_end
