@@ -164,15 +164,17 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
 # K % 32 != 0, take the per-column kernel.  Larger M takes the 64 x 64 tile
 # kernel, with K split over workgroups when the tiles are few for the CUs (256
 # CUs): (70, 130, 256) in 2, (300, 768, 768) in 4, (128, 768, 3072) in 20 (the
-# last split shorter), (100, 60, 522, 18) in 4 with scalar loads (K % 8 != 0),
+# last split shorter), (100, 60, 522, 18) in 4 on the LDS form (K % 8 != 0),
 # (1100, 1100, 256) in 2 with more tiles than CUs; (520, 1040, 128) has too few
-# slices and no split.
+# slices and no split.  K % 32 != 0 on the register form: (90, 70, 200, 8)
+# unsplit and (100, 60, 520, 8) in 4, each ending in a part slice.  The
+# act-order form always takes the LDS form.
 GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 256, 64),
                (32, 130, 512, 128), (17, 1000, 1024, 128), (3, 50, 80, 16),
                (70, 130, 256, 64), (33, 2304, 768, 128), (300, 768, 768, 128),
                (129, 768, 3072, 32), (64, 768, 768, 128), (128, 768, 3072, 128),
                (200, 100, 512, 32), (100, 60, 522, 18), (520, 1040, 128, 32),
-               (1100, 1100, 256, 32)]
+               (1100, 1100, 256, 32), (90, 70, 200, 8), (100, 60, 520, 8)]
 
 
 @pytest.mark.parametrize("m,n,k,gs", GEMM_SHAPES)

@@ -194,15 +194,16 @@ __global__ __launch_bounds__(kI4Block) void k_permute_cols(const float* __restri
 constexpr int kGBM = 64, kGBN = 64, kGBK = 32, kGPitch = 80;
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-// The next slice's raw operands are loaded into registers before the current
-// slice's MFMAs, so their latency overlaps the matrix work.  VEC: A rows and W
-// rows allow 16-byte / 4-byte loads (K % 8 == 0, aligned bases, no perm) and
-// every 8-element run of k lies in one group (gs % 8 == 0).
+// This LDS form serves the act-order gather (PERM) and operands without
+// 16-byte rows (K % 8 != 0, gs % 8 != 0 or unaligned bases); the rest takes
+// k_matmul_int4_regs below.  The next slice's raw operands are loaded into
+// registers before the current slice's MFMAs, so their latency overlaps the
+// matrix work.
 //   SPLIT (few tiles for the CUs): workgroup z of the grid's third dimension
 // takes K range [z kchunk, (z + 1) kchunk) (kchunk a multiple of the slice)
 // and writes its f64 partial tile to part[z] ([gridDim.y * 64, gridDim.x *
 // 64], every element); k_int4_split_sum then adds the partials in z order.
-template <bool PERM, bool VEC, bool SPLIT = false>
+template <bool PERM, bool SPLIT = false>
 __global__ __launch_bounds__(256) void k_matmul_int4_f64(
     const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
     const float* __restrict__ bias, const int64_t* __restrict__ perm, float* __restrict__ Y,
@@ -225,46 +226,30 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
     int rb[4];
     auto fetch = [&](int k0) {
         const int kb = k0 + sk;
-        if (VEC && gm < M && kb + 7 < K) {
-            const float4* p = reinterpret_cast<const float4*>(A + (int64_t)gm * K + kb);
-            const float4 u = p[0], v = p[1];
-            ra[0] = u.x, ra[1] = u.y, ra[2] = u.z, ra[3] = u.w;
-            ra[4] = v.x, ra[5] = v.y, ra[6] = v.z, ra[7] = v.w;
-        } else {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int kk = kb + i;
-                float x = 0.0f;
-                if (gm < M && kk < K) {
-                    // a perm entry outside [0, K) reads 0 (the host mirror rejects it)
-                    const int64_t src_k = PERM ? perm[kk] : (int64_t)kk;
-                    if (src_k >= 0 && src_k < K) x = A[(int64_t)gm * K + src_k];
-                }
-                ra[i] = x;
+        for (int i = 0; i < 8; i++) {
+            const int kk = kb + i;
+            float x = 0.0f;
+            if (gm < M && kk < K) {
+                // a perm entry outside [0, K) reads 0 (the host mirror rejects it)
+                const int64_t src_k = PERM ? perm[kk] : (int64_t)kk;
+                if (src_k >= 0 && src_k < K) x = A[(int64_t)gm * K + src_k];
             }
+            ra[i] = x;
         }
-        if (VEC && gn < N && kb + 7 < K) {
-            const uint32_t w4 = *reinterpret_cast<const uint32_t*>(Wp + (int64_t)gn * half + kb / 2);
-            const float sc = scales[(int64_t)gn * ng + kb / gs];
 #pragma unroll
-            for (int i = 0; i < 4; i++) rb[i] = (int)(w4 >> (8 * i)) & 255;
-#pragma unroll
-            for (int i = 0; i < 8; i++) rs[i] = sc;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int kk = kb + 2 * i;  // even
-                int bb = 0x88;              // codes 8: w = 0
-                float s0 = 0.0f, s1 = 0.0f;
-                if (gn < N && kk < K) {
-                    bb = Wp[(int64_t)gn * half + kk / 2];
-                    s0 = scales[(int64_t)gn * ng + kk / gs];
-                    s1 = scales[(int64_t)gn * ng + (kk + 1) / gs];
-                }
-                rb[i] = bb;
-                rs[2 * i] = s0;
-                rs[2 * i + 1] = s1;
+        for (int i = 0; i < 4; i++) {
+            const int kk = kb + 2 * i;  // even
+            int bb = 0x88;              // codes 8: w = 0
+            float s0 = 0.0f, s1 = 0.0f;
+            if (gn < N && kk < K) {
+                bb = Wp[(int64_t)gn * half + kk / 2];
+                s0 = scales[(int64_t)gn * ng + kk / gs];
+                s1 = scales[(int64_t)gn * ng + (kk + 1) / gs];
             }
+            rb[i] = bb;
+            rs[2 * i] = s0;
+            rs[2 * i + 1] = s1;
         }
     };
     const int kbeg = SPLIT ? (int)blockIdx.z * kchunk : 0;
@@ -319,6 +304,139 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
             for (int v = 0; v < 4; v++) {
                 const int row = m0 + wm * 32 + i * 16 + (lane >> 4) + 4 * v;
                 if (row < M) Y[(int64_t)row * N + col] = (float)(acc[i][j][v] + b);
+            }
+        }
+}
+
+// Operands with 16-byte rows (K % 8 == 0, gs % 8 == 0, A 16-byte and W 4-byte
+// aligned, no perm), without LDS: each wave loads its own operands straight
+// into MFMA fragments, as the decode kernel does.  The MFMA's k index is free (both
+// operands agree on it), so in slice k0 lane l (row / column l % 16, quad
+// q = l / 16) owns k0 + 8 q .. k0 + 8 q + 7 and MFMA step s takes k0 + 8 q + s:
+// each lane reads two float4 of its A row and one 32-bit word of its W row
+// (8 nibbles, one group scale) per 16 x 16 block.  The products are the LDS
+// form's (x as f64 times (nibble - 8) * scale, exact); only the order of the
+// f64 additions differs.  No LDS and no barriers: the four waves of a 64 x 64
+// tile run independently, and the next slice's operands are loaded before the
+// current slice's 32 MFMAs.  Rows past M and columns past N read row M - 1 /
+// column N - 1 and are never stored; quads past the end of K read zeros.
+template <bool SPLIT>
+__global__ __launch_bounds__(256) void k_matmul_int4_regs(
+    const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
+    const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int gs,
+    int kchunk, double* __restrict__ part) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kGBM, n0 = blockIdx.x * kGBN;
+    const int l16 = lane & 15, q = lane >> 4;
+    const int half = K / 2, ng = K / gs;
+    const float* __restrict__ arow[2];
+    const uint8_t* __restrict__ wrow[2];
+    const float* __restrict__ srow[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = min(m0 + wm * 32 + i * 16 + l16, M - 1);
+        const int c = min(n0 + wn * 32 + i * 16 + l16, N - 1);
+        arow[i] = A + (int64_t)r * K;
+        wrow[i] = Wp + (int64_t)c * half;
+        srow[i] = scales + (int64_t)c * ng;
+    }
+    f64x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+    const int kbeg = SPLIT ? (int)blockIdx.z * kchunk : 0;
+    const int kend = SPLIT ? min(K, kbeg + kchunk) : K;
+    struct Buf {
+        float4 a[2][2];
+        uint32_t w[2];
+        float s[2];
+    };
+    // Loads are issued for every slice, the one past the end included, at
+    // addresses clamped into [kbeg, kend): a load under a branch would make
+    // the wait before the next MFMAs cover every load in flight (vmcnt counts
+    // in issue order), and the prefetch would be lost.  K % 8 == 0 and kend %
+    // 8 == 0, so a quad that starts inside [.., kend) ends inside it.
+    auto load = [&](Buf& b, int k0) {
+        const int kc = min(k0 + 8 * q, kend - 8);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const float4* p = reinterpret_cast<const float4*>(arow[i] + kc);
+            b.a[i][0] = p[0];
+            b.a[i][1] = p[1];
+            b.w[i] = *reinterpret_cast<const uint32_t*>(wrow[i] + kc / 2);
+            b.s[i] = srow[i][kc / gs];
+        }
+    };
+    // TAIL: the slice runs past kend (K % 32 != 0); quads starting at or past
+    // kend count zero
+    auto compute = [&](const Buf& b, bool tail, bool in) {
+        double sc[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) sc[i] = tail && !in ? 0.0 : (double)b.s[i];
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            double x[2], w[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const float4 v = b.a[i][st >> 2];
+                const float f = (st & 3) == 0 ? v.x : (st & 3) == 1 ? v.y : (st & 3) == 2 ? v.z : v.w;
+                x[i] = tail && !in ? 0.0 : (double)f;
+                w[i] = (double)((int)((b.w[i] >> (4 * st)) & 15) - 8) * sc[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(x[i], w[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    auto step = [&](const Buf& b, int k0) {
+        if (k0 + kGBK <= kend)
+            compute(b, false, true);
+        else
+            compute(b, true, k0 + 8 * q < kend);
+    };
+    Buf b0, b1;
+    load(b0, kbeg);
+    for (int k0 = kbeg;;) {
+        load(b1, k0 + kGBK);
+        step(b0, k0);
+        k0 += kGBK;
+        if (k0 >= kend) break;
+        load(b0, k0 + kGBK);
+        step(b1, k0);
+        k0 += kGBK;
+        if (k0 >= kend) break;
+    }
+    if constexpr (SPLIT) {
+        const int64_t nt = (int64_t)gridDim.x * kGBN;
+        double* __restrict__ mine = part + (int64_t)blockIdx.z * gridDim.y * kGBM * nt;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int col = n0 + wn * 32 + j * 16 + l16;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = m0 + wm * 32 + i * 16 + q + 4 * v;
+                    mine[(int64_t)row * nt + col] = acc[i][j][v];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + wn * 32 + j * 16 + l16;
+            if (col >= N) continue;
+            const double bb = bias ? (double)bias[col] : 0.0;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = m0 + wm * 32 + i * 16 + q + 4 * v;
+                if (row < M) Y[(int64_t)row * N + col] = (float)(acc[i][j][v] + bb);
             }
         }
 }
@@ -729,16 +847,17 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     const dim3 grid((unsigned)((n + kGBN - 1) / kGBN), (unsigned)((m + kGBM - 1) / kGBM));
     const bool vec = !perm && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4);
     // K split over workgroups (f64 partial tiles that k_int4_split_sum adds
-    // in split order), at least 4 slices per split.  The kernel holds 3
-    // workgroups per CU (132 VGPRs, 40 KB LDS) and one workgroup alone on a CU
-    // waits on its loads (2.0 us per slice against 0.85 us of MFMA work), so:
+    // in split order), at least 4 slices per split.  Both tile kernels hold 3
+    // workgroups per CU (LDS form 132 VGPRs and 40 KB LDS, register form 160
+    // VGPRs), and one workgroup alone on a CU waits on its loads (LDS form:
+    // 2.0 us per slice against 0.85 us of MFMA work), so:
     //  - at most one tile per CU: about 3 workgroups per CU, trimmed to a
     //    whole number of workgroups per CU (288 workgroups on 256 CUs ran
     //    mlp_down M = 64 in 27.3 us, 240 in 22.8 us);
     //  - more tiles: the split count minimising rounds of 3 workgroups per CU
     //    times slices per workgroup, +2% per split for the partial traffic.
     // Sweep of forced split counts over the four GPT-2 shapes (group size
-    // 128, M = 33 .. 4096): this rule is within 1.5% of the best count on
+    // 128, M = 33 .. 4096, LDS form): this rule is within 1.5% of the best count on
     // average; M = 64 mlp_down 188.9 -> 22.8 us, attn_out 48.6 -> 14.7 us,
     // M = 1024 mlp_down 213.4 -> 120.3 us, M = 4096 unsplit (qkv, mlp_up).
     const int64_t tiles = (int64_t)grid.x * grid.y, nslices = ceil_div(k, (int64_t)kGBK);
@@ -766,17 +885,16 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
         double* dp = static_cast<double*>(part);
         const dim3 sgrid(grid.x, grid.y, (unsigned)splits);
         if (perm)
-            hipLaunchKernelGGL((k_matmul_int4_f64<true, false, true>), sgrid, dim3(256), 0,
-                               c->stream, a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k,
-                               (int)gs, (int)kchunk, dp);
+            hipLaunchKernelGGL((k_matmul_int4_f64<true, true>), sgrid, dim3(256), 0, c->stream, a,
+                               wp, scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs,
+                               (int)kchunk, dp);
         else if (vec)
-            hipLaunchKernelGGL((k_matmul_int4_f64<false, true, true>), sgrid, dim3(256), 0,
-                               c->stream, a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k,
-                               (int)gs, (int)kchunk, dp);
+            hipLaunchKernelGGL((k_matmul_int4_regs<true>), sgrid, dim3(256), 0, c->stream, a, wp,
+                               scales, bias, y, (int)m, (int)n, (int)k, (int)gs, (int)kchunk, dp);
         else
-            hipLaunchKernelGGL((k_matmul_int4_f64<false, false, true>), sgrid, dim3(256), 0,
-                               c->stream, a, wp, scales, bias, perm, y, (int)m, (int)n, (int)k,
-                               (int)gs, (int)kchunk, dp);
+            hipLaunchKernelGGL((k_matmul_int4_f64<false, true>), sgrid, dim3(256), 0, c->stream, a,
+                               wp, scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs,
+                               (int)kchunk, dp);
         TKV_LAUNCH_CHECK();
         int64_t rblocks = ceil_div(m * n, (int64_t)256);
         if (rblocks > (int64_t)c->num_cus * 8) rblocks = (int64_t)c->num_cus * 8;
@@ -786,13 +904,13 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
         return TKV_HIP_OK;
     }
     if (perm)
-        hipLaunchKernelGGL((k_matmul_int4_f64<true, false>), grid, dim3(256), 0, c->stream, a, wp,
+        hipLaunchKernelGGL((k_matmul_int4_f64<true>), grid, dim3(256), 0, c->stream, a, wp,
                            scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
     else if (vec)
-        hipLaunchKernelGGL((k_matmul_int4_f64<false, true>), grid, dim3(256), 0, c->stream, a, wp,
-                           scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+        hipLaunchKernelGGL((k_matmul_int4_regs<false>), grid, dim3(256), 0, c->stream, a, wp,
+                           scales, bias, y, (int)m, (int)n, (int)k, (int)gs, 0, nullptr);
     else
-        hipLaunchKernelGGL((k_matmul_int4_f64<false, false>), grid, dim3(256), 0, c->stream, a, wp,
+        hipLaunchKernelGGL((k_matmul_int4_f64<false>), grid, dim3(256), 0, c->stream, a, wp,
                            scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
