@@ -4,7 +4,9 @@ against the CPU oracle on the same seeded inputs.
 
 Bar: codes, scales, zero points and dequantized values bit-exact.  The INT4
 GEMM accumulates in f64 with exact products, so it may differ from the
-reference's sequential sum only by the order of the additions:
+reference's sequential sum only by the order of the additions (and, where it
+applies each group's scale once to the group's sum of x (nibble - 8), by one
+fma rounding per group: gs + K / gs roundings in all, at most 2 K):
 |y - y_ref| <= 2 K 2^-53 sum_k |a_k w_k| + ulp(y_ref) per element, and
 bit-exact on dyadic inputs, where every partial sum is exact.
 """
@@ -166,9 +168,10 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
 # CUs): (70, 130, 256) in 2, (300, 768, 768) in 4, (128, 768, 3072) in 20 (the
 # last split shorter), (100, 60, 522, 18) in 4 on the LDS form (K % 8 != 0),
 # (1100, 1100, 256) in 2 with more tiles than CUs; (520, 1040, 128) has too few
-# slices and no split.  K % 32 != 0 on the register form: (90, 70, 200, 8)
-# unsplit and (100, 60, 520, 8) in 4, each ending in a part slice.  The
-# act-order form always takes the LDS form.
+# slices and no split (group scales applied per group: gs % 32 == 0).  K % 32
+# != 0 on the register form: (90, 70, 200, 8) unsplit and (100, 60, 520, 8) in
+# 4, each ending in a part slice.  The act-order form always takes the LDS
+# form.
 GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 256, 64),
                (32, 130, 512, 128), (17, 1000, 1024, 128), (3, 50, 80, 16),
                (70, 130, 256, 64), (33, 2304, 768, 128), (300, 768, 768, 128),
@@ -200,18 +203,19 @@ def test_int4_matmul(hip, m, n, k, gs):
 
 
 def test_int4_matmul_dyadic_exact_and_errors(hip):
-    """Dyadic inputs (K split in 2 over the tile kernel's workgroups): every
-    partial sum exact, so the GPU result is the reference's bit for bit; then
-    the ValueError / unsupported cases."""
-    m, n, k, gs = 40, 72, 256, 32
-    say("int4 matmul dyadic")
-    a = (RNG.integers(-64, 64, m * k) / 16.0).astype(np.float32)
-    pk = RNG.integers(0, 256, n * k // 2).astype(np.int32)
-    sc = (2.0 ** -RNG.integers(1, 6, n * k // gs)).astype(np.float32)
-    b = (RNG.integers(-8, 8, n) / 8.0).astype(np.float32)
-    y = np.zeros(m * n, np.float32)
-    I4.matmul_int4_grouped(a, pk, b, y, m, n, k, gs, sc)
-    assert np.array_equal(y, O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc))
+    """Dyadic inputs (40 x 72 x 256: K split in 2 over the tile kernel's
+    workgroups; 520 x 72 x 128: unsplit, group scales applied per group):
+    every partial sum exact, so the GPU result is the reference's bit for
+    bit; then the ValueError / unsupported cases."""
+    for m, n, k, gs in ((520, 72, 128, 32), (40, 72, 256, 32)):
+        say(f"int4 matmul dyadic {m}x{n}x{k}")
+        a = (RNG.integers(-64, 64, m * k) / 16.0).astype(np.float32)
+        pk = RNG.integers(0, 256, n * k // 2).astype(np.int32)
+        sc = (2.0 ** -RNG.integers(1, 6, n * k // gs)).astype(np.float32)
+        b = (RNG.integers(-8, 8, n) / 8.0).astype(np.float32)
+        y = np.zeros(m * n, np.float32)
+        I4.matmul_int4_grouped(a, pk, b, y, m, n, k, gs, sc)
+        assert np.array_equal(y, O.matmul_int4_grouped(a, pk, b, m, n, k, gs, sc))
     with pytest.raises(ValueError):
         I4.matmul_int4_grouped(a, pk, b, y, m, n, k, gs, sc[:-1])
     with pytest.raises(ValueError):

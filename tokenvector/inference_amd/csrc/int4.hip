@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void k_matmul_int4_f64(
 // tile run independently, and the next slice's operands are loaded before the
 // current slice's 32 MFMAs.  Rows past M and columns past N read row M - 1 /
 // column N - 1 and are never stored; quads past the end of K read zeros.
-template <bool SPLIT>
+template <bool SPLIT, bool FACT = false>
 __global__ __launch_bounds__(256) void k_matmul_int4_regs(
     const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
     const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int gs,
@@ -341,11 +341,11 @@ __global__ __launch_bounds__(256) void k_matmul_int4_regs(
         wrow[i] = Wp + (int64_t)c * half;
         srow[i] = scales + (int64_t)c * ng;
     }
-    f64x4 acc[2][2];
+    f64x4 acc[2][2], accg[2][2];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+        for (int j = 0; j < 2; j++) acc[i][j] = accg[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
     const int kbeg = SPLIT ? (int)blockIdx.z * kchunk : 0;
     const int kend = SPLIT ? min(K, kbeg + kchunk) : K;
     struct Buf {
@@ -371,6 +371,12 @@ __global__ __launch_bounds__(256) void k_matmul_int4_regs(
     };
     // TAIL: the slice runs past kend (K % 32 != 0); quads starting at or past
     // kend count zero
+    //   FACT (gs % 32 == 0: a slice lies in one group; unsplit launches
+    // only): the B operand is the
+    // nibble's integer value, the products x (nibble - 8) (exact) sum into
+    // accg over a group, and the group's end adds accg * scale into acc with
+    // one fma per output (in the D layout lane l holds column l % 16, whose
+    // scale this lane loaded): 16 f64 multiplies per slice fewer.
     auto compute = [&](const Buf& b, bool tail, bool in) {
         double sc[2];
 #pragma unroll
@@ -383,13 +389,30 @@ __global__ __launch_bounds__(256) void k_matmul_int4_regs(
                 const float4 v = b.a[i][st >> 2];
                 const float f = (st & 3) == 0 ? v.x : (st & 3) == 1 ? v.y : (st & 3) == 2 ? v.z : v.w;
                 x[i] = tail && !in ? 0.0 : (double)f;
-                w[i] = (double)((int)((b.w[i] >> (4 * st)) & 15) - 8) * sc[i];
+                const double d = (double)((int)((b.w[i] >> (4 * st)) & 15) - 8);
+                w[i] = FACT ? d : d * sc[i];
             }
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(x[i], w[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 2; j++) {
+                    if constexpr (FACT)
+                        accg[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(x[i], w[j], accg[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(x[i], w[j], acc[i][j], 0, 0, 0);
+                }
+        }
+    };
+    auto flush = [&](const Buf& b) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const double sc = (double)b.s[j];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[i][j][v] = __builtin_fma(accg[i][j][v], sc, acc[i][j][v]);
+                accg[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+            }
         }
     };
     auto step = [&](const Buf& b, int k0) {
@@ -397,6 +420,8 @@ __global__ __launch_bounds__(256) void k_matmul_int4_regs(
             compute(b, false, true);
         else
             compute(b, true, k0 + 8 * q < kend);
+        if constexpr (FACT)
+            if ((k0 + kGBK) % gs == 0 || k0 + kGBK >= kend) flush(b);
     };
     Buf b0, b1;
     load(b0, kbeg);
@@ -906,6 +931,13 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     if (perm)
         hipLaunchKernelGGL((k_matmul_int4_f64<true>), grid, dim3(256), 0, c->stream, a, wp,
                            scales, bias, perm, y, (int)m, (int)n, (int)k, (int)gs);
+    // The group-scaled form holds 32 more VGPRs (194: 2 workgroups per CU
+    // instead of 3); unsplit it measured 4-6% faster at M = 8192 (qkv 553.6
+    // -> 534.3, mlp_down 747.6 -> 704.3 us), split 1-3% slower, so only the
+    // unsplit launch takes it.
+    else if (vec && gs % 32 == 0)
+        hipLaunchKernelGGL((k_matmul_int4_regs<false, true>), grid, dim3(256), 0, c->stream, a, wp,
+                           scales, bias, y, (int)m, (int)n, (int)k, (int)gs, 0, nullptr);
     else if (vec)
         hipLaunchKernelGGL((k_matmul_int4_regs<false>), grid, dim3(256), 0, c->stream, a, wp,
                            scales, bias, y, (int)m, (int)n, (int)k, (int)gs, 0, nullptr);
