@@ -162,8 +162,11 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
 
 # 2 <= M <= 32 with K % 32 == 0 takes the decode kernel (16-column workgroups,
 # K split over workgroups when the column blocks are few: (16, 200, 256) in 2,
-# (32, 130, 512) in 4, (17, 1000, 1024) in 3); M = 1 and (3, 50, 80, 16), whose
-# K % 32 != 0, take the per-column kernel.  Larger M takes the 64 x 64 tile
+# (32, 130, 512) in 4, (17, 1000, 1024) in 3); M = 1 takes the single-row kernel
+# (one load step per 512 of K, at most 6 per trip: (1, 70, 3600, 8) runs two
+# trips, the second with 2 lanes of its second step inside K; (1, 33, 200, 8)
+# one part step), and (3, 50, 80, 16), whose K % 32 != 0, the per-column
+# kernel, as does every act-order form.  Larger M takes the 64 x 64 tile
 # kernel, with K split over workgroups when the tiles are few for the CUs (256
 # CUs): (70, 130, 256) in 2, (300, 768, 768) in 4, (128, 768, 3072) in 20 (the
 # last split shorter), (100, 60, 522, 18) in 4 on the LDS form (K % 8 != 0),
@@ -177,7 +180,8 @@ GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 25
                (70, 130, 256, 64), (33, 2304, 768, 128), (300, 768, 768, 128),
                (129, 768, 3072, 32), (64, 768, 768, 128), (128, 768, 3072, 128),
                (200, 100, 512, 32), (100, 60, 522, 18), (520, 1040, 128, 32),
-               (1100, 1100, 256, 32), (90, 70, 200, 8), (100, 60, 520, 8)]
+               (1100, 1100, 256, 32), (90, 70, 200, 8), (100, 60, 520, 8),
+               (1, 70, 3600, 8), (1, 33, 200, 8)]
 
 
 @pytest.mark.parametrize("m,n,k,gs", GEMM_SHAPES)

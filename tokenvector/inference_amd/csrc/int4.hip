@@ -546,6 +546,59 @@ __global__ __launch_bounds__(256) void k_gemv_int4_f64(
         }
 }
 
+// One row (decode at batch 1) with 16-byte rows (K % 8 == 0, gs % 8 == 0, A
+// 16-byte and W 4-byte aligned, no perm): one wave per column; at step u lane
+// l takes k = 512 u + 8 l .. + 7 (one 32-bit word of nibbles, one group scale,
+// two float4 of x), and kRowSteps = ceil(K / 512) steps (at most 6) are
+// loaded before any is used, so a column of up to 3072 weights costs one
+// memory round trip.  Lanes past K load the last 8-run again (no branch around
+// a load) and count zero.  Per lane the products are added in k order, then
+// the 64 lane sums pairwise.
+template <int kRowSteps>
+__global__ __launch_bounds__(256) void k_gemv_int4_row(
+    const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
+    const float* __restrict__ bias, float* __restrict__ Y, int N, int K, int gs) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;  // whole waves
+    const int half = K / 2, ng = K / gs;
+    const uint8_t* __restrict__ wr = Wp + (int64_t)n * half;
+    const float* __restrict__ sr = scales + (int64_t)n * ng;
+    double acc = 0.0;
+    for (int base = 0; base < K; base += 512 * kRowSteps) {
+        uint32_t w[kRowSteps];
+        float s[kRowSteps];
+        float4 x0[kRowSteps], x1[kRowSteps];
+        bool in[kRowSteps];
+#pragma unroll
+        for (int u = 0; u < kRowSteps; u++) {
+            const int kk = base + 512 * u + 8 * lane;
+            in[u] = kk < K;
+            const int kc = in[u] ? kk : K - 8;
+            w[u] = *reinterpret_cast<const uint32_t*>(wr + kc / 2);
+            s[u] = sr[kc / gs];
+            const float4* p = reinterpret_cast<const float4*>(A + kc);
+            x0[u] = p[0];
+            x1[u] = p[1];
+        }
+#pragma unroll
+        for (int u = 0; u < kRowSteps; u++) {
+            const double sc = (double)s[u];
+            const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w,
+                                 x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const double x = in[u] ? (double)xs[e] : 0.0;
+                const double wv = (double)((int)((w[u] >> (4 * e)) & 15) - 8) * sc;
+                acc = __builtin_fma(x, wv, acc);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc = acc + __shfl_xor(acc, o, 64);
+    if (lane == 0) Y[n] = (float)(acc + (bias ? (double)bias[n] : 0.0));
+}
+
 // Decode batches on the f64 MFMA (M <= 16 MB rows, K % 32 == 0, gs % 8 == 0,
 // no column permutation).  A workgroup of kDecWaves waves owns 16 output
 // columns and one of `splits` contiguous ranges of 32-deep k blocks; its waves
@@ -845,6 +898,29 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
             hipLaunchKernelGGL((k_gemv_int4_mfma<2>), dim3(grid), dim3(kDecWaves * 64), 0, c->stream, a,
                                wp, scales, bias, y, (int)m, (int)n, (int)k, (int)gs, (int)splits,
                                static_cast<double*>(part), c->gemv_arrivals);
+        TKV_LAUNCH_CHECK();
+        return TKV_HIP_OK;
+    }
+    // One row: one load step per 512 of K.  Against the per-column kernel
+    // below (us per call, GPT-2 shapes): mlp_down (K = 3072) 8.8 -> 4.3-4.5,
+    // the K = 768 shapes 4.5-5.4 -> 4.4-5.0.
+    if (m == 1 && !perm && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4)) {
+        const dim3 g((unsigned)((n + 3) / 4));
+        switch (std::min<int64_t>(ceil_div(k, (int64_t)512), 6)) {
+#define TKV_ROW(S)                                                                                 \
+    case S:                                                                                        \
+        hipLaunchKernelGGL(k_gemv_int4_row<S>, g, dim3(256), 0, c->stream, a, wp, scales, bias, y, \
+                           (int)n, (int)k, (int)gs);                                               \
+        break;
+            TKV_ROW(1)
+            TKV_ROW(2)
+            TKV_ROW(3)
+            TKV_ROW(4)
+            TKV_ROW(5)
+            default:
+            TKV_ROW(6)
+#undef TKV_ROW
+        }
         TKV_LAUNCH_CHECK();
         return TKV_HIP_OK;
     }
