@@ -206,6 +206,25 @@ def test_int4_matmul(hip, m, n, k, gs):
     assert np.all(np.abs(y.astype(np.float64) - ref) <= _gemm_bound(ap, pk, sc, b, m, n, k, gs, ref))
 
 
+def test_int4_matmul_k0(hip):
+    """K = 0 on every GEMM form (single row, decode, tile kernel, act-order):
+    y is the bias (or zero) broadcast over the rows."""
+    n, gs = 37, 8
+    b = O.gi_noise(n, 23, 0.01)
+    for m in (1, 5, 40, 100):
+        say(f"int4 matmul K=0 m={m}")
+        for bias in (b, None):
+            y = np.full(m * n, np.nan, np.float32)
+            I4.matmul_int4_grouped(np.zeros(0, np.float32), np.zeros(0, np.int32), bias, y, m, n,
+                                   0, gs, np.zeros(0, np.float32))
+            want = np.tile(bias if bias is not None else np.zeros(n, np.float32), m)
+            assert np.array_equal(y, want), m
+        y = np.full(m * n, np.nan, np.float32)
+        I4.matmul_int4_grouped_ordered(np.zeros(0, np.float32), np.zeros(0, np.int32), b, y, m, n,
+                                       0, gs, np.zeros(0, np.float32), np.zeros(0, np.int64))
+        assert np.array_equal(y, np.tile(b, m)), m
+
+
 def test_int4_matmul_dyadic_exact_and_errors(hip):
     """Dyadic inputs (40 x 72 x 256: K split in 2 over the tile kernel's
     workgroups; 520 x 72 x 128: unsplit, group scales applied per group):

@@ -424,16 +424,18 @@ __global__ __launch_bounds__(256) void k_matmul_int4_regs(
             if ((k0 + kGBK) % gs == 0 || k0 + kGBK >= kend) flush(b);
     };
     Buf b0, b1;
-    load(b0, kbeg);
-    for (int k0 = kbeg;;) {
-        load(b1, k0 + kGBK);
-        step(b0, k0);
-        k0 += kGBK;
-        if (k0 >= kend) break;
-        load(b0, k0 + kGBK);
-        step(b1, k0);
-        k0 += kGBK;
-        if (k0 >= kend) break;
+    if (kbeg < kend) {  // K = 0 loads nothing (the launcher also keeps it off this kernel)
+        load(b0, kbeg);
+        for (int k0 = kbeg;;) {
+            load(b1, k0 + kGBK);
+            step(b0, k0);
+            k0 += kGBK;
+            if (k0 >= kend) break;
+            load(b0, k0 + kGBK);
+            step(b1, k0);
+            k0 += kGBK;
+            if (k0 >= kend) break;
+        }
     }
     if constexpr (SPLIT) {
         const int64_t nt = (int64_t)gridDim.x * kGBN;
@@ -946,7 +948,7 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
 #undef TKV_GEMV
     }
     const dim3 grid((unsigned)((n + kGBN - 1) / kGBN), (unsigned)((m + kGBM - 1) / kGBM));
-    const bool vec = !perm && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4);
+    const bool vec = !perm && k > 0 && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4);
     // K split over workgroups (f64 partial tiles that k_int4_split_sum adds
     // in split order), at least 4 slices per split.  Both tile kernels hold 3
     // workgroups per CU (LDS form 132 VGPRs and 40 KB LDS, register form 160
