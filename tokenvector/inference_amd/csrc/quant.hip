@@ -179,6 +179,9 @@ int launch_partials(Ctx* c, const float* x, int64_t n, int track_zero, int64_t* 
 
 int launch_minmax_tensor(Ctx* c, const float* x, int64_t n, int mode, int recipe,
                          tkv_hip_qparams_dev* out) {
+    // the kernels read x[0] (the first-element NaN rule): an empty tensor is
+    // the callers' case (the host entry points return the identity params)
+    if (n <= 0 || !x) return set_error(TKV_HIP_BAD_ARG, "min/max of an empty or NULL tensor");
     // Only the asymmetric QuantParams expose the sign of a zero extreme.
     const int track_zero = (mode == MM_ASYMMETRIC) ? 1 : 0;
     if (c->cal_arrivals) {  // one kernel: its last block finalizes
