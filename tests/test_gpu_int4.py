@@ -160,9 +160,10 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
     return 2 * k * 2.0 ** -53 * s.reshape(-1) + np.spacing(np.abs(yref)).astype(np.float64)
 
 
-# 2 <= M <= 32 with K % 32 == 0 takes the decode kernel (16-column workgroups,
-# K split over workgroups when the column blocks are few: (16, 200, 256) in 2,
-# (32, 130, 512) in 4, (17, 1000, 1024) in 3); M = 1 takes the single-row kernel
+# 2 <= M <= 32 with K % 32 == 0 takes the decode kernel (16-column workgroups
+# of 8 waves, K split over workgroups when the column blocks are few and the k
+# blocks allow one per wave: (32, 130, 512) in 2, (17, 1000, 1024) in 3,
+# (16, 200, 256) unsplit); M = 1 takes the single-row kernel
 # (one load step per 512 of K, at most 6 per trip: (1, 70, 3600, 8) runs two
 # trips, the second with 2 lanes of its second step inside K; (1, 33, 200, 8)
 # one part step), and (3, 50, 80, 16), whose K % 32 != 0, the per-column

@@ -626,7 +626,12 @@ __global__ __launch_bounds__(256) void k_gemv_int4_row(
 // tile is in place before any load of it is issued.  A release add with an
 // acquire fence would instead write back and invalidate a whole L2 per
 // workgroup: measured at ~20 us per call over ~500 workgroups.
-constexpr int kDecWaves = 4;
+//   Each wave's k blocks are a chain of dependent MFMAs per row block, so
+// more waves per workgroup shorten every chain: 8 waves against 4 measured
+// 5-14% faster on the four GPT-2 shapes at M = 2 .. 32 (attn_out M = 32
+// 7.8 -> 6.7 us, mlp_down M = 32 13.5 -> 12.4 us); 12 waves tied with 8 and
+// 16 were slower (qkv M = 32 9.5 us).
+constexpr int kDecWaves = 8;
 
 template <int MB>
 __global__ __launch_bounds__(kDecWaves * 64) void k_gemv_int4_mfma(
