@@ -279,6 +279,81 @@ def test_int4_decode_gpt2_shapes(ctx, name, n, k, m):
         assert np.array_equal(dy.download(), y)
 
 
+def test_graph_replays_int4(ctx):
+    """matmul_int4_grouped on device buffers captured in one graph: M = 1
+    (single-row kernel), 32 (decode kernel, K split over workgroups with
+    arrival counts), 200 (tile kernel, K split + split sum) on a 768 x 3072
+    weight and 520 (tile kernel unsplit, group scales per group) on a 256 x
+    128 one.  Replays after new activations, with eager calls of other sizes
+    between them, give the eager results bit for bit; the eager results are
+    within the reordering bound of the oracle."""
+    say("graph replays int4")
+    cases = []
+    for (n, k, gs, ms, seed) in ((768, 3072, 128, (1, 32, 200), 61), (256, 128, 32, (520,), 63)):
+        w = _weights(n, k, seed)
+        pk, sc = O.quantize_int4_grouped(w, n, k, gs)
+        dw = D.DeviceBuffer.from_host(ctx, pk.astype(np.uint8))
+        ds = D.DeviceBuffer.from_host(ctx, sc)
+        b = O.gi_noise(n, seed + 5, 0.01)
+        db = D.DeviceBuffer.from_host(ctx, b)
+        for m in ms:
+            xs = [O.gi_noise(m * k, seed + 10 * i + m, 1.0) for i in range(2)]
+            cases.append((m, n, k, gs, pk, sc, b, dw, ds, db, xs,
+                          D.DeviceBuffer.empty(ctx, m * k, np.float32),
+                          D.DeviceBuffer.empty(ctx, (m, n), np.float32)))
+
+    def run():
+        for (m, n, k, gs, pk, sc, b, dw, ds, db, xs, dx, dy) in cases:
+            D.matmul_int4_grouped(ctx, dx, dw, ds, db, None, dy, m, n, k, gs)
+
+    want = []
+    for i in range(2):
+        for c in cases:
+            c[11].upload(c[10][i])
+        run()
+        ctx.synchronize()
+        want.append([c[12].download().tobytes() for c in cases])
+    for j, (m, n, k, gs, pk, sc, b, dw, ds, db, xs, dx, dy) in enumerate(cases):
+        if m * n * k > 10 ** 8:
+            continue
+        y = np.frombuffer(want[1][j], np.float32)
+        ref = O.matmul_int4_grouped(xs[1], pk, b, m, n, k, gs, sc)
+        assert np.all(np.abs(y.astype(np.float64) - ref) <= _gemm_bound(xs[1], pk, sc, b, m, n, k,
+                                                                          gs, ref)), m
+    # eager calls of other sizes on the same weights and workspaces
+    m0, n0, k0, gs0, _, _, _, dw0, ds0, db0 = cases[0][:10]
+    ox = D.DeviceBuffer.from_host(ctx, O.gi_noise(64 * k0, 99, 1.0))
+    oy = D.DeviceBuffer.empty(ctx, (64, n0), np.float32)
+    oy2 = D.DeviceBuffer.empty(ctx, (16, n0), np.float32)
+
+    def other():
+        D.matmul_int4_grouped(ctx, ox, dw0, ds0, db0, None, oy, 64, n0, k0, gs0)
+        D.matmul_int4_grouped(ctx, ox, dw0, ds0, None, None, oy2, 16, n0, k0, gs0)
+
+    other()
+    ctx.synchronize()
+    with D.Graph(ctx) as g:
+        run()
+    for rep in range(2):
+        for i in range(2):
+            for c in cases:
+                c[11].upload(c[10][i])
+            other()
+            ctx.synchronize()
+            for c in cases:
+                D.memset(ctx, c[12], 0, c[12].nbytes)
+            g.launch()
+            ctx.synchronize()
+            assert [c[12].download().tobytes() for c in cases] == want[i], (rep, i)
+    g.close()
+    bufs = {}
+    for c in cases:
+        for buf in c[7:10] + c[11:13]:
+            bufs[id(buf)] = buf
+    for buf in list(bufs.values()) + [ox, oy, oy2]:
+        buf.close()
+
+
 def test_int4_decode_dyadic_exact(hip):
     """Dyadic inputs through the decode kernel with a K split over
     workgroups: every partial sum is exact, so the result is the reference's
