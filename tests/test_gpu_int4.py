@@ -411,10 +411,18 @@ def test_gguf_blocks(ctx, dtype):
         want = O.dequantize_gguf(raw, n, dtype)
         assert _bits_equal(got, want), (dtype, n)
     n = nb * 32 - 5
+    want = O.dequantize_gguf(raw, n, dtype)
     dr = D.DeviceBuffer.from_host(ctx, raw)
     dy = D.DeviceBuffer.empty(ctx, n, np.float32)
-    D.dequantize_gguf(ctx, dr, n, dtype, dy)
-    assert _bits_equal(dy.download(), O.dequantize_gguf(raw, n, dtype))
+    D.dequantize_gguf(ctx, dr, n, dtype, dy)          # four outputs per thread
+    assert _bits_equal(dy.download(), want)
+    # blocks at an odd address, output not 16-byte aligned: one output per thread
+    dr1 = D.DeviceBuffer.from_host(ctx, np.concatenate([np.zeros(1, np.uint8), raw]))
+    dy1 = D.DeviceBuffer.empty(ctx, n + 1, np.float32)
+    D.dequantize_gguf(ctx, dr1.ptr + 1, n, dtype, dy1.ptr + 4)
+    assert _bits_equal(dy1.download()[1:], want)
+    for buf in (dr, dy, dr1, dy1):
+        buf.close()
     with pytest.raises(ValueError):
         G.dequant_blocks(raw[: step * 3].tobytes(), 0, 4 * 32, dtype)
     with pytest.raises(_lib.TkvHipError):

@@ -794,6 +794,58 @@ __global__ __launch_bounds__(kI4Block) void k_gguf_blocks(const uint8_t* __restr
     }
 }
 
+// Four outputs per thread and one float4 store (out 16-byte aligned); the
+// block's f16 scale and the four codes' bytes come as 16-bit loads: blocks
+// are 34 / 18 / 20 bytes, so with raw 2-byte aligned every scale, and every
+// run of 4 codes starting at a multiple of 4, sits on an even address.  The
+// per-element arithmetic is k_gguf_blocks'.  Elements past the last whole
+// block read 0 (a float4 group is either all inside the whole blocks or all
+// past them: both bounds are multiples of 4).
+__device__ __forceinline__ float half_u16(unsigned short h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kI4Block) void k_gguf_blocks4(const uint8_t* __restrict__ raw,
+                                                           int64_t n, float* __restrict__ out) {
+    constexpr int STEP = DT == 8 ? 34 : DT == 2 ? 18 : 20;
+    const int64_t full = n / 32 * 32, n4 = n / 4, stride = (int64_t)gridDim.x * kI4Block;
+    const int64_t tid = (int64_t)blockIdx.x * kI4Block + threadIdx.x;
+    for (int64_t t = tid; t < n4; t += stride) {
+        const int64_t i = 4 * t;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < full) {
+            const uint8_t* p = raw + (i / 32) * STEP;
+            const int j0 = (int)(i & 31);
+            const float d = half_u16(*reinterpret_cast<const unsigned short*>(p));
+            const int off = DT == 8 ? 2 + j0 : (DT == 2 ? 2 : 4) + (j0 & 15);
+            const unsigned c01 = *reinterpret_cast<const unsigned short*>(p + off);
+            const unsigned c23 = *reinterpret_cast<const unsigned short*>(p + off + 2);
+            const unsigned b[4] = {c01 & 255u, c01 >> 8, c23 & 255u, c23 >> 8};
+            float v[4];
+            if (DT == 8) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = d * (float)(int8_t)b[e];
+            } else if (DT == 2) {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    v[e] = d * (float)((int)(j0 < 16 ? (b[e] & 15u) : (b[e] >> 4)) - 8);
+            } else {
+                const double dm = (double)half_u16(*reinterpret_cast<const unsigned short*>(p + 2));
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const double dq = (double)d * (double)(j0 < 16 ? (b[e] & 15u) : (b[e] >> 4));
+                    v[e] = (float)(dq - dm);
+                }
+            }
+            o = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        reinterpret_cast<float4*>(out)[t] = o;
+    }
+    // the last n % 4 elements lie past the whole blocks (n % 4 <= n % 32)
+    for (int64_t j = n4 * 4 + tid; j < n; j += stride) out[j] = 0.0f;
+}
+
 unsigned grid_for(Ctx* c, int64_t work) {
     int64_t g = (work + kI4Block - 1) / kI4Block;
     const int64_t cap = (int64_t)c->num_cus * 8;
@@ -1033,6 +1085,29 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
 
 int launch_gguf_blocks(Ctx* c, const uint8_t* raw, int64_t n, int dtype, float* out) {
     if (n <= 0) return TKV_HIP_OK;
+    // four outputs per thread: 27.7 -> 23.0 us for 28.3 M Q8_0 elements
+    // (0.65 -> 0.78 of 8 TB/s)
+    if (aligned(raw, 2) && aligned(out, 16)) {
+        const unsigned g4 = grid_for(c, n / 4 > 0 ? n / 4 : 1);
+        switch (dtype) {
+            case 8:
+                hipLaunchKernelGGL(k_gguf_blocks4<8>, dim3(g4), dim3(kI4Block), 0, c->stream, raw, n,
+                                   out);
+                break;
+            case 2:
+                hipLaunchKernelGGL(k_gguf_blocks4<2>, dim3(g4), dim3(kI4Block), 0, c->stream, raw, n,
+                                   out);
+                break;
+            case 3:
+                hipLaunchKernelGGL(k_gguf_blocks4<3>, dim3(g4), dim3(kI4Block), 0, c->stream, raw, n,
+                                   out);
+                break;
+            default:
+                return set_error(TKV_HIP_UNSUPPORTED, "gguf: only Q8_0, Q4_0 and Q4_1 blocks");
+        }
+        TKV_LAUNCH_CHECK();
+        return TKV_HIP_OK;
+    }
     const unsigned g = grid_for(c, n);
     switch (dtype) {
         case 8:
