@@ -41,15 +41,25 @@ __device__ __forceinline__ int round_clamp(double v, int lo, int hi) {
 // group parameters (int4.tkv:22-33 symmetric, 96-147 asymmetric)
 // ---------------------------------------------------------------------------
 
-// One wave per group, groups grid-strided.  Symmetric: am = max |x| floored at
-// 1e-8, scale = fl32(am / 7) (NaN elements never compare greater).  Asym: mn /
-// mx in the reference's scan order, which is the NaN-ignoring min / max unless
-// the group's first element is NaN (then both stay NaN).
-template <bool ASYM>
-__global__ __launch_bounds__(kI4Block) void k_int4_group_params(
-    const float* __restrict__ src, int64_t rows, int64_t cols, int64_t gs, float* __restrict__ scales,
-    int64_t* __restrict__ zps) {
-    const int64_t ng = cols / gs, groups = rows * ng;
+// One wave per group, groups grid-strided: the group's parameters, then its
+// bytes.  Symmetric: am = max |x| floored at 1e-8, scale = fl32(am / 7) (NaN
+// elements never compare greater).  Asym: mn / mx in the reference's scan
+// order, which is the NaN-ignoring min / max unless the group's first element
+// is NaN (then both stay NaN).
+//   Bytes: one lane per column pair (c, c + 1), c even, coded with group
+// c / gs (for an odd group size the pair's second column may belong to the
+// next group; the reference codes it with this group's scale too), so the
+// wave of group g packs the pairs whose even column lies in it.  Symmetric:
+// q = clamp(round(x * (1.0 / scale)), -8, 7) + 8 with the f32 scale; asym:
+// mn = -zp * scale, q = clamp(round((x - mn) / scale), 0, 15).  OUT32 writes
+// the reference's int32-per-byte list.
+template <bool ASYM, bool OUT32>
+__global__ __launch_bounds__(kI4Block) void k_int4_quantize(const float* __restrict__ src,
+                                                            int64_t rows, int64_t cols, int64_t gs,
+                                                            float* __restrict__ scales,
+                                                            int64_t* __restrict__ zps,
+                                                            void* __restrict__ packed) {
+    const int64_t ng = cols / gs, groups = rows * ng, half = cols / 2;
     const int lane = threadIdx.x & 63;
     const int64_t waves = (int64_t)gridDim.x * (kI4Block / 64);
     for (int64_t q = (int64_t)blockIdx.x * (kI4Block / 64) + (threadIdx.x >> 6); q < groups;
@@ -75,65 +85,56 @@ __global__ __launch_bounds__(kI4Block) void k_int4_group_params(
                 a = fmaxf(a, __shfl_xor(a, o, 64));
             }
         }
-        if (lane != 0) continue;
+        // every lane holds the reduced values: each forms the parameters
+        float scf;
+        int zp = 8;
         if (!ASYM) {
             double am = (double)a;
             if (am < 0.00000001) am = 0.00000001;
-            scales[q] = (float)(am / 7.0);
-            continue;
-        }
-        double dmn = (double)mn, dmx = (double)mx;
-        if (x[0] != x[0]) dmn = dmx = (double)x[0];
-        if (dmx - dmn < 0.00000001) dmx = dmn + 0.00000001;
-        double sc = (dmx - dmn) / 15.0;
-        int zp = round_clamp(-dmn / sc, 0, 15);
-        if (zp == 0) {
-            if (dmn > 0) {
-                sc = dmx / 15.0;
-                if (sc < 0.00000001) sc = 0.00000001;
-                zp = 0;
-            }
-        } else if (zp == 15) {
-            sc = -dmn / 15.0;
-        }
-        if (sc < 0.00000001) sc = 0.00000001;
-        scales[q] = (float)sc;
-        zps[q] = zp;
-    }
-}
-
-// One lane per byte: columns (c, c + 1), c even, coded with group c / gs.
-// Symmetric: q = clamp(round(x * (1.0 / scale)), -8, 7) + 8.  Asym: mn =
-// -zp * scale, q = clamp(round((x - mn) / scale), 0, 15).  OUT32 writes the
-// reference's int32-per-byte list.
-template <bool ASYM, bool OUT32>
-__global__ __launch_bounds__(kI4Block) void k_int4_pack(const float* __restrict__ src,
-                                                        int64_t rows, int64_t cols, int64_t gs,
-                                                        const float* __restrict__ scales,
-                                                        const int64_t* __restrict__ zps,
-                                                        void* __restrict__ packed) {
-    const int64_t half = cols / 2, total = rows * half, ng = cols / gs;
-    const int64_t stride = (int64_t)gridDim.x * kI4Block;
-    for (int64_t i = (int64_t)blockIdx.x * kI4Block + threadIdx.x; i < total; i += stride) {
-        const int64_t r = i / half, c = (i - r * half) * 2;
-        const int64_t gi = r * ng + c / gs;
-        const double sc = (double)scales[gi];
-        const double x0 = (double)src[r * cols + c], x1 = (double)src[r * cols + c + 1];
-        int q0, q1;
-        if (ASYM) {
-            const double mn = (double)(-zps[gi]) * sc;
-            q0 = round_clamp((x0 - mn) / sc, 0, 15);
-            q1 = round_clamp((x1 - mn) / sc, 0, 15);
+            scf = (float)(am / 7.0);
         } else {
-            const double inv = 1.0 / sc;
-            q0 = round_clamp(x0 * inv, -8, 7) + 8;
-            q1 = round_clamp(x1 * inv, -8, 7) + 8;
+            double dmn = (double)mn, dmx = (double)mx;
+            if (x[0] != x[0]) dmn = dmx = (double)x[0];
+            if (dmx - dmn < 0.00000001) dmx = dmn + 0.00000001;
+            double sc = (dmx - dmn) / 15.0;
+            zp = round_clamp(-dmn / sc, 0, 15);
+            if (zp == 0) {
+                if (dmn > 0) {
+                    sc = dmx / 15.0;
+                    if (sc < 0.00000001) sc = 0.00000001;
+                    zp = 0;
+                }
+            } else if (zp == 15) {
+                sc = -dmn / 15.0;
+            }
+            if (sc < 0.00000001) sc = 0.00000001;
+            scf = (float)sc;
         }
-        const int b = (q1 << 4) | q0;
-        if (OUT32)
-            static_cast<int32_t*>(packed)[i] = b;
-        else
-            static_cast<uint8_t*>(packed)[i] = (uint8_t)b;
+        if (lane == 0) {
+            scales[q] = scf;
+            if (ASYM) zps[q] = zp;
+        }
+        const double sc = (double)scf;
+        const int64_t c_end = (g + 1) * gs;
+        for (int64_t c = ((g * gs + 1) & ~(int64_t)1) + 2 * lane; c < c_end; c += 128) {
+            const double x0 = (double)src[r * cols + c], x1 = (double)src[r * cols + c + 1];
+            int q0, q1;
+            if (ASYM) {
+                const double mnv = (double)(-zp) * sc;
+                q0 = round_clamp((x0 - mnv) / sc, 0, 15);
+                q1 = round_clamp((x1 - mnv) / sc, 0, 15);
+            } else {
+                const double inv = 1.0 / sc;
+                q0 = round_clamp(x0 * inv, -8, 7) + 8;
+                q1 = round_clamp(x1 * inv, -8, 7) + 8;
+            }
+            const int b = (q1 << 4) | q0;
+            const int64_t i = r * half + c / 2;
+            if (OUT32)
+                static_cast<int32_t*>(packed)[i] = b;
+            else
+                static_cast<uint8_t*>(packed)[i] = (uint8_t)b;
+        }
     }
 }
 
@@ -860,26 +861,18 @@ int launch_int4_quantize(Ctx* c, const float* src, int64_t rows, int64_t cols, i
     const int64_t groups = rows * (cols / gs);
     if (groups <= 0) return TKV_HIP_OK;
     const unsigned gg = grid_for(c, groups * 64);
-    if (asym)
-        hipLaunchKernelGGL(k_int4_group_params<true>, dim3(gg), dim3(kI4Block), 0, c->stream, src,
-                           rows, cols, gs, scales, zps);
-    else
-        hipLaunchKernelGGL(k_int4_group_params<false>, dim3(gg), dim3(kI4Block), 0, c->stream,
-                           src, rows, cols, gs, scales, zps);
-    TKV_LAUNCH_CHECK();
-    const unsigned gp = grid_for(c, rows * (cols / 2));
-#define TKV_PACK(AS, O32)                                                                    \
-    hipLaunchKernelGGL((k_int4_pack<AS, O32>), dim3(gp), dim3(kI4Block), 0, c->stream, src, \
+#define TKV_QUANT4(AS, O32)                                                                   \
+    hipLaunchKernelGGL((k_int4_quantize<AS, O32>), dim3(gg), dim3(kI4Block), 0, c->stream, src, \
                        rows, cols, gs, scales, zps, packed)
     if (asym && out32)
-        TKV_PACK(true, true);
+        TKV_QUANT4(true, true);
     else if (asym)
-        TKV_PACK(true, false);
+        TKV_QUANT4(true, false);
     else if (out32)
-        TKV_PACK(false, true);
+        TKV_QUANT4(false, true);
     else
-        TKV_PACK(false, false);
-#undef TKV_PACK
+        TKV_QUANT4(false, false);
+#undef TKV_QUANT4
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
