@@ -171,8 +171,9 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
 # kernel, with K split over workgroups when the tiles are few for the CUs (256
 # CUs): (70, 130, 256) in 2, (300, 768, 768) in 4, (128, 768, 3072) in 20 (the
 # last split shorter), (100, 60, 522, 18) in 4 on the LDS form (K % 8 != 0),
-# (1100, 1100, 256) in 2 with more tiles than CUs; (520, 1040, 128) has too few
-# slices and no split (group scales applied per group: gs % 32 == 0).  K % 32
+# (1100, 1100, 256, 16) in 2 with more tiles than CUs; (520, 1040, 128) has too
+# few slices and no split (group scales applied per group: gs % 32 == 0), nor
+# has a group-scaled launch with 8 tiles per slice of K or more.  K % 32
 # != 0 on the register form: (90, 70, 200, 8) unsplit and (100, 60, 520, 8) in
 # 4, each ending in a part slice.  The act-order form always takes the LDS
 # form.
@@ -181,7 +182,7 @@ GEMM_SHAPES = [(1, 100, 64, 32), (2, 64, 128, 32), (5, 37, 96, 32), (16, 200, 25
                (70, 130, 256, 64), (33, 2304, 768, 128), (300, 768, 768, 128),
                (129, 768, 3072, 32), (64, 768, 768, 128), (128, 768, 3072, 128),
                (200, 100, 512, 32), (100, 60, 522, 18), (520, 1040, 128, 32),
-               (1100, 1100, 256, 32), (90, 70, 200, 8), (100, 60, 520, 8),
+               (1100, 1100, 256, 16), (90, 70, 200, 8), (100, 60, 520, 8),
                (1, 70, 3600, 8), (1, 33, 200, 8)]
 
 

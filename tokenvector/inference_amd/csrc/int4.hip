@@ -1000,8 +1000,8 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     const dim3 grid((unsigned)((n + kGBN - 1) / kGBN), (unsigned)((m + kGBM - 1) / kGBM));
     const bool vec = !perm && k > 0 && k % 8 == 0 && gs % 8 == 0 && aligned(a, 16) && aligned(wp, 4);
     // K split over workgroups (f64 partial tiles that k_int4_split_sum adds
-    // in split order), at least 4 slices per split.  Both tile kernels hold 3
-    // workgroups per CU (LDS form 132 VGPRs and 40 KB LDS, register form 160
+    // in split order), at least 4 slices per split.  The split forms hold 3
+    // workgroups per CU (LDS form 132 VGPRs and 40 KB LDS, register form 138
     // VGPRs), and one workgroup alone on a CU waits on its loads (LDS form:
     // 2.0 us per slice against 0.85 us of MFMA work), so:
     //  - at most one tile per CU: about 3 workgroups per CU, trimmed to a
@@ -1010,14 +1010,26 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     //  - more tiles: the split count minimising rounds of 3 workgroups per CU
     //    times slices per workgroup, +2% per split for the partial traffic.
     // Sweep of forced split counts over the four GPT-2 shapes (group size
-    // 128, M = 33 .. 4096, LDS form): this rule is within 1.5% of the best count on
-    // average; M = 64 mlp_down 188.9 -> 22.8 us, attn_out 48.6 -> 14.7 us,
-    // M = 1024 mlp_down 213.4 -> 120.3 us, M = 4096 unsplit (qkv, mlp_up).
+    // 128, M = 33 .. 4096, LDS form): this rule is within 1.5% of the best
+    // count on average; M = 64 mlp_down 188.9 -> 22.8 us, attn_out 48.6 ->
+    // 14.7 us, M = 1024 mlp_down 213.4 -> 120.3 us.
+    //   The unsplit group-scaled register form is faster per slice than any
+    // split form, so with it a tile count of at least 8 per 32-wide slice of
+    // K stays unsplit, unless the tiles overflow the CUs by less than a
+    // quarter (then a few CUs would run two tiles while the rest idle).  The
+    // same sweep on the current kernels (M = 64 .. 4096) put this within 1.0%
+    // of the best count on average, 6.7% at worst (3.3% and 31% without it):
+    // qkv M = 768 74.0 -> 64.0 us, M = 3072 250.0 -> 214.5 us, mlp_up M = 256
+    // 40.2 -> 33.7 us; mlp_down (96 slices) splits up to 767 tiles.
     const int64_t tiles = (int64_t)grid.x * grid.y, nslices = ceil_div(k, (int64_t)kGBK);
     const int64_t ncu = c->num_cus, smax = nslices / 4;
     const int64_t mt = (int64_t)grid.y * kGBM, nt = (int64_t)grid.x * kGBN;
+    const bool fact = vec && gs % 32 == 0;
+    const bool fills = tiles <= ncu || tiles % ncu == 0 || tiles % ncu >= ncu / 4;
     int64_t splits = 1;
-    if (smax >= 2 && tiles <= ncu) {
+    if (fact && tiles >= 8 * nslices && fills) {
+        splits = 1;
+    } else if (smax >= 2 && tiles <= ncu) {
         splits = std::min(ceil_div(3 * ncu, tiles), smax);
         if (tiles * splits > ncu) splits = std::min(splits, tiles * splits / ncu * ncu / tiles);
     } else if (smax >= 2 && tiles < 16 * ncu) {
@@ -1063,7 +1075,7 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     // instead of 3); unsplit it measured 4-6% faster at M = 8192 (qkv 553.6
     // -> 534.3, mlp_down 747.6 -> 704.3 us), split 1-3% slower, so only the
     // unsplit launch takes it.
-    else if (vec && gs % 32 == 0)
+    else if (fact)
         hipLaunchKernelGGL((k_matmul_int4_regs<false, true>), grid, dim3(256), 0, c->stream, a, wp,
                            scales, bias, y, (int)m, (int)n, (int)k, (int)gs, 0, nullptr);
     else if (vec)
