@@ -1,23 +1,30 @@
 // int4.hip -- grouped INT4 weights (tv/quantization/int4.tkv) and the GGUF
 // block formats that feed quantized linears (tv/format/gguf.tkv:284-313).
 //
-//   group parameters   one wave per (row, group): max |x| (symmetric) or
-//                      min / max (AWQ-asym) by wave reduction, then the
-//                      reference's scalar f64 arithmetic for scale / zp.
-//   pack / unpack      one lane per byte (an even column and its neighbour),
+//   quantize           one wave per (row, group): max |x| (symmetric) or
+//                      min / max (AWQ-asym) by wave reduction, the
+//                      reference's scalar f64 arithmetic for scale / zp, then
+//                      the group's bytes (an even column and its neighbour,
 //                      the pair coded with the scale of group c / group_size
-//                      as in the reference.
+//                      as in the reference).  Unpack: one lane per byte.
 //   INT4 GEMM          y = fl32(sum_k x * ((nibble - 8) * scale) + bias) with
-//                      f64 accumulation on v_mfma_f64_16x16x4_f64 (decode
-//                      batches: one wave per column with f64 FMAs).  Every
-//                      product x * w is exact in f64 (24 + 4 + 24 bits), so the
-//                      result differs from the reference's sequential f64 sum
-//                      only by the order of the additions.
-//   GGUF blocks        one lane per output element; f16 scales through the
-//                      hardware conversion (exact for every finite code).
+//                      f64 accumulation on v_mfma_f64_16x16x4_f64: 64 x 64
+//                      tiles (operands straight into MFMA fragments, or
+//                      staged in LDS for the act-order gather), K split over
+//                      workgroups when the tiles are few; decode batches of
+//                      2-32 rows on 16-column MFMA workgroups; one row with
+//                      one wave per column.  Every product x * w is exact in
+//                      f64 (24 + 4 + 24 bits), so the result differs from the
+//                      reference's sequential f64 sum only by the order of
+//                      the additions (and, where the group scale is applied
+//                      once per group, one fma rounding per group).
+//   GGUF blocks        four outputs per lane (one per lane for unaligned
+//                      buffers); f16 scales through the hardware conversion
+//                      (exact for every finite code).
 //
 // Codes are packed bytes on the device ([rows, cols / 2], low nibble = even
 // column); the host mirrors move the reference's int32-per-byte lists.
+#include <algorithm>
 #include <cstdlib>
 
 #include "tkv_device.h"
