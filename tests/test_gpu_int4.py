@@ -162,7 +162,7 @@ def _gemm_bound(a, pk, sc, bias, m, n, k, gs, yref):
 
 # 2 <= M <= 32 with K % 32 == 0 takes the decode kernel (16-column workgroups
 # of 8 waves, K split over workgroups when the column blocks are few and the k
-# blocks allow one per wave: (32, 130, 512) in 2, (17, 1000, 1024) in 3,
+# blocks allow one per wave: (32, 130, 512) in 2, (17, 1000, 1024) in 4,
 # (16, 200, 256) unsplit); M = 1 takes the single-row kernel
 # (one load step per 512 of K, at most 6 per trip: (1, 70, 3600, 8) runs two
 # trips, the second with 2 lanes of its second step inside K; (1, 33, 200, 8)

@@ -927,20 +927,22 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
         (m + kGBM - 1) / kGBM > 65535)
         return set_error(TKV_HIP_UNSUPPORTED, "matmul_int4_grouped: sizes beyond the grid");
     // Decode batches of 2..32 rows: 16-column workgroups on the f64 MFMA, K
-    // split over workgroups until the grid is about half the CUs (one
-    // counter per column block).  A single row keeps the per-column kernel.
-    // Sweep over the four GPT-2 shapes (us per call, HIP events, M = 1 / 4 /
-    // 16 / 32, per-column kernel first): qkv 4.6 / 8.2 / 21.7 / 40.4 against
-    // 6.3 / 6.5 / 7.2 / 10.3, mlp_down 8.7 / 20.0 / 55.6 / 108.4 against
-    // 9.2 / 9.3 / 10.0 / 13.9; a grid of about half the CUs was best for the
-    // N = 768 shapes (attn_out M = 32: 7.9 us against 10.1 / 12.4 us with
-    // twice / four times the workgroups).
+    // split over workgroups until the grid is about three quarters of the
+    // CUs, at least one k block per wave (one counter per column block).  A
+    // single row takes the single-row kernel below.  Sweep over the four
+    // GPT-2 shapes (us per call, HIP events, M = 1 / 4 / 16 / 32, per-column
+    // kernel first): qkv 4.6 / 8.2 / 21.7 / 40.4 against 6.3 / 6.5 / 7.2 /
+    // 10.3, mlp_down 8.7 / 20.0 / 55.6 / 108.4 against 9.2 / 9.3 / 10.0 /
+    // 13.9 (4-wave workgroups).  With 8-wave workgroups, forced split counts
+    // on mlp_down (48 column blocks) at M = 4 / 16 / 32: 4 splits 7.9 / 8.4 /
+    // 11.1 us against 8.5 / 8.9 / 12.2 with 3, 9.6 / 10.2 / 13.0 with 8;
+    // attn_out (24 k blocks) is capped at 3.
     if (m >= 2 && m <= kGemvRows && !perm && k % 32 == 0 && gs % 8 == 0 && aligned(a, 16) &&
         aligned(wp, 4) && !getenv("TKV_INT4_GEMV_WAVE")) {
         const int64_t ncb = (n + 15) / 16, nkb = k / 32;
         int64_t splits = 1;
         if (ncb <= kGemvSplitBlocks && 2 * ncb < (int64_t)c->num_cus) {
-            splits = ceil_div((int64_t)c->num_cus, 2 * ncb);
+            splits = ceil_div(3 * (int64_t)c->num_cus, 4 * ncb);
             if (splits > nkb / kDecWaves) splits = nkb / kDecWaves;
             if (splits < 1) splits = 1;
         }
