@@ -52,7 +52,7 @@ SECTIONS = ("step", "quant", "fp8", "decode", "qlinear", "int4")
 
 
 def run_gpu(steps, warmup, sections=SECTIONS):
-    import oracle as O
+    from tokenvector.inference_amd import synthetic as G
     from tokenvector.inference_amd import _lib
     from tokenvector.inference_amd import device as D
 
@@ -61,11 +61,11 @@ def run_gpu(steps, warmup, sections=SECTIONS):
     ctx = D.Context(0)
     r = {}
     if "step" in sections:
-        r.update(bench_step(ctx, D, O, steps, warmup))
-    for name, fn in (("quant", lambda: bench_quant(ctx, D, O)), ("fp8", lambda: bench_fp8(ctx, D, O)),
-                     ("decode", lambda: bench_decode(ctx, D, O)),
+        r.update(bench_step(ctx, D, G, steps, warmup))
+    for name, fn in (("quant", lambda: bench_quant(ctx, D, G)), ("fp8", lambda: bench_fp8(ctx, D, G)),
+                     ("decode", lambda: bench_decode(ctx, D, G)),
                      ("qlinear", lambda: bench_qlinear(ctx, D)),
-                     ("int4", lambda: bench_int4(ctx, D, O))):
+                     ("int4", lambda: bench_int4(ctx, D, G))):
         if name in sections:
             log(f"bench section {name}")
             r[name] = fn()
@@ -73,17 +73,17 @@ def run_gpu(steps, warmup, sections=SECTIONS):
     return r
 
 
-def bench_step(ctx, D, O, steps, warmup):
+def bench_step(ctx, D, G, steps, warmup):
     """the timed W8A8 step over all 48 GPT-2 linears."""
     # ---- inputs (generated on the host once, resident in HBM) ----
     t0 = time.time()
-    x_host = {768: O.gi_noise(M * 768, 0, 1.0), 3072: O.gi_noise(M * 3072, 7, 1.0)}
+    x_host = {768: G.gi_noise(M * 768, 0, 1.0), 3072: G.gi_noise(M * 3072, 7, 1.0)}
     layers = []
     for l in range(LAYERS):
         lin = []
         for j, (name, n, k) in enumerate(SHAPES):
-            w = O.gi_noise(n * k, 10 + 100 * l + j + 1, 0.02)
-            b = O.gi_noise(n, 10 + 100 * l + j + 51, 0.01)
+            w = G.gi_noise(n * k, 10 + 100 * l + j + 1, 0.02)
+            b = G.gi_noise(n, 10 + 100 * l + j + 51, 0.01)
             dw = D.DeviceBuffer.from_host(ctx, w)
             db = D.DeviceBuffer.from_host(ctx, b)
             q = D.QuantizedLinear.from_float(ctx, dw, n, k, db, D.WEIGHT_INT8)
@@ -186,7 +186,7 @@ def _time_us(ctx, D, fn, reps):
     return e0.elapsed_ms(e1) * 1e3 / reps
 
 
-def bench_fp8(ctx, D, O, ms=(2048, 8192, 32768), reps=10):
+def bench_fp8(ctx, D, G, ms=(2048, 8192, 32768), reps=10):
     """FP8-e4m3 W8A8 GEMM on the four GPT-2 shapes.  Activations are
     per-tensor scaled into e4m3 and weights per-channel (both outside the
     timed launches); the timed launch is the GEMM with the per-token /
@@ -194,12 +194,12 @@ def bench_fp8(ctx, D, O, ms=(2048, 8192, 32768), reps=10):
     for the reference-products path.  Two input sets are cycled."""
     out = {}
     for (name, n, k) in SHAPES:
-        w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 21, 0.02))
-        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 22, 0.01))
+        w = D.DeviceBuffer.from_host(ctx, G.gi_noise(n * k, 21, 0.02))
+        b = D.DeviceBuffer.from_host(ctx, G.gi_noise(n, 22, 0.01))
         lin = D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_FP8_FAST)
         w.close()
         for m in ms:
-            xh = O.gi_noise(m * k, 23, 1.0)
+            xh = G.gi_noise(m * k, 23, 1.0)
             sets = []
             for _ in range(2):
                 dx = D.DeviceBuffer.from_host(ctx, xh)
@@ -256,7 +256,7 @@ def bench_qlinear(ctx, D, m=M, reps=20):
     return out
 
 
-def bench_int4(ctx, D, O, ms=(1, 32, 256, 8192), gs=128):
+def bench_int4(ctx, D, G, ms=(1, 32, 256, 8192), gs=128):
     """Grouped INT4 (int4.tkv) on the four GPT-2 shapes: the GEMM with f64
     accumulation (exact products; v_mfma_f64_16x16x4_f64, peak 78.6 TFLOP/s)
     at decode, small-prefill (K split over workgroups) and prefill batches,
@@ -268,14 +268,14 @@ def bench_int4(ctx, D, O, ms=(1, 32, 256, 8192), gs=128):
     for (name, n, k) in SHAPES:
         ws = []
         for l in range(LAYERS):
-            w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 500 + l, 0.02))
+            w = D.DeviceBuffer.from_host(ctx, G.gi_noise(n * k, 500 + l, 0.02))
             pk = D.DeviceBuffer.empty(ctx, n * k // 2, np.uint8)
             sc = D.DeviceBuffer.empty(ctx, n * k // gs, np.float32)
             D.quantize_int4_grouped(ctx, w, n, k, gs, pk, sc)
             ws.append((w, pk, sc))
-        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 600, 0.01))
+        b = D.DeviceBuffer.from_host(ctx, G.gi_noise(n, 600, 0.01))
         for m in ms:
-            dx = D.DeviceBuffer.from_host(ctx, O.gi_noise(m * k, 601, 1.0))
+            dx = D.DeviceBuffer.from_host(ctx, G.gi_noise(m * k, 601, 1.0))
             dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
             reps = 5 if m > 1024 else 30
             us = _time_us(ctx, D, lambda i: D.matmul_int4_grouped(
@@ -315,7 +315,7 @@ def bench_int4(ctx, D, O, ms=(1, 32, 256, 8192), gs=128):
     return out
 
 
-def bench_decode(ctx, D, O, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
+def bench_decode(ctx, D, G, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
     """decode batches, INT8 weights pre-quantized per channel,
     activations quantized per token inside the timed call
     (tkv_hip_linear_forward, ACT_PER_TOKEN: one kernel for M <= 32).
@@ -325,15 +325,15 @@ def bench_decode(ctx, D, O, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
     shapes = [("qkv", 2304, 768), ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)]
     out = {}
     for (name, n, k) in shapes:
-        w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 300, 0.02))
-        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 400, 0.01))
+        w = D.DeviceBuffer.from_host(ctx, G.gi_noise(n * k, 300, 0.02))
+        b = D.DeviceBuffer.from_host(ctx, G.gi_noise(n, 400, 0.01))
         base = D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_INT8)
         w.close()
         nsets = max(2, -(-cold_bytes // (n * k)))
         lins = [base] + [D.QuantizedLinear.from_int8(ctx, base.codes, base.scales, n, k, b)
                          for _ in range(nsets - 1)]
         for m in ms:
-            dx = D.DeviceBuffer.from_host(ctx, O.gi_noise(m * k, 24, 1.0))
+            dx = D.DeviceBuffer.from_host(ctx, G.gi_noise(m * k, 24, 1.0))
             dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
             cold = _time_us(ctx, D, lambda i: lins[i % nsets].forward(dx, m, dy, D.ACT_PER_TOKEN),
                             nsets)
@@ -355,9 +355,9 @@ def bench_decode(ctx, D, O, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
     return out
 
 
-def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
+def bench_quant(ctx, D, G, m=65536, cols=768, reps=20):
     n = m * cols
-    x = O.add_outliers(O.gi_noise(n, 0, 1.0), 0.001, 3, 4, 20.0)
+    x = G.add_outliers(G.gi_noise(n, 0, 1.0), 0.001, 3, 4, 20.0)
     # distinct buffers per repetition keep the Infinity Cache cold
     nbuf = 4
     xs = [D.DeviceBuffer.from_host(ctx, x) for _ in range(nbuf)]
@@ -400,11 +400,11 @@ def bench_quant(ctx, D, O, m=65536, cols=768, reps=20):
     out["config"] = f"M={m} x {cols} f32 (config 2, largest)"
     for b in xs:
         b.close()
-    out["activations"] = bench_act_quant(ctx, D, O)
+    out["activations"] = bench_act_quant(ctx, D, G)
     return out
 
 
-def bench_act_quant(ctx, D, O, reps=24):
+def bench_act_quant(ctx, D, G, reps=24):
     """Per-tensor calibrate + quantize of the step's activations (configs[2]:
     8192 x 768 for qkv / attn_out / mlp_up, 8192 x 3072 for mlp_down).
     `cold` rotates distinct inputs totalling more than the 256 MB Infinity
@@ -416,7 +416,7 @@ def bench_act_quant(ctx, D, O, reps=24):
     out = {}
     for rows, cols in ((8192, 768), (8192, 3072)):
         n = rows * cols
-        x = O.add_outliers(O.gi_noise(n, 3, 1.0), 0.001, 3, 4, 20.0)
+        x = G.add_outliers(G.gi_noise(n, 3, 1.0), 0.001, 3, 4, 20.0)
         nbuf = max(2, -(-(320 << 20) // (4 * n)))
         xs = [D.DeviceBuffer.from_host(ctx, x) for _ in range(nbuf)]
         q8 = D.DeviceBuffer.empty(ctx, n, np.int8)
@@ -454,7 +454,7 @@ def traffic_probe(reps=3, copy_bytes=1 << 30):
     known bytes: the counters' scale factor), then runs each GPT-2 linear's
     activation quantize + INT8 GEMM `reps` times on distinct buffers, so that
     every GEMM launch starts with its operands outside the caches."""
-    import oracle as O
+    from tokenvector.inference_amd import synthetic as G
     from tokenvector.inference_amd import _lib
     from tokenvector.inference_amd import device as D
 
@@ -471,10 +471,10 @@ def traffic_probe(reps=3, copy_bytes=1 << 30):
     dst.close()
     log(f"traffic probe: {reps} x k_copy16 of {copy_bytes} bytes")
     for j, (name, n, k) in enumerate(SHAPES):
-        w = D.DeviceBuffer.from_host(ctx, O.gi_noise(n * k, 11 + j, 0.02))
-        b = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 61 + j, 0.01))
+        w = D.DeviceBuffer.from_host(ctx, G.gi_noise(n * k, 11 + j, 0.02))
+        b = D.DeviceBuffer.from_host(ctx, G.gi_noise(n, 61 + j, 0.01))
         q = D.QuantizedLinear.from_float(ctx, w, n, k, b, D.WEIGHT_INT8)
-        xh = O.gi_noise(M * k, 0, 1.0)
+        xh = G.gi_noise(M * k, 0, 1.0)
         bufs = [(D.DeviceBuffer.from_host(ctx, xh), D.DeviceBuffer.empty(ctx, (M, k), np.int8),
                  D.DeviceBuffer.empty(ctx, (M, n), np.float32), D.params_buffer(ctx))
                 for _ in range(reps)]

@@ -848,6 +848,8 @@ static int launch_cfg(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
 // phase groups were slower.  Epilogues with int8 outputs (QLinearMatMul)
 // store a quarter of the bytes and only lose the delay (attn_out 12.9 ->
 // 15.2 us in a trace): they start unstaggered.  Results do not depend on it.
+// A per-shape sweep of the delay (0, 1, 2, 4, 6, 8; TKV_GEMM_STAGGER) kept
+// 4 for every shape, the one-tile-per-CU launches (N = 768) included.
 constexpr int kStartStagger = 4;
 
 template <class C, class P, class E>
@@ -857,9 +859,10 @@ static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int6
     const int64_t resident = (int64_t)c->num_cus * per_cu;
     const int64_t tiles = tiles_of<C>(m, n);
     const int64_t grid = tiles < resident ? tiles : resident;
+    int stagger = E::kOut32 ? kStartStagger : 0;
+    if (const char* v = getenv("TKV_GEMM_STAGGER")) stagger = atoi(v);  // tuning sweeps
     hipLaunchKernelGGL((k_gemm_ws<C, P, E>), dim3((unsigned)grid), dim3(C::THREADS), 0,
-                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y,
-                       E::kOut32 ? kStartStagger : 0);
+                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, stagger);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
