@@ -195,14 +195,24 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
 // a workgroup's activation bytes (RG K 4) at its weight bytes (16 K); 8
 // beyond, where more groups cost more in workgroup dispatch than their
 // bytes save (trace of the three decode shapes at M = 32, RG 4 / 8 / 16:
-// 7.7 / 7.0 / 7.4, 9.4 / 7.0 / 7.6, 11.4 / 9.6 / 12.7 us).  TKV_DECODE_RG
-// overrides it (sweeps).
-static int decode_rows_per_group(int64_t m) {
+// 7.7 / 7.0 / 7.4, 9.4 / 7.0 / 7.6, 11.4 / 9.6 / 12.7 us).  When the column
+// blocks and those groups would keep fewer than half of the CUs busy (N = 768
+// gives 48 blocks), the tokens are split into about 3/4 CUs / blocks groups
+// instead: mlp_down at M = 8, 5.45 us with 2 tokens per group against 6.65
+// with 4 (cold medians of three interleaved rounds, one box); qkv and mlp_up
+// measured within 0.1 us of their best at any group size from 4 to 16.
+// TKV_DECODE_RG overrides it (sweeps).
+static int decode_rows_per_group(int64_t m, int64_t ncb, int num_cus) {
     if (const char* v = getenv("TKV_DECODE_RG")) {
         const int r = atoi(v);
         if (r >= 1 && r <= 16) return r;
     }
-    return m <= 4 ? (int)m : (m <= 16 ? 4 : 8);
+    int64_t rg = m <= 4 ? m : (m <= 16 ? 4 : 8);
+    if (2 * ncb * ceil_div(m, rg) < num_cus) {
+        const int64_t groups = ceil_div((int64_t)num_cus * 3 / 4, ncb);
+        rg = ceil_div(m, groups);
+    }
+    return (int)rg;
 }
 
 int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t ldk,
@@ -211,8 +221,9 @@ int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
         ldk % 16 != 0 || ldk < k || !aligned(x, 16) || !aligned(w, 16) || n < 1 ||
         n >= (1ll << 28))
         return TKV_HIP_UNSUPPORTED;
-    const int rg = decode_rows_per_group(m);
-    const int64_t ncb = ceil_div(n, 16), ngr = ceil_div(m, (int64_t)rg);
+    const int64_t ncb = ceil_div(n, 16);
+    const int rg = decode_rows_per_group(m, ncb, c->num_cus);
+    const int64_t ngr = ceil_div(m, (int64_t)rg);
     const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
     hipLaunchKernelGGL(k_decode_i8, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
                        (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk, rg, (int)ncb, (int)ngr,
