@@ -86,6 +86,34 @@ int32_t tkv_hip_ctx_destroy(int64_t ctx);
 int32_t tkv_hip_ctx_set_stream(int64_t ctx, void* stream);
 int32_t tkv_hip_ctx_get_stream(int64_t ctx, void** stream_out);
 int32_t tkv_hip_ctx_synchronize(int64_t ctx);
+/* Tuning and test overrides of one context.  No reference counterpart: the
+ * library picks every launch shape itself; these exist for sweeps and for
+ * tests that must reach a path the automatic choice avoids.  value -1
+ * restores the automatic choice; anything outside a knob's range is
+ * TKV_HIP_BAD_ARG.  Results are bit-identical under every setting except
+ * TKV_HIP_TUNE_INT4_GEMV_WAVE, whose kernel adds the f64 products of the INT4
+ * decode GEMV in another order (the same bound applies to both).
+ *   GEMM_CFG        0..11  GEMM tile configuration of every INT8 / FP8
+ *                          product (10: the skinny kernel, INT8 with M <= 32)
+ *   GEMM_STAGGER    0..8   start delay of every other workgroup per XCD in
+ *                          the warp-specialised GEMM (units of 1024 cycles)
+ *   DECODE_GROUP    1..16  tokens per workgroup of the decode linear
+ *   QUANT_TWO_PASS  0..1   1: per-tensor calibrate + quantize always takes
+ *                          the two-kernel path (never the single pass)
+ *   INT4_GEMV_WAVE  0..1   1: INT4 decode batches take the per-column kernel
+ *   GRID_SPIN       0..2^20  polls a workgroup of the single-pass calibrate
+ *                          + quantize makes at its grid barrier before it
+ *                          scans the whole tensor itself (0: at once) */
+enum {
+    TKV_HIP_TUNE_GEMM_CFG = 0,
+    TKV_HIP_TUNE_GEMM_STAGGER = 1,
+    TKV_HIP_TUNE_DECODE_GROUP = 2,
+    TKV_HIP_TUNE_QUANT_TWO_PASS = 3,
+    TKV_HIP_TUNE_INT4_GEMV_WAVE = 4,
+    TKV_HIP_TUNE_GRID_SPIN = 5,
+    TKV_HIP_TUNE_COUNT = 6
+};
+int32_t tkv_hip_ctx_set_tuning(int64_t ctx, int32_t knob, int64_t value);
 /* Device memory and copies for callers without their own allocator (tests,
  * the .NET side).  Copies are ordered on the context's stream. */
 int32_t tkv_hip_malloc(int64_t ctx, int64_t bytes, void** ptr_out);
@@ -117,9 +145,11 @@ int32_t tkv_hip_event_elapsed_ms(int64_t ev_start, int64_t ev_end, float* ms_out
  * context is alive, a workspace that grows keeps its old buffer (it is
  * freed with the context's last graph, or with the context), so a replay
  * after a larger eager call still reads and writes valid memory.
- * Device-resident QuantParams are re-read on every replay.  Destroy a
- * context's graphs before the context; replays and eager calls on one
- * context are ordered on its stream. */
+ * Device-resident QuantParams are re-read on every replay.  Replays and
+ * eager calls on one context are ordered on its stream.  A context destroyed
+ * while some of its graphs are alive releases their executables and
+ * detaches them: graph_launch then fails with TKV_HIP_BAD_ARG, and
+ * graph_destroy only frees the handle, so either destruction order is safe. */
 int32_t tkv_hip_capture_begin(int64_t ctx);
 int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out);
 int32_t tkv_hip_graph_launch(int64_t ctx, int64_t graph);
@@ -379,7 +409,9 @@ int32_t tkv_hip_linear_forward(int64_t ctx, int64_t weight, const float* x, int6
  * on the first call).  INT8 weights only (FP8: TKV_HIP_UNSUPPORTED); larger
  * m * k or m: TKV_HIP_BAD_ARG.  Every call on a GPU shares that GPU's area,
  * which keeps the last call's contents: calls that overlap on one GPU (other
- * streams, other threads) race, so order them on one stream. */
+ * streams, other threads) race, so order them on one stream.  The weight's
+ * device is made current for the call; the calling thread's current device
+ * is restored before the call returns. */
 #define TKV_HIP_STATIC_CODES_BYTES (32ll << 20)
 int32_t tkv_hip_linear_forward_static(int64_t weight, const float* x, int64_t m,
                                       int32_t act_mode, float* y, void* stream);

@@ -117,3 +117,50 @@ def test_two_threads_drive_host_mirrors(hip):
         h.join(timeout=100)
     assert not any(h.is_alive() for h in th), "a mirror call did not return"
     assert not errors, errors
+
+
+def test_context_destroyed_before_its_graph(hip):
+    """A context closed while one of its graphs is alive releases the graph's
+    executable and detaches it: launching it later is TKV_HIP_BAD_ARG, and
+    destroying it afterwards frees only the handle (the order of the two
+    destructions no longer matters)."""
+    say("context closed before its graph")
+    L = _lib.lib()
+    ctx = D.Context(0)
+    n = 4096
+    dx = D.DeviceBuffer.from_host(ctx, O.gi_noise(n, 3, 1.0))
+    dq = D.DeviceBuffer.empty(ctx, n, np.int8)
+    p = D.params_buffer(ctx)
+    D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
+    ctx.synchronize()
+    with D.Graph(ctx) as g:
+        D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
+    g.launch()
+    ctx.synchronize()
+    handle = g.handle
+    for buf in (dx, dq, p):
+        buf.close()
+    ctx.close()                                   # before the graph
+    other = D.Context(0)
+    assert L.tkv_hip_graph_launch(other.handle, handle) == _lib.BAD_ARG
+    g.close()                                     # detached: frees the handle only
+    assert g.handle == 0
+    other.close()
+
+
+def test_set_tuning_ranges(hip):
+    """Per-context tuning overrides: each knob accepts its documented range
+    and -1, and refuses anything else (and unknown knobs) with BAD_ARG."""
+    L = _lib.lib()
+    ctx = D.Context(0)
+    ranges = {D.TUNE_GEMM_CFG: (0, 11), D.TUNE_GEMM_STAGGER: (0, 8),
+              D.TUNE_DECODE_GROUP: (1, 16), D.TUNE_QUANT_TWO_PASS: (0, 1),
+              D.TUNE_INT4_GEMV_WAVE: (0, 1), D.TUNE_GRID_SPIN: (0, 1 << 20)}
+    for knob, (lo, hi) in ranges.items():
+        for v in (lo, hi, -1):
+            assert L.tkv_hip_ctx_set_tuning(ctx.handle, knob, v) == _lib.OK, (knob, v)
+        for v in (lo - 1 if lo - 1 != -1 else -2, hi + 1):
+            assert L.tkv_hip_ctx_set_tuning(ctx.handle, knob, v) == _lib.BAD_ARG, (knob, v)
+    assert L.tkv_hip_ctx_set_tuning(ctx.handle, 6, 0) == _lib.BAD_ARG
+    assert L.tkv_hip_ctx_set_tuning(ctx.handle, -1, 0) == _lib.BAD_ARG
+    ctx.close()

@@ -472,19 +472,19 @@ def _res_input(n, seed):
     return O.add_outliers(x, 0.001, 3, 4, 20.0)
 
 
-def _dyn_quant(ctx, x, two_pass=False):
-    import os
+def _dyn_quant(ctx, x, two_pass=False, spin=-1):
     n = x.size
     dx = D.DeviceBuffer.from_host(ctx, x)
     dq = D.DeviceBuffer.empty(ctx, n, np.int8)
     p = D.params_buffer(ctx)
-    if two_pass:
-        os.environ["TKV_QUANT_TWO_PASS"] = "1"
+    ctx.set_tuning(D.TUNE_QUANT_TWO_PASS, 1 if two_pass else -1)
+    ctx.set_tuning(D.TUNE_GRID_SPIN, spin)
     try:
         D.quantize_int8_dynamic_tensor(ctx, dx, n, dq, p)
         ctx.synchronize()
     finally:
-        os.environ.pop("TKV_QUANT_TWO_PASS", None)
+        ctx.set_tuning(D.TUNE_QUANT_TWO_PASS, -1)
+        ctx.set_tuning(D.TUNE_GRID_SPIN, -1)
     return D.read_params(p), dq.download().astype(np.int32)
 
 
@@ -542,6 +542,30 @@ def test_int8_dynamic_tensor_specials(ctx, case, n):
         assert _same_f32([two_p.scale, two_p.min_val, two_p.max_val],
                          [got_p.scale, got_p.min_val, got_p.max_val])
         assert np.array_equal(two_q, want_q)
+
+
+@pytest.mark.parametrize("spin", [0, 1])
+def test_int8_dynamic_tensor_barrier_give_up(ctx, spin):
+    """The single-pass kernel's bounded grid barrier with the spin limit set
+    from the host to 0 or 1 poll: every workgroup (or all but the leader's
+    gather) gives up and scans the whole tensor itself.  QuantParams and codes
+    bit-exact against the oracle at 8192 x 3072 (with a NaN first element too),
+    and an ordinary call right after, whose barrier must still see consistent
+    slot generations."""
+    n = 8192 * 3072
+    for case in ("plain", "nan_first"):
+        say(f"int8 dynamic tensor give-up spin={spin} {case} n={n}")
+        x = _res_input(n, 91)
+        if case == "nan_first":
+            x[0] = np.nan
+        got_p, got_q = _dyn_quant(ctx, x, spin=spin)
+        want_p = O.calibrate_minmax(x, 1)
+        assert _same_f32([got_p.scale, got_p.min_val, got_p.max_val],
+                         [want_p.scale, want_p.min_val, want_p.max_val]), (spin, case)
+        want_q = O.quantize_int8_symmetric(x, want_p.scale)
+        assert np.array_equal(got_q, want_q), (spin, case)
+        again_p, again_q = _dyn_quant(ctx, x)
+        assert _same_f32([again_p.scale], [want_p.scale]) and np.array_equal(again_q, want_q)
 
 
 def test_int8_dynamic_tensor_repeated(ctx):
@@ -846,18 +870,19 @@ def test_fp8_gemm_fast(ctx, m, n, k):
 
 
 # ---------------------------------------------------------------------------
-# Every GEMM tile configuration (TKV_GEMM_CFG forces one per launch)
+# Every GEMM tile configuration (the context's GEMM_CFG override forces one per launch)
 # ---------------------------------------------------------------------------
 
-GEMM_CFGS = list(range(11))
+GEMM_CFGS = list(range(12))
 CFG_SHAPES = [(1, 1, 128), (37, 100, 200), (300, 500, 384), (1100, 2304, 768), (513, 768, 3072)]
 
 
 @pytest.fixture
-def gemm_cfg(monkeypatch):
+def gemm_cfg(ctx):
     def force(cfg):
-        monkeypatch.setenv("TKV_GEMM_CFG", str(cfg))
-    return force
+        ctx.set_tuning(D.TUNE_GEMM_CFG, cfg)
+    yield force
+    ctx.set_tuning(D.TUNE_GEMM_CFG, -1)
 
 
 @pytest.mark.parametrize("cfg", GEMM_CFGS)
@@ -973,15 +998,21 @@ DECODE_EDGE = [(1, 100, 64), (3, 17, 128), (5, 33, 192), (17, 200, 1024), (31, 2
                (32, 768, 3072), (2, 768, 3072), (8, 3072, 768)]
 
 
-@pytest.mark.parametrize("rg", [None, "1", "3", "16"])
-def test_decode_linear_edge_cases(ctx, monkeypatch, rg):
+@pytest.mark.parametrize("rg", [None, 1, 3, 16])
+def test_decode_linear_edge_cases(ctx, rg):
     """The one-kernel decode linear (per-token quantize + INT8 GEMM +
     epilogue, M <= 32): ragged row groups and column blocks, one to sixteen
     waves, a zero row (scale floor), a row holding NaN (skipped by the
     absmax, coded 0), an outlier row; forced row-group sizes; and a
     misaligned x, which takes the two-kernel path.  Bit-exact."""
-    if rg is not None:
-        monkeypatch.setenv("TKV_DECODE_RG", rg)
+    ctx.set_tuning(D.TUNE_DECODE_GROUP, -1 if rg is None else rg)
+    try:
+        _decode_edge_cases(ctx, rg)
+    finally:
+        ctx.set_tuning(D.TUNE_DECODE_GROUP, -1)
+
+
+def _decode_edge_cases(ctx, rg):
     for m, n, k in DECODE_EDGE:
         say(f"decode linear rg={rg} {m}x{n}x{k}")
         x = _x(m * k, 31 + m, 1.0).reshape(m, k)

@@ -24,8 +24,9 @@ U = 2.0 ** -24
 CASES = {
     # qkv-shaped MatMul, B = [K, N], float weights quantized by the fold, per-channel scales
     "matmul_kn_float_w": dict(m=64, k=768, n=2304),
-    # mlp_down-shaped Gemm with trans_b and a bias
-    "gemm_nk_bias": dict(m=200, k=3072, n=768, op=G.OperatorType_Gemm, b_nk=True, bias=True),
+    # attn_out-shaped Gemm with trans_b (a square B, which the reference reads as [N, K])
+    # and a bias
+    "gemm_nk_bias": dict(m=200, k=768, n=768, op=G.OperatorType_Gemm, b_nk=True, bias=True),
     # FusedLinear on stored int8 codes with one weight scale
     "fused_int8_w_tensor_scale": dict(m=33, k=256, n=96, op=G.OperatorType_FusedLinear,
                                       weight="int8", w_scale="tensor", bias=True),

@@ -38,13 +38,24 @@ def test_matmul_kn_per_channel_folds_and_transposes():
 
 
 def test_gemm_trans_b_with_bias_keeps_layout():
-    m, k, n = 3, 16, 8
+    # square B: the reference's Gemm (session.tkv:812-868) reads it as [N, K] under trans_b
+    m, k, n = 3, 16, 16
     g, d = build(m, k, n, op=G.OperatorType_Gemm, b_nk=True, weight="int8", bias=True)
     codes = g.initializers_int8["Wc"].copy()
     assert G.QdqFoldPass().run(g) == 1
     q = _qgemm(g)
     assert q.inputs[2] == "bias"
     assert np.array_equal(g.initializers_int8[q.inputs[1]], codes)
+
+
+def test_gemm_trans_b_non_square_is_not_folded():
+    # _exec_gemm takes N from B.shape[1] and reads b[j * B.shape[0] + p] under trans_b, which
+    # is not the [N, K] product for a non-square B: the node stays the reference's own
+    m, k, n = 3, 16, 8
+    g, d = build(m, k, n, op=G.OperatorType_Gemm, b_nk=True, weight="int8", bias=True)
+    G.QdqFoldPass().run(g)
+    assert not any(nd.op_type == G.OperatorType_QuantizedGemm for nd in g.nodes)
+    assert any(nd.op_type == G.OperatorType_Gemm for nd in g.nodes)
 
 
 def test_per_tensor_weight_scale_uses_scale_b():

@@ -201,12 +201,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
 // instead: mlp_down at M = 8, 5.45 us with 2 tokens per group against 6.65
 // with 4 (cold medians of three interleaved rounds, one box); qkv and mlp_up
 // measured within 0.1 us of their best at any group size from 4 to 16.
-// TKV_DECODE_RG overrides it (sweeps).
-static int decode_rows_per_group(int64_t m, int64_t ncb, int num_cus) {
-    if (const char* v = getenv("TKV_DECODE_RG")) {
-        const int r = atoi(v);
-        if (r >= 1 && r <= 16) return r;
-    }
+// The context's TKV_HIP_TUNE_DECODE_GROUP override forces it (sweeps, tests).
+static int decode_rows_per_group(const Ctx* c, int64_t m, int64_t ncb, int num_cus) {
+    if (tuned(c, TKV_HIP_TUNE_DECODE_GROUP) >= 1) return (int)tuned(c, TKV_HIP_TUNE_DECODE_GROUP);
     int64_t rg = m <= 4 ? m : (m <= 16 ? 4 : 8);
     if (2 * ncb * ceil_div(m, rg) < num_cus) {
         const int64_t groups = ceil_div((int64_t)num_cus * 3 / 4, ncb);
@@ -222,7 +219,7 @@ int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
         n >= (1ll << 28))
         return TKV_HIP_UNSUPPORTED;
     const int64_t ncb = ceil_div(n, 16);
-    const int rg = decode_rows_per_group(m, ncb, c->num_cus);
+    const int rg = decode_rows_per_group(c, m, ncb, c->num_cus);
     const int64_t ngr = ceil_div(m, (int64_t)rg);
     const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
     hipLaunchKernelGGL(k_decode_i8, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),

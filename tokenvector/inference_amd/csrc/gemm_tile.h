@@ -299,6 +299,9 @@ __device__ __forceinline__ void mainloop(const uint8_t* __restrict__ A,
 // INT8: v_mfma_i32_32x32x32_i8, 16 K-bytes per lane per 32-K step.
 struct PolicyI8 {
     typedef v16i Acc;
+    __device__ __forceinline__ static Acc mfma(const v4i& a, const v4i& b, const Acc& c) {
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+    }
     __device__ __forceinline__ static void zero(Acc& a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) a[r] = 0;
@@ -360,6 +363,11 @@ __device__ __forceinline__ int byte_sum4(const v4i& f, int s) {
 
 struct PolicyI8Q {
     typedef AccQ Acc;
+    __device__ __forceinline__ static Acc mfma(const v4i& a, const v4i& b, const Acc& c) {
+        Acc r = c;
+        r.v = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c.v, 0, 0, 0);
+        return r;
+    }
     __device__ __forceinline__ static void zero(Acc& a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) a.v[r] = 0;
@@ -487,6 +495,10 @@ __device__ __forceinline__ uint32_t dec2_f16(uint32_t x) {
 // 2^-8 pre-scale on both operands.
 struct PolicyF16 {
     typedef v16f Acc;
+    __device__ __forceinline__ static Acc mfma(const v4i& a, const v4i& b, const Acc& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a),
+                                                      __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+    }
     __device__ __forceinline__ static void zero(Acc& a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) a[r] = 0.0f;

@@ -938,7 +938,7 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
     // 11.1 us against 8.5 / 8.9 / 12.2 with 3, 9.6 / 10.2 / 13.0 with 8;
     // attn_out (24 k blocks) is capped at 3.
     if (m >= 2 && m <= kGemvRows && !perm && k % 32 == 0 && gs % 8 == 0 && aligned(a, 16) &&
-        aligned(wp, 4) && !getenv("TKV_INT4_GEMV_WAVE")) {
+        aligned(wp, 4) && tuned(c, TKV_HIP_TUNE_INT4_GEMV_WAVE) != 1) {
         const int64_t ncb = (n + 15) / 16, nkb = k / 32;
         int64_t splits = 1;
         if (ncb <= kGemvSplitBlocks && 2 * ncb < (int64_t)c->num_cus) {

@@ -185,6 +185,9 @@ static int static_scratch(int dev, uint8_t** out, int* cus) {
     return TKV_HIP_OK;
 }
 
+static int linear_forward_static_on(Weight* wt, const float* x, int64_t m, int32_t act_mode,
+                                    float* y, void* stream);
+
 }  // namespace tkv
 
 using namespace tkv;
@@ -310,7 +313,25 @@ int32_t tkv_hip_linear_forward_static(int64_t weight, const float* x, int64_t m,
                              std::to_string(TKV_HIP_STATIC_CODES_BYTES) + " bytes, " +
                              std::to_string(kStaticMaxRows) + " rows)");
     if (m == 0) return TKV_HIP_OK;
+    // The weight's device is made current for the call and the caller's
+    // current device restored before returning, whatever the outcome.
+    int prev_dev = 0;
+    TKV_HIP_TRY(hipGetDevice(&prev_dev));
     TKV_HIP_TRY(hipSetDevice(wt->device));
+    const int rc = linear_forward_static_on(wt, x, m, act_mode, y, stream);
+    const hipError_t e = hipSetDevice(prev_dev);
+    if (rc != TKV_HIP_OK) return rc;
+    if (e != hipSuccess) return fail_hip(e, "hipSetDevice(restore)", __FILE__, __LINE__);
+    return TKV_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace tkv {
+
+// The static entry's body, with wt->device current.
+static int linear_forward_static_on(Weight* wt, const float* x, int64_t m, int32_t act_mode,
+                                    float* y, void* stream) {
     uint8_t* base;
     int cus;
     TKV_RC_TRY(static_scratch(wt->device, &base, &cus));
@@ -338,4 +359,4 @@ int32_t tkv_hip_linear_forward_static(int64_t weight, const float* x, int64_t m,
     return linear_forward(&c, wt, x, m, act_mode, y);
 }
 
-}  // extern "C"
+}  // namespace tkv

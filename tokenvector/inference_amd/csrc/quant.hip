@@ -425,10 +425,11 @@ int launch_quant_i8_tensor(Ctx* c, const float* x, int64_t n, const tkv_hip_qpar
 // counter (256 agent-scope adds on one word serialize, ~10 us).  The grid is
 // one workgroup per CU (the LDS share leaves room for no second), so every
 // workgroup is resident once the CUs are free of earlier work.  The wait is
-// bounded all the same: a workgroup that gives up (kResSpin polls) takes the
-// absmax of the whole tensor itself, which gives the same scale (max is exact
-// in any order), so the result never depends on the barrier completing and
-// no workgroup can wait forever.
+// bounded all the same: a workgroup that gives up (kResSpin polls, or the
+// context's TKV_HIP_TUNE_GRID_SPIN override) takes the absmax of the whole
+// tensor itself, which gives the same scale (max is exact in any order), so
+// the result never depends on the barrier completing and no workgroup can
+// wait forever.
 // ---------------------------------------------------------------------------
 constexpr int kResBlock = 768;
 constexpr int kResRegs = 19;   // float4 per thread in registers (164 VGPRs in all)
@@ -456,7 +457,7 @@ __device__ __forceinline__ float block_max_res(float v, float* s) {
 template <bool OUT_I32>
 __global__ __launch_bounds__(kResBlock, 3) void k_quant_i8_resident(
     const float* __restrict__ x, int64_t n, tkv_hip_qparams_dev* __restrict__ p,
-    void* __restrict__ q, int recipe, unsigned long long* __restrict__ slots) {
+    void* __restrict__ q, int recipe, unsigned long long* __restrict__ slots, int spin) {
     __shared__ float4 s_x[kResLds * kResBlock];
     __shared__ float s_red[kResBlock / 64];
     __shared__ float s_all;
@@ -503,7 +504,7 @@ __global__ __launch_bounds__(kResBlock, 3) void k_quant_i8_resident(
         int ok = 0;
         if (blockIdx.x == 0) {
             // the leader gathers every slot, then publishes the max
-            for (int it = 0; it < kResSpin; it++) {
+            for (int it = 0; it < spin; it++) {
                 int ready = 1;
                 float gg = 0.0f;
                 for (int b = lane; b < (int)gridDim.x; b += 64) {
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(kResBlock, 3) void k_quant_i8_resident(
                 __hip_atomic_store(result, ((unsigned long long)gen << 32) | __float_as_uint(g),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else if (lane == 0) {
-            for (int it = 0; it < kResSpin; it++) {
+            for (int it = 0; it < spin; it++) {
                 const unsigned long long rv =
                     __hip_atomic_load(result, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if ((unsigned)(rv >> 32) == gen) {
@@ -584,12 +585,14 @@ static int launch_quant_i8_resident(Ctx* c, const float* x, int64_t n, int recip
         !aligned(x, 16) || !aligned(q, out_i32 ? 16 : 4) ||
         n / 4 > g * kResBlock * (kResRegs + kResLds))
         return TKV_HIP_UNSUPPORTED;
+    const int spin = tuned(c, TKV_HIP_TUNE_GRID_SPIN) >= 0 ? (int)tuned(c, TKV_HIP_TUNE_GRID_SPIN)
+                                                           : kResSpin;
     if (out_i32)
         hipLaunchKernelGGL((k_quant_i8_resident<true>), dim3((unsigned)g), dim3(kResBlock), 0,
-                           c->stream, x, n, p, q, recipe, c->grid_slots);
+                           c->stream, x, n, p, q, recipe, c->grid_slots, spin);
     else
         hipLaunchKernelGGL((k_quant_i8_resident<false>), dim3((unsigned)g), dim3(kResBlock), 0,
-                           c->stream, x, n, p, q, recipe, c->grid_slots);
+                           c->stream, x, n, p, q, recipe, c->grid_slots, spin);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
@@ -601,7 +604,7 @@ static int launch_quant_i8_resident(Ctx* c, const float* x, int64_t n, int recip
 int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
                             tkv_hip_qparams_dev* p, void* q, bool out_i32) {
     if (n <= 0) return launch_minmax_tensor(c, x, n, MM_SYMMETRIC, recipe, p);
-    if (!getenv("TKV_QUANT_TWO_PASS")) {
+    if (tuned(c, TKV_HIP_TUNE_QUANT_TWO_PASS) != 1) {
         const int rc = launch_quant_i8_resident(c, x, n, recipe, p, q, out_i32);
         if (rc != TKV_HIP_UNSUPPORTED) return rc;
     }

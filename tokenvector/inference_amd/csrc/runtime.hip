@@ -106,11 +106,28 @@ int ctx_create(int device, Ctx** out) {
     return TKV_HIP_OK;
 }
 
+// A captured graph and the context whose workspaces it replays (null once
+// that context has been destroyed: the graph is then detached, its
+// executable released, and only the handle itself is left to free).
+struct Graph {
+    hipGraphExec_t exec = nullptr;
+    Ctx* ctx = nullptr;
+};
+
 int ctx_destroy(Ctx* c) {
     if (!c) return TKV_HIP_OK;
     // Teardown: errors here leave nothing the caller can act on.
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    // Graphs still alive replay this context's workspaces: release their
+    // executables now and detach the handles, so that a later graph_destroy
+    // frees only the handle and never touches the freed context.
+    for (Graph* g : c->graphs) {
+        if (g->exec) (void)hipGraphExecDestroy(g->exec);
+        g->exec = nullptr;
+        g->ctx = nullptr;
+    }
+    c->graphs.clear();
     for (int i = 0; i < Ctx::kSlots; i++)
         if (c->ws[i]) (void)hipFree(c->ws[i]);
     for (void* p : c->retired) (void)hipFree(p);
@@ -154,7 +171,7 @@ int ctx_workspace(Ctx* c, int slot, size_t bytes, void** out) {
                                  " would grow inside a stream capture: make the same calls "
                                  "once before capturing");
         if (c->ws[slot]) {
-            if (c->live_graphs > 0) {
+            if (!c->graphs.empty()) {
                 // a live graph may replay into the old buffer: keep it
                 c->retired.push_back(c->ws[slot]);
             } else {
@@ -280,6 +297,22 @@ int32_t tkv_hip_ctx_get_stream(int64_t ctx, void** stream_out) {
     return TKV_HIP_OK;
 }
 
+int32_t tkv_hip_ctx_set_tuning(int64_t ctx, int32_t knob, int64_t value) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    static const int64_t hi[TKV_HIP_TUNE_COUNT] = {11, 8, 16, 1, 1, 1 << 20};
+    static const int64_t lo[TKV_HIP_TUNE_COUNT] = {0, 0, 1, 0, 0, 0};
+    if (knob < 0 || knob >= TKV_HIP_TUNE_COUNT)
+        return set_error(TKV_HIP_BAD_ARG, "set_tuning: unknown knob " + std::to_string(knob));
+    if (value != -1 && (value < lo[knob] || value > hi[knob]))
+        return set_error(TKV_HIP_BAD_ARG, "set_tuning: value " + std::to_string(value) +
+                                              " outside knob " + std::to_string(knob) +
+                                              "'s range [" + std::to_string(lo[knob]) + ", " +
+                                              std::to_string(hi[knob]) + "] (or -1)");
+    c->tune[knob] = value;
+    return TKV_HIP_OK;
+}
+
 int32_t tkv_hip_ctx_synchronize(int64_t ctx) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
@@ -360,12 +393,6 @@ int32_t tkv_hip_capture_begin(int64_t ctx) {
     return TKV_HIP_OK;
 }
 
-// A captured graph and the context whose workspaces it replays.
-struct Graph {
-    hipGraphExec_t exec = nullptr;
-    Ctx* ctx = nullptr;
-};
-
 int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
@@ -386,7 +413,7 @@ int32_t tkv_hip_capture_end(int64_t ctx, int64_t* graph_out) {
     }
     gr->exec = x;
     gr->ctx = c;
-    c->live_graphs++;
+    c->graphs.push_back(gr);
     *graph_out = reinterpret_cast<int64_t>(gr);
     return TKV_HIP_OK;
 }
@@ -396,7 +423,10 @@ int32_t tkv_hip_graph_launch(int64_t ctx, int64_t graph) {
     TKV_RC_TRY(ctx_get(ctx, &c));
     if (!graph) return set_error(TKV_HIP_BAD_ARG, "graph_launch: NULL graph");
     if (c->capturing) return set_error(TKV_HIP_BAD_ARG, "graph_launch: context is capturing");
-    TKV_HIP_TRY(hipGraphLaunch(reinterpret_cast<Graph*>(graph)->exec, c->stream));
+    const Graph* gr = reinterpret_cast<const Graph*>(graph);
+    if (!gr->exec)
+        return set_error(TKV_HIP_BAD_ARG, "graph_launch: the graph's context has been destroyed");
+    TKV_HIP_TRY(hipGraphLaunch(gr->exec, c->stream));
     return TKV_HIP_OK;
 }
 
@@ -404,13 +434,18 @@ int32_t tkv_hip_graph_destroy(int64_t graph) {
     Graph* gr = reinterpret_cast<Graph*>(graph);
     if (!gr) return TKV_HIP_OK;
     Ctx* c = gr->ctx;
+    if (!c) {  // detached by ctx_destroy, which released the executable
+        delete gr;
+        return TKV_HIP_OK;
+    }
     TKV_HIP_TRY(hipSetDevice(c->device));
     // replays already queued must finish before the graph or the buffers
     // it reads go away
     TKV_HIP_TRY(hipStreamSynchronize(c->stream));
     TKV_HIP_TRY(hipGraphExecDestroy(gr->exec));
+    c->graphs.erase(std::find(c->graphs.begin(), c->graphs.end(), gr));
     delete gr;
-    if (--c->live_graphs == 0) {
+    if (c->graphs.empty()) {
         for (void* p : c->retired) TKV_HIP_TRY(hipFree(p));
         c->retired.clear();
     }

@@ -48,6 +48,8 @@ constexpr int kMaxGridSlots = 1024;
 constexpr int kCalCounters = 4;
 constexpr int64_t kCalHistBins = 4096;  // the largest KL histogram
 
+struct Graph;
+
 struct RedPartial {
     float mn;
     float mx;
@@ -87,13 +89,20 @@ struct Ctx {
     // Graphs captured on this context and not yet destroyed.  They replay
     // the workspace addresses they captured, so while any is alive a slot
     // that grows keeps its old buffer here (freed with the last graph, or
-    // with the context) instead of freeing it.
-    int live_graphs = 0;
+    // with the context) instead of freeing it.  Destroying the context
+    // first releases every live graph's executable and detaches the graph
+    // handles, which stay valid for graph_destroy (see runtime.hip).
+    std::vector<Graph*> graphs;
     std::vector<void*> retired;
     // A context over caller-fixed memory (the static-scratch entry point):
     // its workspaces never grow; a call that would need more fails.
     bool no_alloc = false;
+    // Tuning overrides (TKV_HIP_TUNE_*), -1 = automatic.
+    int64_t tune[TKV_HIP_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1};
 };
+
+// The override of `knob` on context c, or -1 (automatic).
+inline int64_t tuned(const Ctx* c, int knob) { return c->tune[knob]; }
 
 int ctx_create(int device, Ctx** out);
 int ctx_destroy(Ctx* c);

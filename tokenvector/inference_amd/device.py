@@ -30,6 +30,15 @@ def _vp(x) -> C.c_void_p:
     return C.c_void_p(int(x))
 
 
+# Tuning knobs of Context.set_tuning (tkv_hip.h, TKV_HIP_TUNE_*).
+TUNE_GEMM_CFG = 0
+TUNE_GEMM_STAGGER = 1
+TUNE_DECODE_GROUP = 2
+TUNE_QUANT_TWO_PASS = 3
+TUNE_INT4_GEMV_WAVE = 4
+TUNE_GRID_SPIN = 5
+
+
 class Context:
     """A libtkv_hip context: one HIP stream plus grow-only workspaces."""
 
@@ -40,6 +49,10 @@ class Context:
 
     def synchronize(self) -> None:
         _lib.check(_lib.lib().tkv_hip_ctx_synchronize(self.handle))
+
+    def set_tuning(self, knob: int, value: int) -> None:
+        """Tuning / test override of this context (TKV_HIP_TUNE_*; -1 = automatic)."""
+        _lib.check(_lib.lib().tkv_hip_ctx_set_tuning(self.handle, int(knob), int(value)))
 
     def retired_buffers(self) -> int:
         """Workspace buffers kept alive for this context's live graphs."""

@@ -20,8 +20,11 @@ A is rank 2, the weight is an int8 initializer or a Q of a float initializer (qu
 once, by the Q node's own kernel), and the node is a plain product: FusedLinear without an
 activation; Gemm with alpha = 1, trans_a = 0 and, with a C input, beta = 1 and C of N
 elements.  B's layout follows the reference's node: MatMul / FusedLinear read [N, K] when
-B's second dimension equals K and [K, N] otherwise (``_exec_linear``, session.tkv:736-773),
-Gemm reads ``trans_b`` (session.tkv:840-866); [K, N] codes are stored transposed.
+B's second dimension equals K and [K, N] otherwise (``_exec_linear``, session.tkv:736-773);
+[K, N] codes are stored transposed.  Gemm (``_exec_gemm``, session.tkv:812-868) always takes
+N from B's second dimension and, with ``trans_b``, reads b[j * B.shape[0] + p]: that is the
+[N, K] product only for a square B, so a ``trans_b`` Gemm folds only when B is square
+(otherwise it keeps the reference's own node, which reads B that way).
 
 The folded node computes the QDQ graph's value with exact integer sums and the reference's
 per-channel epilogue: y = fl32(fl64(fl64(Σ qx qw · sx) · sw[n]) + b[n]).  The f32 float path
@@ -245,6 +248,8 @@ class QdqFoldPass(IGraphPass):
             b_nk = mm.trans_b != 0
             if b_shape[1 if b_nk else 0] != k:
                 return None
+            if b_nk and b_shape[0] != b_shape[1]:
+                return None  # the reference's trans_b indexing (see the module docstring)
         elif b_shape[1] == k:
             b_nk = True
         elif b_shape[0] == k:
