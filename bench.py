@@ -453,7 +453,8 @@ def traffic_probe(reps=3, copy_bytes=1 << 30):
     `copy_bytes` `reps` times with the library's plain copy kernel (k_copy16,
     known bytes: the counters' scale factor), then runs each GPT-2 linear's
     activation quantize + INT8 GEMM `reps` times on distinct buffers, so that
-    every GEMM launch starts with its operands outside the caches."""
+    every GEMM launch starts with its operands outside the caches; then the
+    FP8 GEMM (full rate and reference products) `reps` times per shape."""
     from tokenvector.inference_amd import synthetic as G
     from tokenvector.inference_amd import _lib
     from tokenvector.inference_amd import device as D
@@ -488,6 +489,24 @@ def traffic_probe(reps=3, copy_bytes=1 << 30):
         for t in bufs:
             for buf in t:
                 buf.close()
+    # FP8 products on the same shapes (raw e4m3 bytes, finite codes), for the
+    # MFMA-busy pass: the full-rate kernel, then the reference-products path
+    # (decode pre-passes + f16 MFMA)
+    rng = np.random.default_rng(5)
+    for j, (name, n, k) in enumerate(SHAPES):
+        a8 = (rng.integers(0, 126, (M, k)) | (rng.integers(0, 2, (M, k)) << 7)).astype(np.uint8)
+        w8 = (rng.integers(0, 126, (n, k)) | (rng.integers(0, 2, (n, k)) << 7)).astype(np.uint8)
+        da, dw = D.DeviceBuffer.from_host(ctx, a8), D.DeviceBuffer.from_host(ctx, w8)
+        db = D.DeviceBuffer.from_host(ctx, G.gi_noise(n, 71 + j, 0.01))
+        dy = D.DeviceBuffer.empty(ctx, (M, n), np.float32)
+        for fast in (True, False):
+            for _ in range(reps):
+                D.matmul_fp8_e4m3(ctx, da, dw, M, n, k, None, 0, None, db, dy, fast=fast)
+            ctx.synchronize()
+            log(f"traffic probe: {reps} x {name} FP8 GEMM ({'full rate' if fast else 'reference products'}) "
+                f"M={M} N={n} K={k}")
+        for buf in (da, dw, db, dy):
+            buf.close()
         q.close()
     ctx.close()
 

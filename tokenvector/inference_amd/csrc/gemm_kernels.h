@@ -1103,18 +1103,11 @@ static int launch_gemv(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, in
 template <class P, class E>
 static int launch_any(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                       int64_t ldk, const E& ep, void* y) {
-    int cfg = pick_cfg(c, m, n);
+    const int cfg = pick_cfg(c, m, n);
     const bool forced = tuned(c, TKV_HIP_TUNE_GEMM_CFG) >= 0;
     if constexpr (std::is_same_v<P, PolicyI8>) {
         if (m <= kGemvMaxM && (cfg == 10 || !forced))
             return launch_gemv(c, a, w, m, n, ldk, ep, y);
-        // Many tiles per CU with f32 / INT32 outputs: two fused-role
-        // workgroups per CU overlap one's output stores with the other's K
-        // loop.  mlp_up at M = 8192 (1024 cfg 2 tiles): 37.4 against 40.8 us
-        // (12 rotating weight sets, medians of 7 interleaved rounds, one
-        // box); qkv (768 tiles) measured equal and stays on cfg 2.
-        if (!forced && cfg == 2 && E::kOut32 && tiles_of<Cfg2>(m, n) >= 4 * (int64_t)c->num_cus)
-            cfg = 11;
     }
     switch (cfg) {
         case 0: return launch_cfg<Cfg0, P>(c, a, w, m, n, ldk, ep, y);
