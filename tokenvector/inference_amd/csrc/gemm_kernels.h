@@ -857,11 +857,12 @@ constexpr int kGemvUnroll = 8;
 // SPLIT: workgroup b takes column block b % ncb and the K steps of split
 // b / ncb (of `splits`), so narrow N still spreads over the CUs.  Its INT32
 // partial sums go into part[block][1024] with device-scope atomic adds (exact
-// in any order); after an agent-scope release it counts itself into
-// arrivals[block] with an acquire-release device-scope atomic.  The workgroup
-// that completes the count takes the sums with an exchange that also clears
-// them, clears the count, and runs the epilogue: no workgroup ever waits for another, and part / arrivals are
-// zero again when the kernel ends (zeroed at context creation).
+// in any order); once those adds have completed it counts itself into
+// arrivals[block] with another device-scope atomic.  The workgroup that
+// completes the count takes the sums with an exchange that also clears them,
+// clears the count, and runs the epilogue: no workgroup ever waits for
+// another, and part / arrivals are zero again when the kernel ends (zeroed at
+// context creation).
 template <int KW, bool SPLIT, class E>
 __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__ A,
                                                      const uint8_t* __restrict__ W, int M, int N,
@@ -921,18 +922,23 @@ __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__
         for (int i = 0; i < 16; i++)
             __hip_atomic_fetch_add(pc + i * 64 + lane, sum[0][0][i], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-        // Release: every lane's adds are ordered before its agent-scope
-        // release fence, which the wave executes before lane 0 counts the
-        // workgroup in with an acquire-release add; the workgroup that
-        // completes the count acquires (every lane, after the arrival has
-        // returned) before its exchanges read the sums.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        // Every access to part[] and arrivals[] is a device-scope atomic
+        // (the adds, the count, the exchanges that read the sums), performed
+        // where every XCD sees it.  The wave waits for its adds to complete
+        // (vmcnt counts atomics and retires in issue order) before lane 0
+        // issues the arrival, and the exchanges issue only after the
+        // arrival has returned.  That is the hardware's ordering of this
+        // wave's own memory operations, not a release / acquire pair of the
+        // HIP memory model: agent-scope fences (an L2 writeback before the
+        // arrival, an L2 invalidate before the exchanges) made the split
+        // call 4.2 us slower (mlp_down decode shape, 6.6 -> 10.8 us at
+        // M = 1, three interleaved rounds on one box), so they are not used.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         int last = 0;
         if (lane == 0)
-            last = __hip_atomic_fetch_add(arrivals + cb, 1u, __ATOMIC_ACQ_REL,
+            last = __hip_atomic_fetch_add(arrivals + cb, 1u, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(splits - 1);
         if (!__shfl(last, 0, 64)) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
         for (int i = 0; i < 16; i++)
             sum[0][0][i] = __hip_atomic_exchange(pc + i * 64 + lane, 0, __ATOMIC_RELAXED,
