@@ -1045,8 +1045,13 @@ static int launch_fused(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, i
 // phase groups were slower.  Epilogues with int8 outputs (QLinearMatMul)
 // store a quarter of the bytes and only lose the delay (attn_out 12.9 ->
 // 15.2 us in a trace): they start unstaggered.  Results do not depend on it.
-// A per-shape sweep of the delay (0, 1, 2, 4, 6, 8; TKV_GEMM_STAGGER) kept
-// 4 for every shape, the one-tile-per-CU launches (N = 768) included.
+// A per-shape sweep of the delay (0, 1, 2, 4, 6, 8) over back-to-back GEMMs
+// kept 4 for every shape.  Inside the bench step, where each GEMM follows its
+// activation kernels, the launches with one tile per workgroup (attn_out and
+// mlp_down, N = 768) only pay the delay: the step took 1.8672 ms with 4 on
+// every shape, 1.8662 / 1.8575 ms with 4 on mlp_down / attn_out alone and
+// 1.8523 / 1.8530 ms with 4 on qkv / mlp_up alone (5 interleaved rounds,
+// one box), so the delay applies only when workgroups run several tiles.
 constexpr int kStartStagger = 4;
 
 template <class C, class P, class E>
@@ -1056,7 +1061,7 @@ static int launch_ws(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int6
     const int64_t resident = (int64_t)c->num_cus * per_cu;
     const int64_t tiles = tiles_of<C>(m, n);
     const int64_t grid = tiles < resident ? tiles : resident;
-    int stagger = E::kOut32 ? kStartStagger : 0;
+    int stagger = E::kOut32 && tiles > grid ? kStartStagger : 0;
     if (tuned(c, TKV_HIP_TUNE_GEMM_STAGGER) >= 0) stagger = (int)tuned(c, TKV_HIP_TUNE_GEMM_STAGGER);
     hipLaunchKernelGGL((k_gemm_ws<C, P, E>), dim3((unsigned)grid), dim3(C::THREADS), 0,
                        c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, stagger);
