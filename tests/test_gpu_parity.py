@@ -1051,9 +1051,11 @@ def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
     gemm_cfg(cfg)
     # zero points: both set; zpa = 0 (no W sums needed); zpw = 0 (no A sums);
     # both 0 (no pre-pass at all); zpw = 0 with |zpa| large enough for the f64
-    # correction path at K = 768.  M > 32 with few K slices per workgroup
-    # forms the row sums inside the GEMM; K = 3072 at M = 1024 takes the
-    # pre-pass.
+    # correction path at K = 768.  M > 32 with one tile or few K slices per
+    # workgroup forms the row sums inside the GEMM (split over the waves on
+    # the warp-specialised configurations); launches with several tiles per
+    # workgroup and many slices (the pre-pass) are in
+    # test_qlinear_sums_tile_runs.
     cases = [((37, 100, 200), (-3, 5, 7)), ((1024, 768, 768), (-3, 5, 7)),
              ((16, 2304, 768), (-3, 5, 7)), ((16, 768, 3072), (-3, 5, 7)),
              ((37, 100, 200), (0, 5, 7)), ((37, 100, 200), (-3, 0, 7)),
@@ -1074,6 +1076,37 @@ def test_qlinear_matmul_device_every_config(ctx, gemm_cfg, cfg):
         want = O.qlinear_matmul(a.astype(np.int32), sa, zpa, b, sw, zpw, sy, zpy, m * n, m, n, k)
         got = dy.download().astype(np.int32).reshape(-1)
         assert np.array_equal(got, want), (cfg, m, n, k, int(np.sum(got != want)))
+
+
+def test_qlinear_sums_tile_runs(ctx, gemm_cfg):
+    """QLinearMatMul on launches where workgroups run several tiles.  Row /
+    column sums split over the waves of the warp-specialised kernel and
+    exchanged through LDS at each tile's end (the two LDS areas alternate by
+    tile): 264 tiles of cfg 2 on 256 CUs, more on cfg 5 / 8, with one K slice
+    (the exchange's first and last slice coincide) and three; both zero-point
+    sums, and W sums only.  K = 896 gives 14 slices per workgroup: the sums
+    come from the pre-pass.  Bit-exact against the oracle."""
+    for (m, n, k), (zpa, zpw, zpy) in [((4224, 1536, 128), (-3, 5, 7)),
+                                       ((4224, 1536, 384), (-3, 5, 7)),
+                                       ((4224, 1536, 384), (6, 0, -2)),
+                                       ((4224, 1536, 896), (-3, 5, 7))]:
+        a = RNG.integers(-128, 128, m * k).astype(np.int8)
+        w = RNG.integers(-128, 128, n * k).astype(np.int8)
+        sa, sw = np.float32(0.02), np.float32(0.003)
+        sy = np.float32(np.sqrt(k) * 128 * 128 * sa * sw / 90.0)
+        b = np.ascontiguousarray(w.reshape(n, k).T).reshape(-1).astype(np.int32)
+        want = O.qlinear_matmul(a.astype(np.int32), sa, zpa, b, sw, zpw, sy, zpy, m * n, m, n, k)
+        da, dw = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, w)
+        dy = D.DeviceBuffer.empty(ctx, (m, n), np.int8)
+        for cfg in (-1, 2, 5, 8):
+            say(f"qlinear tile runs cfg={cfg} {m}x{n}x{k} zp={zpa},{zpw},{zpy}")
+            gemm_cfg(cfg)
+            _lib_check(D, "tkv_hip_dev_qlinear_matmul", ctx.handle, da.ptr, float(sa), zpa,
+                       dw.ptr, float(sw), zpw, float(sy), zpy, dy.ptr, m, n, k, 0)
+            got = dy.download().astype(np.int32).reshape(-1)
+            assert np.array_equal(got, want), (cfg, m, n, k, int(np.sum(got != want)))
+        for buf in (da, dw, dy):
+            buf.close()
 
 
 def _lib_check(D, name, *args):

@@ -83,19 +83,26 @@ int launch_gemm_qlinear(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int
     const auto* ua = static_cast<const uint8_t*>(pa);
     const auto* uw = static_cast<const uint8_t*>(pw);
     const bool i32 = bound < (1ll << 31) && std::isfinite(q.mult);
-    // Tiled kernels can form the sums themselves (PolicyI8Q): that costs
-    // ~0.3 us per 128-deep K slice a workgroup runs, against ~4.5-6 us for
-    // the pre-pass at M = 8192 (traces of both on one box: attn_out 15.0
-    // against 13.3 + 4.4 us; qkv, mlp_up and mlp_down, at 18-24 slices per
-    // workgroup, 1.5-3.4 us slower).  So they do it up to 12 slices.
-    const int64_t slices = ceil_div(gemm::tiles_of<gemm::Cfg2>(m, n), (int64_t)c->num_cus) *
-                           (ldk / gemm::kBK);
-    if (m > gemm::kGemvMaxM && slices <= 12) {
+    // Tiled kernels can form the sums themselves.  Summed in every wave
+    // (PolicyI8Q) that cost ~0.3 us per 128-deep K slice a workgroup runs;
+    // split over the waves of the warp-specialised kernel (PolicyI8QS, each
+    // byte summed once, partials exchanged through LDS at each tile's end)
+    // it costs less per slice but adds an exchange per tile.  The pre-pass
+    // costs ~4.5-7 us at M = 8192, growing with M K.  bench.py's qlinear
+    // section, interleaved rounds on one box, split sums against the earlier
+    // choice (pre-pass beyond 12 slices per workgroup, per-wave sums below):
+    // attn_out 14.1 / 15.0 us, mlp_down (one tile of 24 slices per
+    // workgroup) 29.8 / 32.4, qkv (three tiles of 6) 34.1 / 33.9, mlp_up
+    // (four tiles of 6) 43.3 / 41.9.  So the GEMM sums whenever a workgroup
+    // runs one tile, or few slices in all.
+    const int64_t tiles = gemm::tiles_of<gemm::Cfg2>(m, n);
+    const int64_t slices = ceil_div(tiles, (int64_t)c->num_cus) * (ldk / gemm::kBK);
+    if (m > gemm::kGemvMaxM && (tiles <= c->num_cus || slices <= 12)) {
         if (i32)
-            return gemm::launch_any<gemm::PolicyI8Q>(
+            return gemm::launch_any<gemm::PolicyI8QS>(
                 c, ua, uw, m, n, ldk,
                 gemm::EpiQL<true, true>{nullptr, nullptr, q.zpa, q.zpw, q.zpy, kzz, q.mult}, y);
-        return gemm::launch_any<gemm::PolicyI8Q>(
+        return gemm::launch_any<gemm::PolicyI8QS>(
             c, ua, uw, m, n, ldk,
             gemm::EpiQL<false, true>{nullptr, nullptr, q.zpa, q.zpw, q.zpy, kzz, q.mult}, y);
     }

@@ -629,8 +629,11 @@ __global__ __launch_bounds__(C::THREADS, C::MIN_WAVES_EU) void k_gemm_ws(const u
             for (int kt = 0; kt < nk; kt++, s++) {
                 const uint8_t* sa = smem + (s % C::STAGES) * C::STAGE_BYTES;
                 P::template slice<C>(sa, sa + C::A_BYTES, a_row, w_row, khalf, acc);
+                if constexpr (shares_sums<P>::value)
+                    if (kt == nk - 1) P::template publish<C>(acc, ti & 1);
                 barrier();
             }
+            if constexpr (shares_sums<P>::value) P::template gather<C>(acc, ti & 1);
             ep.template store<C, P>(acc, eo, m0, n0, M, N, Y);
         }
     } else {
@@ -1116,11 +1119,26 @@ static int launch_any(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int
                       int64_t ldk, const E& ep, void* y) {
     const int cfg = pick_cfg(c, m, n);
     const bool forced = tuned(c, TKV_HIP_TUNE_GEMM_CFG) >= 0;
+    // The split sums need the warp-specialised kernel and 2 (BM WN + BN WM)
+    // ints of LDS beside its ring (all of cfg 6's LDS is ring); other
+    // configurations sum in every wave (PolicyI8Q).
+    if constexpr (std::is_same_v<P, PolicyI8QS>) {
+        switch (cfg) {
+            case 2: return launch_ws<Cfg2, P>(c, a, w, m, n, ldk, ep, y);
+            case 3: return launch_ws<Cfg3, P>(c, a, w, m, n, ldk, ep, y);
+            case 4: return launch_ws<Cfg4, P>(c, a, w, m, n, ldk, ep, y);
+            case 5: return launch_ws<Cfg5, P>(c, a, w, m, n, ldk, ep, y);
+            case 7: return launch_ws<Cfg7, P>(c, a, w, m, n, ldk, ep, y);
+            case 8: return launch_ws<Cfg8, P>(c, a, w, m, n, ldk, ep, y);
+            case 9: return launch_ws<Cfg9, P>(c, a, w, m, n, ldk, ep, y);
+            default: return launch_any<PolicyI8Q>(c, a, w, m, n, ldk, ep, y);
+        }
+    }
     if constexpr (std::is_same_v<P, PolicyI8>) {
         if (m <= kGemvMaxM && (cfg == 10 || !forced))
             return launch_gemv(c, a, w, m, n, ldk, ep, y);
     }
-    switch (cfg) {
+    if constexpr (!std::is_same_v<P, PolicyI8QS>) switch (cfg) {
         case 0: return launch_cfg<Cfg0, P>(c, a, w, m, n, ldk, ep, y);
         case 1: return launch_cfg<Cfg1, P>(c, a, w, m, n, ldk, ep, y);
         case 2: return launch_ws<Cfg2, P>(c, a, w, m, n, ldk, ep, y);

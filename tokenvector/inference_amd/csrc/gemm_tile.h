@@ -409,6 +409,122 @@ struct PolicyI8Q {
     }
 };
 
+// PolicyI8Q with the sums split over the waves that share them, for the
+// warp-specialised kernel: wave (wm, wn) adds the A fragment bytes of the
+// k-steps with ks % WN == wn and the W fragment bytes of those with
+// ks % WM == wm, so every byte of a slice is summed once per workgroup
+// instead of WN (A) or WM (W) times (20 dot4 per slice and wave instead of 64
+// with cfg 2).  After a tile's last slice each wave stores its partial sums
+// in LDS (publish, before that slice's barrier); after the barrier every wave
+// adds the partials of its rows and columns (gather), which leaves
+// acc[i][0].rs / acc[0][j].cs in PolicyI8Q's form (a lane's value plus that
+// of lane ^ 32 is the full sum).  Two LDS areas alternate by tile: a wave
+// can only write the next tile's partials after every wave has passed that
+// tile's first barrier, i.e. finished reading this tile's.
+struct PolicyI8QS : PolicyI8Q {
+    template <class C>
+    static constexpr int share_ints() { return C::BM * C::WN + C::BN * C::WM; }
+
+    template <class C>
+    __device__ __forceinline__ static int32_t* share_area() {
+        __shared__ __attribute__((aligned(16))) int32_t s_share[2 * share_ints<C>()];
+        return s_share;
+    }
+
+    template <class C>
+    __device__ __forceinline__ static void slice(const uint8_t* sa, const uint8_t* sw,
+                                                 const int (&a_row)[C::TM],
+                                                 const int (&w_row)[C::TN], int khalf,
+                                                 Acc (&acc)[C::TM][C::TN]) {
+        constexpr int KS = C::BK / 32, D = C::FRAG_DEPTH;
+        const int wave = wave_id();
+        const int wm = wave / C::WN, wn = wave % C::WN;
+        v4i af[KS][C::TM], bf[KS][C::TN];
+        auto load = [&](int ks) {
+            const int ch = ks * 2 + khalf;
+#pragma unroll
+            for (int i = 0; i < C::TM; i++) af[ks][i] = lds_chunk<C>(sa, a_row[i], ch);
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) bf[ks][j] = lds_chunk<C>(sw, w_row[j], ch);
+        };
+#pragma unroll
+        for (int ks = 0; ks < D - 1 && ks < KS; ks++) load(ks);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks + D - 1 < KS) load(ks + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++)
+                    acc[i][j].v = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j],
+                                                                        acc[i][j].v, 0, 0, 0);
+            if (ks % C::WN == wn) {
+#pragma unroll
+                for (int i = 0; i < C::TM; i++) acc[i][0].rs = byte_sum4(af[ks][i], acc[i][0].rs);
+            }
+            if (ks % C::WM == wm) {
+#pragma unroll
+                for (int j = 0; j < C::TN; j++) acc[0][j].cs = byte_sum4(bf[ks][j], acc[0][j].cs);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Area `buf`: row sums [WN][BM] (partial over the k-steps of wave column
+    // wn), then column sums [WM][BN] (partial over those of wave row wm).
+    template <class C>
+    __device__ __forceinline__ static void publish(const Acc (&acc)[C::TM][C::TN], int buf) {
+        const int lane = threadIdx.x & 63, wave = wave_id();
+        const int wm = wave / C::WN, wn = wave % C::WN;
+        int32_t* rs = share_area<C>() + buf * share_ints<C>();
+        int32_t* cs = rs + C::BM * C::WN;
+#pragma unroll
+        for (int i = 0; i < C::TM; i++) {
+            const int full = acc[i][0].rs + __shfl_xor(acc[i][0].rs, 32, 64);
+            if (lane < 32) rs[wn * C::BM + wm * C::WTM + i * 32 + lane] = full;
+        }
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int full = acc[0][j].cs + __shfl_xor(acc[0][j].cs, 32, 64);
+            if (lane < 32) cs[wm * C::BN + wn * C::WTN + j * 32 + lane] = full;
+        }
+    }
+
+    template <class C>
+    __device__ __forceinline__ static void gather(Acc (&acc)[C::TM][C::TN], int buf) {
+        const int lane = threadIdx.x & 63, wave = wave_id();
+        const int wm = wave / C::WN, wn = wave % C::WN;
+        const int32_t* rs = share_area<C>() + buf * share_ints<C>();
+        const int32_t* cs = rs + C::BM * C::WN;
+#pragma unroll
+        for (int i = 0; i < C::TM; i++) {
+            const int row = wm * C::WTM + i * 32 + (lane & 31);
+            int t = 0;
+#pragma unroll
+            for (int w = 0; w < C::WN; w++) t += rs[w * C::BM + row];
+            acc[i][0].rs = lane < 32 ? t : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int col = wn * C::WTN + j * 32 + (lane & 31);
+            int t = 0;
+#pragma unroll
+            for (int w = 0; w < C::WM; w++) t += cs[w * C::BN + col];
+            acc[0][j].cs = lane < 32 ? t : 0;
+        }
+    }
+};
+
+template <class P>
+struct shares_sums {
+    static constexpr bool value = false;
+};
+template <>
+struct shares_sums<PolicyI8QS> {
+    static constexpr bool value = true;
+};
+
 // FP8 full rate: v_mfma_scale_f32_32x32x64_f8f6f4 (both operands e4m3,
 // E8M0 scales 2^0), 32 K-bytes per lane per 64-K step.  Hardware decode is
 // OCP e4m3fn and the dot product is accumulated at reduced precision.
