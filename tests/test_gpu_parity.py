@@ -995,16 +995,18 @@ def _per_token_want(x, w, b, m, n, k):
 
 
 DECODE_EDGE = [(1, 100, 64), (3, 17, 128), (5, 33, 192), (17, 200, 1024), (31, 2304, 768),
-               (32, 768, 3072), (2, 768, 3072), (8, 3072, 768)]
+               (32, 768, 3072), (2, 768, 3072), (8, 3072, 768), (20, 100, 64), (24, 130, 128)]
 
 
 @pytest.mark.parametrize("rg", [None, 1, 3, 16])
 def test_decode_linear_edge_cases(ctx, rg):
     """The one-kernel decode linear (per-token quantize + INT8 GEMM +
     epilogue, M <= 32): ragged row groups and column blocks, one to sixteen
-    waves, a zero row (scale floor), a row holding NaN (skipped by the
-    absmax, coded 0), an outlier row; forced row-group sizes; and a
-    misaligned x, which takes the two-kernel path.  Bit-exact."""
+    waves, workgroups of several column blocks above 16 tokens (with fewer
+    waves than blocks at K = 64 and 128), a zero row (scale floor), a row
+    holding NaN (skipped by the absmax, coded 0), an outlier row; forced
+    row-group sizes; and a misaligned x, which takes the two-kernel path.
+    Bit-exact."""
     ctx.set_tuning(D.TUNE_DECODE_GROUP, -1 if rg is None else rg)
     try:
         _decode_edge_cases(ctx, rg)

@@ -6,8 +6,9 @@
 // bias epilogue with the token's scale (the per-token form of the R11 chain:
 // y = fl32(fl64(fl64(acc * sa[m]) * sw[n]) + b[n]), sa[m] = fl32(am / 127)).
 //
-// Workgroup (cb, rg) owns output columns [16 cb, 16 cb + 16) and token rows
-// [RG rg, RG rg + RG).  It needs its rows' full activation (the token scale
+// Workgroup (cb, rg) owns output columns [16 NCB cb, 16 NCB (cb + 1)) (NCB
+// 16-column blocks, one MFMA each per k-step) and token rows [RG rg, RG rg +
+// RG).  It needs its rows' full activation (the token scale
 // is the row's absmax over all of K) and its columns' full weight rows, so
 // it reads both itself and nothing crosses workgroups: no atomics, no
 // barrier, no scratch memory, and the result does not depend on scheduling.
@@ -20,7 +21,7 @@
 //     over the waves (LDS), then each wave quantizes its fragments in
 //     registers and runs its MFMAs.
 //   * The waves' INT32 partial tiles are summed exactly with LDS atomics and
-//     wave 0 runs the epilogue.
+//     wave c runs the epilogue of column block c.
 // Splitting the tokens into row groups keeps the activation bytes per
 // workgroup near its weight bytes (16 K each at RG = 4): a CU then moves
 // ~32 K bytes per workgroup whatever M is, instead of 4 M K.
@@ -74,6 +75,7 @@ __device__ __forceinline__ float amax4(float m, const float4 v) {
 // up to M = 16 in a kernel trace of both on one box.)
 constexpr int kChunks = 3;  // 16 rows * 3072 / (16 elements * 1024 threads) = 3
 
+template <int NCB>
 __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     const float* __restrict__ x, const uint8_t* __restrict__ W, int M, int N, int K, int ldk,
     int RG, int ncb, int ngr, const float* __restrict__ sw, const float* __restrict__ bias,
@@ -82,26 +84,30 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     __shared__ uint32_t s_am[16];
     __shared__ double s_inv[16];
     __shared__ float s_sa[16];
-    __shared__ int32_t s_acc[256];
+    __shared__ int32_t s_acc[256 * NCB];
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int nthreads = (int)blockDim.x;
     const int t = xcd_tile((int)blockIdx.x, ncb * ngr);
     const int cb = t / ngr, rg = t % ngr;
-    const int n0 = cb * 16, r0 = rg * RG;
+    const int n0 = cb * 16 * NCB, r0 = rg * RG;
     const int rows = M - r0 < RG ? M - r0 : RG;  // valid rows of this group (1 .. 16)
     const int nks = K / 64;
     const int lr = lane & 15, kg = lane >> 4;
     const int ks0 = wave * kKsw;
 
-    // weight fragments (B operand): column n0 + lr, bytes [64 ks + 16 kg, +16)
-    const int wcol = n0 + lr < N ? n0 + lr : N - 1;
-    const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + kg * 16;
-    v4i wf[kKsw];
+    // weight fragments (B operand): column n0 + 16 c + lr, bytes [64 ks + 16 kg, +16)
+    v4i wf[NCB][kKsw];
 #pragma unroll
-    for (int s = 0; s < kKsw; s++) {
-        const int ks = ks0 + s;
-        wf[s] = ks < nks ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64))
-                         : v4i{0, 0, 0, 0};
+    for (int c = 0; c < NCB; c++) {
+        const int wcol = n0 + 16 * c + lr < N ? n0 + 16 * c + lr : N - 1;
+        const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + kg * 16;
+#pragma unroll
+        for (int s = 0; s < kKsw; s++) {
+            const int ks = ks0 + s;
+            wf[c][s] = ks < nks
+                           ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64))
+                           : v4i{0, 0, 0, 0};
+        }
     }
     // activation chunks of the valid rows
     const int nchunks = nks * 4 * rows;
@@ -119,7 +125,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
             xv[j][q] = c < nchunks ? xp[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if (threadIdx.x < 16) s_am[threadIdx.x] = 0u;
-    for (int i = threadIdx.x; i < 256; i += nthreads) s_acc[i] = 0;
+    for (int i = threadIdx.x; i < 256 * NCB; i += nthreads) s_acc[i] = 0;
     __syncthreads();
     // row absmax from 0 (engine.tkv:272-276: NaN never compares greater;
     // fmaxf skips it, so the bits compared below are those of a finite or
@@ -156,7 +162,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     }
     __syncthreads();
 
-    v4i acc = {0, 0, 0, 0};
+    v4i acc[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; c++) acc[c] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < kKsw; s++) {
         const int ks = ks0 + s;
@@ -164,28 +172,41 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
             const v4i af = lr < rows
                                ? *reinterpret_cast<const v4i*>(s_a + (((ks * 4 + kg) * 16 + lr) << 4))
                                : v4i{0, 0, 0, 0};
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, wf[s], acc, 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < NCB; c++)
+                acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, wf[c][s], acc[c], 0, 0, 0);
         }
     }
-    // 16 x 16 result: lane holds column lane & 15, rows 4 (lane >> 4) + i
+    // 16 x 16 result per column block: lane holds column lane & 15, rows
+    // 4 (lane >> 4) + i
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        if (4 * kg + i < rows) atomicAdd(&s_acc[(4 * kg + i) * 16 + lr], acc[i]);
+    for (int c = 0; c < NCB; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * kg + i < rows) atomicAdd(&s_acc[c * 256 + (4 * kg + i) * 16 + lr], acc[c][i]);
     __syncthreads();
-    if (wave != 0) return;
-    const int col = n0 + lr;
-    if (col >= N) return;
-    const double swc = (double)sw[col];
-    const double bc = bias ? (double)bias[col] : 0.0;
+    auto store_block = [&](int c) {
+        const int col = n0 + 16 * c + lr;
+        if (col >= N) return;
+        const double swc = (double)sw[col];
+        const double bc = bias ? (double)bias[col] : 0.0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 4 * kg + i;
-        if (r < rows) {
-            double v = (double)s_acc[r * 16 + lr] * (double)s_sa[r];
-            v = v * swc;
-            v = v + bc;
-            __builtin_nontemporal_store((float)v, y + (int64_t)(r0 + r) * N + col);
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * kg + i;
+            if (r < rows) {
+                double v = (double)s_acc[c * 256 + r * 16 + lr] * (double)s_sa[r];
+                v = v * swc;
+                v = v + bc;
+                __builtin_nontemporal_store((float)v, y + (int64_t)(r0 + r) * N + col);
+            }
         }
+    };
+    if constexpr (NCB == 1) {
+        if (wave == 0) store_block(0);
+    } else {
+        // wave w stores column blocks w, w + waves, ... (a workgroup may have
+        // fewer waves than column blocks)
+        for (int c = wave; c < NCB; c += nthreads / 64) store_block(c);
     }
 }
 
@@ -218,13 +239,29 @@ int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
         ldk % 16 != 0 || ldk < k || !aligned(x, 16) || !aligned(w, 16) || n < 1 ||
         n >= (1ll << 28))
         return TKV_HIP_UNSUPPORTED;
-    const int64_t ncb = ceil_div(n, 16);
+    // 16-column blocks per workgroup.  Above 16 tokens a workgroup's row
+    // group is quantized once for several column blocks: 64 columns while
+    // their weight rows stay within 64 KB (K <= 1024), else 32 (cold calls at
+    // M = 32, interleaved rounds on one box: qkv 6.95 -> 6.76 us, mlp_up
+    // 7.08 -> 6.50, mlp_down 8.85 -> 8.44 with 32 columns and 11.0 with 64;
+    // at M = 16 two blocks measured 0.1-0.4 us slower than one).
+    const int ncols = m <= 16 ? 1 : (k <= 1024 ? 4 : 2);
+    const int64_t ncb = ceil_div(n, (int64_t)16 * ncols);
     const int rg = decode_rows_per_group(c, m, ncb, c->num_cus);
     const int64_t ngr = ceil_div(m, (int64_t)rg);
     const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
-    hipLaunchKernelGGL(k_decode_i8, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
-                       (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk, rg, (int)ncb, (int)ngr,
-                       scales_w, bias, y);
+    if (ncols == 4)
+        hipLaunchKernelGGL(k_decode_i8<4>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
+                           (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
+                           rg, (int)ncb, (int)ngr, scales_w, bias, y);
+    else if (ncols == 2)
+        hipLaunchKernelGGL(k_decode_i8<2>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
+                           (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
+                           rg, (int)ncb, (int)ngr, scales_w, bias, y);
+    else
+        hipLaunchKernelGGL(k_decode_i8<1>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
+                           (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
+                           rg, (int)ncb, (int)ngr, scales_w, bias, y);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
