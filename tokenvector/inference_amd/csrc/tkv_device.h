@@ -26,6 +26,21 @@ __device__ __forceinline__ int rne_clamp(double p, double lo, double hi) {
     return i < l ? l : (i > h ? h : i);
 }
 
+// clamp(int(round(x * inv)), -127, 127) for f32 x and inv.  Their product is
+// exact in f64, so this equals rne_clamp((double)x * inv, -127, 127) with
+// f32 operations only: one fma adds 1.5 * 2^23 to the exact product and
+// rounds once, to nearest even, onto the integer grid of [2^23, 2^24), which
+// is exact for |x * inv| < 2^22; the sum is clamped to 1.5 * 2^23 +- 127
+// before its bits are read, so larger products and infinities saturate, and
+// NaN gives 0, as the saturating conversion does.
+__device__ __forceinline__ int rne_clamp127_f32(float x, float inv) {
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23, bits 0x4B400000
+    const float r = __builtin_fmaf(x, inv, kMagic);
+    const float c = __builtin_amdgcn_fmed3f(r, kMagic - 127.0f, kMagic + 127.0f);
+    const int i = __float_as_int(c) - 0x4B400000;
+    return r != r ? 0 : i;
+}
+
 // e4m3 encode of the reference (types.tkv:154-191 with bias 7, 3 mantissa
 // bits, emax field 15, no inf, saturation code 0x7E) on the binary32 bits.
 // Its three departures from OCP e4m3fn are kept: |x| >= 248 -> 0x7E,
