@@ -29,24 +29,34 @@ __global__ void __launch_bounds__(256) k_fp8_ref_to_f16(const uint8_t* __restric
     }
 }
 
-static int decode_f16(Ctx* c, const uint8_t* src, int64_t bytes, int slot, uint8_t** out) {
-    void* d;
-    TKV_RC_TRY(ctx_workspace(c, slot, (size_t)bytes * 2, &d));
+static int decode_into(Ctx* c, const uint8_t* src, int64_t bytes, void* d) {
     const int64_t n16 = bytes / 16;  // rows are ldk (a multiple of 128) bytes
     const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(n16 > 0 ? n16 : 1, 256),
                                                       (int64_t)c->num_cus * 8);
     hipLaunchKernelGGL(k_fp8_ref_to_f16, dim3(grid), dim3(256), 0, c->stream, src, n16,
                        static_cast<uint8_t*>(d));
     TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+static int decode_f16(Ctx* c, const uint8_t* src, int64_t bytes, int slot, uint8_t** out) {
+    void* d;
+    TKV_RC_TRY(ctx_workspace(c, slot, (size_t)bytes * 2, &d));
+    TKV_RC_TRY(decode_into(c, src, bytes, d));
     *out = static_cast<uint8_t*>(d);
     return TKV_HIP_OK;
 }
 
 }  // namespace gemm
 
+int launch_fp8_ref_to_f16(Ctx* c, const uint8_t* src, int64_t bytes, void* dst) {
+    if (bytes % 16 != 0) return set_error(TKV_HIP_BAD_ARG, "fp8 decode: bytes not a multiple of 16");
+    return gemm::decode_into(c, src, bytes, dst);
+}
+
 int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n, int64_t k,
                    const float* scale_a, int64_t scale_a_stride, const float* scales_w,
-                   const float* bias, float* y, bool fast) {
+                   const float* bias, float* y, bool fast, const void* w16) {
     if (m <= 0 || n <= 0) return TKV_HIP_OK;
     TKV_RC_TRY(gemm::check_sizes(m, n, k, "FP8 GEMM"));
     if ((scales_w == nullptr) != (scale_a == nullptr))
@@ -57,12 +67,17 @@ int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_
     const uint8_t* ua = static_cast<const uint8_t*>(pa);
     const uint8_t* uw = static_cast<const uint8_t*>(pw);
     // Reference products: both operands decoded once into exact (pre-scaled)
-    // f16, then the f16 MFMA over rows of 2 ldk bytes.
+    // f16, then the f16 MFMA over rows of 2 ldk bytes.  A weight decoded in
+    // advance (w16) is used as it is when W needed no repack.
+    const bool have_w16 = w16 && pw == static_cast<const void*>(w) && ldk == k;
     auto run = [&](const auto& ep) -> int {
         if (fast) return gemm::launch_any<gemm::PolicyF8>(c, ua, uw, m, n, ldk, ep, y);
         uint8_t *ha, *hw;
         TKV_RC_TRY(gemm::decode_f16(c, ua, m * ldk, 10, &ha));
-        TKV_RC_TRY(gemm::decode_f16(c, uw, n * ldk, 11, &hw));
+        if (have_w16)
+            hw = static_cast<uint8_t*>(const_cast<void*>(w16));
+        else
+            TKV_RC_TRY(gemm::decode_f16(c, uw, n * ldk, 11, &hw));
         return gemm::launch_any<gemm::PolicyF16>(c, ha, hw, m, n, 2 * ldk, ep, y);
     };
     if (scales_w && scale_a_stride != 0)

@@ -22,6 +22,7 @@ struct Weight {
     int format = TKV_HIP_WEIGHT_INT8;
     int64_t n = 0, k = 0, ldk = 0;
     void* codes = nullptr;   // [n, ldk] int8 or e4m3 bytes, zero-padded
+    void* codes16 = nullptr; // WEIGHT_FP8: [n, ldk] halves, the codes' reference decode
     float* scales = nullptr; // [n] per-channel scales
     float* bias = nullptr;   // [n] or null
 };
@@ -79,6 +80,7 @@ static void weight_release(Weight* wt) {
     (void)hipSetDevice(wt->device);
     (void)hipDeviceSynchronize();
     if (wt->codes) (void)hipFree(wt->codes);
+    if (wt->codes16) (void)hipFree(wt->codes16);
     if (wt->scales) (void)hipFree(wt->scales);
     if (wt->bias) (void)hipFree(wt->bias);
     delete wt;
@@ -132,7 +134,7 @@ static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t
     TKV_RC_TRY(launch_quant_fp8_dynamic(c, x, m * k, ap, qa, false));
     return launch_gemm_f8(c, static_cast<uint8_t*>(qa), static_cast<uint8_t*>(wt->codes), m, wt->n,
                           k, &ap->scale, 0, wt->scales, wt->bias, y,
-                          wt->format == TKV_HIP_WEIGHT_FP8_FAST);
+                          wt->format == TKV_HIP_WEIGHT_FP8_FAST, wt->codes16);
 }
 
 // ---------------------------------------------------------------------------
@@ -232,6 +234,16 @@ int32_t tkv_hip_weight_create(int64_t ctx, const float* w, int64_t n, int64_t k,
                                w, n, k, wt->scales, static_cast<uint8_t*>(wt->codes), wt->ldk);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) rc = fail_hip(e, "fp8 weight pack", __FILE__, __LINE__);
+            // The reference-products GEMM multiplies the codes' exact f16
+            // decode: done here once instead of in every call.
+            if (rc == TKV_HIP_OK && format == TKV_HIP_WEIGHT_FP8) {
+                e = hipMalloc(&wt->codes16, (size_t)(n * wt->ldk) * 2);
+                if (e != hipSuccess)
+                    rc = fail_hip(e, "hipMalloc", __FILE__, __LINE__);
+                else
+                    rc = launch_fp8_ref_to_f16(c, static_cast<const uint8_t*>(wt->codes),
+                                               n * wt->ldk, wt->codes16);
+            }
         }
     }
     if (rc == TKV_HIP_OK) {

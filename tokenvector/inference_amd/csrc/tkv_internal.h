@@ -192,10 +192,16 @@ enum { EPI_PER_CHANNEL = 0, EPI_SYMMETRIC = 1, EPI_ACCUM_I32 = 2 };
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
                    const I8Epilogue& ep, void* y);
 // fast: full-rate FP8 MFMA (hardware OCP decode and rounding); otherwise the
-// reference decoder's products on f16 MFMA.
+// reference decoder's products on f16 MFMA.  w16, when given, is W already
+// decoded (launch_fp8_ref_to_f16 of its [n, k] rows, k a multiple of the GEMM
+// K step): the reference-products path then decodes only A.
 int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                    int64_t k, const float* scale_a, int64_t scale_a_stride,
-                   const float* scales_w, const float* bias, float* y, bool fast);
+                   const float* scales_w, const float* bias, float* y, bool fast,
+                   const void* w16 = nullptr);
+// The reference e4m3 decode of `bytes` codes (a multiple of 16) into halves
+// (exact, pre-scaled by 2^-8) at dst, on c's stream.
+int launch_fp8_ref_to_f16(Ctx* c, const uint8_t* src, int64_t bytes, void* dst);
 // QLinearMatMul (session.tkv:1992-2071) on packed codes: A [m,k], W [n,k]
 // (the node's B transposed), both with row stride k; y int8 [m,n].
 struct QLinearParams {
