@@ -49,6 +49,23 @@ static int decode_f16(Ctx* c, const uint8_t* src, int64_t bytes, int slot, uint8
 
 }  // namespace gemm
 
+int launch_gemm_f8_decoded(Ctx* c, const void* a16, const void* w16, int64_t m, int64_t n,
+                           int64_t k, const float* scale_a, const float* scales_w,
+                           const float* bias, float* y) {
+    if (m <= 0 || n <= 0) return TKV_HIP_OK;
+    TKV_RC_TRY(gemm::check_sizes(m, n, k, "FP8 GEMM"));
+    if (k % gemm::kBK != 0 || !aligned(a16, 16) || !aligned(w16, 16))
+        return set_error(TKV_HIP_BAD_ARG, "FP8 GEMM (decoded): K or alignment");
+    const auto* ha = static_cast<const uint8_t*>(a16);
+    const auto* hw = static_cast<const uint8_t*>(w16);
+    if (scales_w)
+        return gemm::launch_any<gemm::PolicyF16>(
+            c, ha, hw, m, n, 2 * k, gemm::EpiF8<true, false>{scale_a, 0, scales_w, bias}, y);
+    return gemm::launch_any<gemm::PolicyF16>(c, ha, hw, m, n, 2 * k,
+                                             gemm::EpiF8<false, false>{nullptr, 0, nullptr, bias},
+                                             y);
+}
+
 int launch_fp8_ref_to_f16(Ctx* c, const uint8_t* src, int64_t bytes, void* dst) {
     if (bytes % 16 != 0) return set_error(TKV_HIP_BAD_ARG, "fp8 decode: bytes not a multiple of 16");
     return gemm::decode_into(c, src, bytes, dst);
@@ -56,7 +73,7 @@ int launch_fp8_ref_to_f16(Ctx* c, const uint8_t* src, int64_t bytes, void* dst) 
 
 int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n, int64_t k,
                    const float* scale_a, int64_t scale_a_stride, const float* scales_w,
-                   const float* bias, float* y, bool fast, const void* w16) {
+                   const float* bias, float* y, bool fast) {
     if (m <= 0 || n <= 0) return TKV_HIP_OK;
     TKV_RC_TRY(gemm::check_sizes(m, n, k, "FP8 GEMM"));
     if ((scales_w == nullptr) != (scale_a == nullptr))
@@ -67,17 +84,12 @@ int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_
     const uint8_t* ua = static_cast<const uint8_t*>(pa);
     const uint8_t* uw = static_cast<const uint8_t*>(pw);
     // Reference products: both operands decoded once into exact (pre-scaled)
-    // f16, then the f16 MFMA over rows of 2 ldk bytes.  A weight decoded in
-    // advance (w16) is used as it is when W needed no repack.
-    const bool have_w16 = w16 && pw == static_cast<const void*>(w) && ldk == k;
+    // f16, then the f16 MFMA over rows of 2 ldk bytes.
     auto run = [&](const auto& ep) -> int {
         if (fast) return gemm::launch_any<gemm::PolicyF8>(c, ua, uw, m, n, ldk, ep, y);
         uint8_t *ha, *hw;
         TKV_RC_TRY(gemm::decode_f16(c, ua, m * ldk, 10, &ha));
-        if (have_w16)
-            hw = static_cast<uint8_t*>(const_cast<void*>(w16));
-        else
-            TKV_RC_TRY(gemm::decode_f16(c, uw, n * ldk, 11, &hw));
+        TKV_RC_TRY(gemm::decode_f16(c, uw, n * ldk, 11, &hw));
         return gemm::launch_any<gemm::PolicyF16>(c, ha, hw, m, n, 2 * ldk, ep, y);
     };
     if (scales_w && scale_a_stride != 0)

@@ -131,10 +131,19 @@ static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t
     }
     if (act_mode != TKV_HIP_ACT_PER_TENSOR)
         return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: FP8 weights take per-tensor activations");
+    if (wt->codes16) {
+        // reference products: the activation's codes go straight to their
+        // f16 decode, which the GEMM multiplies with the weight's
+        void* ha;
+        TKV_RC_TRY(ctx_workspace(c, 10, (size_t)(m * k) * 2, &ha));
+        TKV_RC_TRY(launch_quant_fp8_dynamic_f16(c, x, m * k, ap, ha));
+        return launch_gemm_f8_decoded(c, ha, wt->codes16, m, wt->n, k, &ap->scale, wt->scales,
+                                      wt->bias, y);
+    }
     TKV_RC_TRY(launch_quant_fp8_dynamic(c, x, m * k, ap, qa, false));
     return launch_gemm_f8(c, static_cast<uint8_t*>(qa), static_cast<uint8_t*>(wt->codes), m, wt->n,
                           k, &ap->scale, 0, wt->scales, wt->bias, y,
-                          wt->format == TKV_HIP_WEIGHT_FP8_FAST, wt->codes16);
+                          wt->format == TKV_HIP_WEIGHT_FP8_FAST);
 }
 
 // ---------------------------------------------------------------------------

@@ -24,6 +24,7 @@
 #include <float.h>
 #include <cstdlib>
 
+#include "gemm_tile.h"
 #include "tkv_device.h"
 #include "tkv_internal.h"
 #include "tkv_reduce.h"
@@ -902,19 +903,37 @@ int launch_dequant_i8(Ctx* c, const void* q, bool in_i32, int64_t rows, int64_t 
 // reference's int32 codes (byte - 128).  With `scaled` the input is first
 // multiplied by fl32(1 / scale) in f32 (extension for per-tensor FP8).
 // ---------------------------------------------------------------------------
-// Four packed e4m3 bytes (element 0 in bits 7:0) as raw bytes, or as the
-// reference's int32 codes (byte - 128).
-template <bool OUT_I32>
+// Four packed e4m3 bytes (element 0 in bits 7:0) as raw bytes (FP8_BYTES),
+// as the reference's int32 codes (byte - 128, FP8_I32), or as their exact
+// reference decode in f16, pre-scaled by 2^-8 (FP8_F16: what the
+// reference-products GEMM multiplies).
+enum { FP8_BYTES = 0, FP8_I32 = 1, FP8_F16 = 2 };
+
+template <int OUT>
 __device__ __forceinline__ void store_fp8x4(void* q, int64_t i4, uint32_t w) {
-    if (OUT_I32)
+    if constexpr (OUT == FP8_I32)
         reinterpret_cast<int4*>(q)[i4] =
             make_int4((int)(w & 0xffu) - 128, (int)((w >> 8) & 0xffu) - 128,
                       (int)((w >> 16) & 0xffu) - 128, (int)(w >> 24) - 128);
+    else if constexpr (OUT == FP8_F16)
+        reinterpret_cast<uint2*>(q)[i4] =
+            make_uint2(gemm::dec2_f16(__builtin_amdgcn_perm(0u, w, 0x0c010c00u)),
+                       gemm::dec2_f16(__builtin_amdgcn_perm(0u, w, 0x0c030c02u)));
     else
         reinterpret_cast<uint32_t*>(q)[i4] = w;
 }
 
-template <bool OUT_I32>
+template <int OUT>
+__device__ __forceinline__ void store_fp8x1(void* q, int64_t j, uint32_t e) {
+    if constexpr (OUT == FP8_I32)
+        reinterpret_cast<int32_t*>(q)[j] = (int)e - 128;
+    else if constexpr (OUT == FP8_F16)
+        reinterpret_cast<uint16_t*>(q)[j] = (uint16_t)(gemm::dec2_f16(e) & 0xffffu);
+    else
+        reinterpret_cast<uint8_t*>(q)[j] = (uint8_t)e;
+}
+
+template <int OUT>
 __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__ x, int64_t n,
                                                        int vec,
                                                        const tkv_hip_qparams_dev* __restrict__ sp,
@@ -949,7 +968,7 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
             for (int u = 0; u < kUnroll; u++) w[u] = e4m3_encode4(v[u].x, v[u].y, v[u].z, v[u].w);
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) store_fp8x4<OUT_I32>(q, i + u * stride, w[u]);
+        for (int u = 0; u < kUnroll; u++) store_fp8x4<OUT>(q, i + u * stride, w[u]);
     }
     for (; i < n4; i += stride) {
         float4 v = ld4(x4 + i);
@@ -959,23 +978,20 @@ __global__ __launch_bounds__(kBlock) void k_fp8_encode(const float* __restrict__
             v.z *= mul;
             v.w *= mul;
         }
-        store_fp8x4<OUT_I32>(q, i, e4m3_encode4(v.x, v.y, v.z, v.w));
+        store_fp8x4<OUT>(q, i, e4m3_encode4(v.x, v.y, v.z, v.w));
     }
     for (int64_t j = n4 * 4 + tid; j < n; j += stride) {
         float v = x[j];
         if (scaled) v *= mul;
-        uint32_t e = e4m3_encode1(v);
-        if (OUT_I32)
-            reinterpret_cast<int32_t*>(q)[j] = (int)e - 128;
-        else
-            reinterpret_cast<uint8_t*>(q)[j] = (uint8_t)e;
+        store_fp8x1<OUT>(q, j, e4m3_encode1(v));
     }
 }
 
-int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* scaled,
-                      void* q, bool out_i32) {
+static int launch_fp8_encode_as(Ctx* c, const float* x, int64_t n,
+                                const tkv_hip_qparams_dev* scaled, void* q, int out) {
     if (n <= 0) return TKV_HIP_OK;
-    int vec = (aligned(x, 16) && aligned(q, out_i32 ? 16 : 4)) ? 1 : 0;
+    const int qalign = out == FP8_I32 ? 16 : (out == FP8_F16 ? 8 : 4);
+    int vec = (aligned(x, 16) && aligned(q, qalign)) ? 1 : 0;
     // The e4m3 encode costs more ALU work per element than the int8 quantize
     // (~11 operations per element: the magnitude clamps in front of the
     // hardware conversion): three blocks per CU overlap it with the loads at
@@ -987,14 +1003,22 @@ int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_d
     const int64_t cap = (int64_t)c->num_cus * (vec ? 3 : 16);
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
-    if (out_i32)
-        hipLaunchKernelGGL(k_fp8_encode<true>, dim3((unsigned)blocks), dim3(kBlock), 0, c->stream,
-                           x, n, vec, scaled, q);
+    if (out == FP8_I32)
+        hipLaunchKernelGGL(k_fp8_encode<FP8_I32>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, scaled, q);
+    else if (out == FP8_F16)
+        hipLaunchKernelGGL(k_fp8_encode<FP8_F16>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                           c->stream, x, n, vec, scaled, q);
     else
-        hipLaunchKernelGGL(k_fp8_encode<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
+        hipLaunchKernelGGL(k_fp8_encode<FP8_BYTES>, dim3((unsigned)blocks), dim3(kBlock), 0,
                            c->stream, x, n, vec, scaled, q);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
+}
+
+int launch_fp8_encode(Ctx* c, const float* x, int64_t n, const tkv_hip_qparams_dev* scaled,
+                      void* q, bool out_i32) {
+    return launch_fp8_encode_as(c, x, n, scaled, q, out_i32 ? FP8_I32 : FP8_BYTES);
 }
 
 // Per-tensor FP8 activation quantize: the MM_FP8 scale, then the scaled
@@ -1003,6 +1027,14 @@ int launch_quant_fp8_dynamic(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_
                              bool out_i32) {
     TKV_RC_TRY(launch_minmax_tensor(c, x, n, MM_FP8, TKV_HIP_RECIPE_PRIMARY, p));
     return launch_fp8_encode(c, x, n, p, q, out_i32);
+}
+
+// The same, writing the codes' reference decode in f16 (for the
+// reference-products GEMM) instead of the codes.
+int launch_quant_fp8_dynamic_f16(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_dev* p,
+                                 void* h16) {
+    TKV_RC_TRY(launch_minmax_tensor(c, x, n, MM_FP8, TKV_HIP_RECIPE_PRIMARY, p));
+    return launch_fp8_encode_as(c, x, n, p, h16, FP8_F16);
 }
 
 template <bool IN_I32>

@@ -152,6 +152,10 @@ int launch_quant_i8_dynamic(Ctx* c, const float* x, int64_t n, int recipe,
 // Per-tensor FP8 scale (MM_FP8) + scaled e4m3 encode; *p = QuantParams.
 int launch_quant_fp8_dynamic(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_dev* p,
                              void* q, bool out_i32);
+// The same, writing each code's exact reference decode as f16 (pre-scaled by
+// 2^-8, 2 bytes per element, 8-byte aligned h16) instead of the code.
+int launch_quant_fp8_dynamic_f16(Ctx* c, const float* x, int64_t n, tkv_hip_qparams_dev* p,
+                                 void* h16);
 int launch_quant_rows(Ctx* c, const float* x, int64_t rows, int64_t cols, int mode,
                       const float* scales_in, void* q, bool out_i32, float* scales_out,
                       tkv_hip_qparams_dev* row_params, int symmetric);
@@ -192,16 +196,19 @@ enum { EPI_PER_CHANNEL = 0, EPI_SYMMETRIC = 1, EPI_ACCUM_I32 = 2 };
 int launch_gemm_i8(Ctx* c, const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
                    const I8Epilogue& ep, void* y);
 // fast: full-rate FP8 MFMA (hardware OCP decode and rounding); otherwise the
-// reference decoder's products on f16 MFMA.  w16, when given, is W already
-// decoded (launch_fp8_ref_to_f16 of its [n, k] rows, k a multiple of the GEMM
-// K step): the reference-products path then decodes only A.
+// reference decoder's products on f16 MFMA.
 int launch_gemm_f8(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, int64_t n,
                    int64_t k, const float* scale_a, int64_t scale_a_stride,
-                   const float* scales_w, const float* bias, float* y, bool fast,
-                   const void* w16 = nullptr);
+                   const float* scales_w, const float* bias, float* y, bool fast);
 // The reference e4m3 decode of `bytes` codes (a multiple of 16) into halves
 // (exact, pre-scaled by 2^-8) at dst, on c's stream.
 int launch_fp8_ref_to_f16(Ctx* c, const uint8_t* src, int64_t bytes, void* dst);
+// The reference-products FP8 GEMM on operands already decoded that way:
+// a16 [m, k] and w16 [n, k] halves, k a multiple of the GEMM K step, rows
+// 16-byte aligned; per-tensor scale_a, per-channel scales_w, bias optional.
+int launch_gemm_f8_decoded(Ctx* c, const void* a16, const void* w16, int64_t m, int64_t n,
+                           int64_t k, const float* scale_a, const float* scales_w,
+                           const float* bias, float* y);
 // QLinearMatMul (session.tkv:1992-2071) on packed codes: A [m,k], W [n,k]
 // (the node's B transposed), both with row stride k; y int8 [m,n].
 struct QLinearParams {
