@@ -161,6 +161,22 @@ static void device_checks() {
         CHECK(tkv_hip_memcpy_d2h(ctx, yb.data(), dy2, m * n * 4) == TKV_HIP_OK, "d2h y2");
         CHECK(memcmp(ya.data(), yb.data(), m * n * 4) == 0, "static entry equals linear_forward");
     }
+    // FP8 weights: the reference-products handle (codes plus their f16
+    // decode) and the full-rate one, per-tensor activations
+    for (int32_t fmt : {TKV_HIP_WEIGHT_FP8, TKV_HIP_WEIGHT_FP8_FAST}) {
+        int64_t wf = 0;
+        CHECK(tkv_hip_weight_create(ctx, (const float*)dw, n, k, (const float*)db, fmt, &wf) ==
+                  TKV_HIP_OK,
+              "fp8 weight_create");
+        CHECK(tkv_hip_linear_forward(ctx, wf, (const float*)dx, m, TKV_HIP_ACT_PER_TENSOR,
+                                     (float*)dy) == TKV_HIP_OK,
+              "fp8 linear_forward");
+        CHECK(tkv_hip_linear_forward(ctx, wf, (const float*)dx, m, TKV_HIP_ACT_PER_TOKEN,
+                                     (float*)dy) == TKV_HIP_UNSUPPORTED,
+              "fp8 linear_forward refuses per-token activations");
+        CHECK(tkv_hip_ctx_synchronize(ctx) == TKV_HIP_OK, "fp8 synchronize");
+        CHECK(tkv_hip_weight_free(wf) == TKV_HIP_OK, "fp8 weight_free");
+    }
     // tuning overrides: every configuration of the tiled GEMM on one product
     for (int cfg = 0; cfg <= 11; cfg++) {
         CHECK(tkv_hip_ctx_set_tuning(ctx, TKV_HIP_TUNE_GEMM_CFG, cfg) == TKV_HIP_OK, "set cfg");
