@@ -21,7 +21,7 @@
 //     over the waves (LDS), then each wave quantizes its fragments in
 //     registers and runs its MFMAs.
 //   * The waves' INT32 partial tiles are summed exactly with LDS atomics and
-//     wave c runs the epilogue of column block c.
+//     wave c % waves runs the epilogue of column block c.
 // Splitting the tokens into row groups keeps the activation bytes per
 // workgroup near its weight bytes (16 K each at RG = 4): a CU then moves
 // ~32 K bytes per workgroup whatever M is, instead of 4 M K.

@@ -418,9 +418,10 @@ struct PolicyI8Q {
 // in LDS (publish, before that slice's barrier); after the barrier every wave
 // adds the partials of its rows and columns (gather), which leaves
 // acc[i][0].rs / acc[0][j].cs in PolicyI8Q's form (a lane's value plus that
-// of lane ^ 32 is the full sum).  Two LDS areas alternate by tile: a wave
-// can only write the next tile's partials after every wave has passed that
-// tile's first barrier, i.e. finished reading this tile's.
+// of lane ^ 32 is the full sum).  Two LDS areas alternate by tile: tile t's
+// area is written again only at tile t + 2's last slice, which a wave reaches
+// only after every wave has passed tile t + 1's barriers, i.e. has finished
+// reading tile t's sums.
 struct PolicyI8QS : PolicyI8Q {
     template <class C>
     static constexpr int share_ints() { return C::BM * C::WN + C::BN * C::WM; }
