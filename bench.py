@@ -14,7 +14,8 @@ Infinity Cache), all resident before timing.
 
 `value` = GEMM ops of the step (2*M*N*K summed, 1.3916e12) / step time.
 The JSON line also carries the INT8 GEMM kernel's roofline (achieved from
-HIP events around every GEMM launch in the timed region), the config-2
+HIP events around one GEMM launch per timed step, the four shapes in
+turn), the config-2
 quantize / calibrate bandwidths, and the CPU baseline (the oracle's scalar
 restatement of the reference loops, on a bounded sample).
 """
@@ -99,44 +100,54 @@ def bench_step(ctx, D, G, steps, warmup):
 
     ops_step = sum(2.0 * M * n * k for (_, n, k) in SHAPES) * LAYERS
     n_gemm = LAYERS * len(SHAPES)
-    # HIP events bracket the four GEMMs of one layer per timed step, the layer
-    # rotating with the step: each event record is a marker packet that costs
-    # a few microseconds of stream time, so bracketing all 48 launches would
-    # add ~12% to the step it measures.
-    ev_pairs = [(D.Event(), D.Event()) for _ in range(len(SHAPES) * steps)]
+    # HIP events bracket one GEMM per timed step, the shape cycling with the
+    # step (s % 4) and the layer rotating (s % 12), so every shape gets
+    # steps / 4 samples: each event record is a marker packet that costs a few
+    # microseconds of stream time (bracketing all 48 launches added ~12% to
+    # the step, one layer's four launches ~1-3%).  With fewer steps than
+    # shapes, all four launches of one layer are bracketed per step.
+    per_step = 1 if steps >= len(SHAPES) else len(SHAPES)
+    ev_pairs = [(D.Event(), D.Event()) for _ in range(per_step * steps)]
+    ev_shape = []
 
-    def step(record=None, layer=-1):
+    def step(record=None, layer=-1, shapes=()):
         for l, lin in enumerate(layers):
             for j, (name, n, k, q, dx, dy, qa, db) in enumerate(lin):
                 p = params[j]
                 # calibrate_minmax + quantize_int8_symmetric (device, no sync)
                 D.quantize_int8_dynamic_tensor(ctx, dx, M * k, qa, p)
-                if l == layer:
-                    record[j][0].record(ctx)
+                mark = l == layer and j in shapes
+                if mark:
+                    record[shapes.index(j)][0].record(ctx)
                 # INT8 GEMM + dequant (scale_a from the calibration) + bias
                 D.matmul_int8(ctx, qa, q.codes, M, n, k, p.ptr, 0, 0.0, q.scales, q.bias, dy)
-                if l == layer:
-                    record[j][1].record(ctx)
+                if mark:
+                    record[shapes.index(j)][1].record(ctx)
 
     for _ in range(warmup):
         step()
     ctx.synchronize()
     t_start = time.perf_counter()
     for s in range(steps):
-        step(ev_pairs[s * len(SHAPES):(s + 1) * len(SHAPES)], s % LAYERS)
+        shapes = (s % len(SHAPES),) if per_step == 1 else tuple(range(len(SHAPES)))
+        ev_shape.extend(shapes)
+        step(ev_pairs[s * per_step:(s + 1) * per_step], s % LAYERS, shapes)
     ctx.synchronize()
     t_end = time.perf_counter()
     ms_per_step = (t_end - t_start) * 1000.0 / steps
     gemm_ms = [a.elapsed_ms(b) for (a, b) in ev_pairs]
-    avg_gemm_ms = float(np.mean(gemm_ms))
+    shape_ms = [float(np.mean([t for t, j in zip(gemm_ms, ev_shape) if j == js]))
+                for js in range(len(SHAPES))]
+    # the mean launch over the four shapes, each weighted equally (as the
+    # step runs them), so uneven sample counts do not bias it
+    avg_gemm_ms = float(np.mean(shape_ms))
     ops_per_launch = ops_step / n_gemm
     bytes_per_launch = float(np.mean([gemm_bytes(M, n, k) for (_, n, k) in SHAPES]))
     achieved_tops = ops_per_launch / (avg_gemm_ms * 1e-3) / 1e12
     achieved_gbps = bytes_per_launch / (avg_gemm_ms * 1e-3) / 1e9
     per_shape = {}
     for j, (name, n, k) in enumerate(SHAPES):
-        t = [gemm_ms[s * len(SHAPES) + j] for s in range(steps)]
-        tm = float(np.mean(t))
+        tm = shape_ms[j]
         ops = 2.0 * M * n * k
         ceil = min(PEAK_INT8_TOPS, ops / gemm_bytes(M, n, k) * PEAK_HBM_GBPS * 1e9 / 1e12)
         per_shape[name] = {"us": round(tm * 1e3, 2), "tops": round(ops / (tm * 1e-3) / 1e12, 1),
@@ -612,7 +623,7 @@ def cpu_baseline(rows_single=2048, rows_all=M):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=2048,
