@@ -39,6 +39,7 @@ PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
 PEAK_F16_TFLOPS = 2500.0     # MI355X dense FP16 MFMA
 PEAK_HBM_GBPS = 8000.0       # MI355X HBM3E
 PEAK_F64_TFLOPS = 78.6       # MI355X FP64 matrix (v_mfma_f64)
+PEAK_VALU_Q8_TOPS = 1258.3   # Q8_0 GEMM: 2 f32 VALU ops per 32 MACs, 256 CU x 4 SIMD x 16 lanes x 2.4 GHz
 
 
 def log(*a):
@@ -49,7 +50,7 @@ def gemm_bytes(m, n, k):
     return m * k + n * k + 8 * n + 4 * m * n
 
 
-SECTIONS = ("step", "quant", "fp8", "decode", "qlinear", "int4")
+SECTIONS = ("step", "quant", "fp8", "decode", "qlinear", "q8_0", "int4")
 
 
 def run_gpu(steps, warmup, sections=SECTIONS):
@@ -66,6 +67,7 @@ def run_gpu(steps, warmup, sections=SECTIONS):
     for name, fn in (("quant", lambda: bench_quant(ctx, D, G)), ("fp8", lambda: bench_fp8(ctx, D, G)),
                      ("decode", lambda: bench_decode(ctx, D, G)),
                      ("qlinear", lambda: bench_qlinear(ctx, D)),
+                     ("q8_0", lambda: bench_q8_0(ctx, D)),
                      ("int4", lambda: bench_int4(ctx, D, G))):
         if name in sections:
             log(f"bench section {name}")
@@ -264,6 +266,46 @@ def bench_qlinear(ctx, D, m=M, reps=20):
                 buf.close()
         w.close()
     out["note"] = "int8 in / int8 out, zero points and requantization fused in the epilogue"
+    return out
+
+
+def bench_q8_0(ctx, D, m=M, reps=20):
+    """GGUF Q8_0 weights on the INT8 GEMM (extension; the reference decodes
+    Q8_0 to f32, gguf.tkv:284-290) on the four GPT-2 shapes: int8 activation
+    codes with per-token scales, each 32-element group's exact INT32 dot
+    scaled by its f16 d with one fma.  The conversion and fma per output and
+    group bound it: 2 VALU ops per 32 MACs at 256 CUs x 4 SIMDs x 16 lanes x
+    2.4 GHz = 1258 TOPS.  Weights come from raw blocks through
+    tkv_hip_weight_create_gguf_q8_0; two input sets are cycled."""
+    rng = np.random.default_rng(11)
+    out = {}
+    for (name, n, k) in SHAPES:
+        kb = k // 32
+        raw = np.zeros((n, kb, 34), np.uint8)
+        d = rng.integers(0x1C00, 0x2C00, (n, kb))
+        raw[:, :, 0] = d & 255
+        raw[:, :, 1] = d >> 8
+        raw[:, :, 2:] = rng.integers(0, 256, (n, kb, 32))
+        dr = D.DeviceBuffer.from_host(ctx, raw.reshape(-1))
+        wt = D.QuantizedLinear.from_gguf_q8_0(ctx, dr, n, k)
+        dr.close()
+        sa = D.DeviceBuffer.from_host(ctx, (rng.random(m) * 0.01 + 1e-3).astype(np.float32))
+        sets = [(D.DeviceBuffer.from_host(ctx, rng.integers(-127, 128, m * k).astype(np.int8)),
+                 D.DeviceBuffer.empty(ctx, (m, n), np.float32)) for _ in range(2)]
+        us = _time_us(ctx, D, lambda i: D.matmul_q8_0(
+            ctx, sets[i % 2][0], wt.codes, wt.scales, m, n, k, sa, 1, None, sets[i % 2][1]), reps)
+        ops = 2.0 * m * n * k
+        tops = ops / (us * 1e-6) / 1e12
+        out[f"{name}_m{m}"] = {"us": round(us, 2), "tops": round(tops, 1),
+                               "frac_of_valu_bound": round(tops / PEAK_VALU_Q8_TOPS, 3),
+                               "frac_of_int8_peak": round(tops / PEAK_INT8_TOPS, 3)}
+        for t in sets:
+            for buf in t:
+                buf.close()
+        sa.close()
+        wt.close()
+    out["note"] = ("k_gemm_q8: group-scaled INT8 MFMA, bound by the per-group f32 conversion + fma "
+                   "(1258 TOPS), not by the MFMA peak")
     return out
 
 

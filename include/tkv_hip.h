@@ -506,6 +506,35 @@ int32_t tkv_hip_dev_matmul_int4_grouped(int64_t ctx, const float* a, const uint8
 int32_t tkv_hip_dev_dequantize_gguf(int64_t ctx, const uint8_t* raw, int64_t n, int32_t dtype,
                                     float* out);
 
+/* ---- GGUF Q8_0 weights on the INT8 GEMM (extension) ------------------- */
+/* No counterpart in the reference, which decodes Q8_0 blocks to f32
+ * (_dequant_tensor, gguf.tkv:284-290) before any matmul.  A Q8_0 weight
+ * [N, K] (N rows of K / 32 blocks of 34 bytes: f16 d, 32 int8 q) becomes
+ * int8 codes [N, K] and f32 group scales [N, K / 32], and multiplies the
+ * int8 codes a [M, K] of an activation whose scale is sa:
+ *   dot_g = sum over block g's 32 k of a[m, k] q[n, k]          (exact)
+ *   acc   = 0;  acc = fmaf((float)dot_g, d[n, g], acc)   g = 0, 1, ... in order
+ *   y     = fl32(fl64(fl64(acc) * sa) + bias[n])              (bias 0 if NULL)
+ * Against the reference's decode-then-multiply of the float activation x,
+ * the int8 activation codes contribute at most (sa / 2) sum_k |d q[n, k]|
+ * per output, and the f32 chain one rounding per group. */
+#define TKV_HIP_WEIGHT_Q8_0 3
+/* Weight handle from raw Q8_0 blocks (device bytes, row-major) for
+ * tkv_hip_linear_forward: either act_mode, the activation quantized as for
+ * INT8 weights (K % 128 == 0 there).  K % 32 != 0: BAD_ARG.
+ * tkv_hip_weight_info returns the group scales [N, k / 32] as `scales`
+ * (k = the codes' padded row stride). */
+int32_t tkv_hip_weight_create_gguf_q8_0(int64_t ctx, const uint8_t* raw, int64_t n, int64_t k,
+                                        const float* bias, int64_t* handle_out);
+/* The GEMM on device buffers: a int8 [M, K], codes int8 [N, K], group_scales
+ * f32 [N, K / 32] (each 16-byte aligned), sa = scale_a[m * scale_a_stride]
+ * (stride 0: per tensor, 1: per token).  K not a positive multiple of 128:
+ * UNSUPPORTED. */
+int32_t tkv_hip_dev_matmul_q8_0(int64_t ctx, const int8_t* a, const int8_t* codes,
+                                const float* group_scales, int64_t m, int64_t n, int64_t k,
+                                const float* scale_a, int64_t scale_a_stride, const float* bias,
+                                float* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -114,6 +114,7 @@ def _declare(L: C.CDLL) -> None:
         "tkvo_matmul_int4_grouped": (I32, [P, P, P, I64, P, I64, I64, I64, I64, P, I64, P]),
         "tkvo_f16_to_f32": (F32, [I64]),
         "tkvo_dequantize_gguf": (I32, [P, I64, I64, I32, P]),
+        "tkvo_matmul_q8_0": (I32, [P, P, I64, P, I64, P, I64, P, I64, I64, I64]),
         "tkvo_lcg31": (I64, [I64]),
         "tkvo_gi_noise": (None, [P, I64, I64, F64]),
         "tkvo_add_outliers": (None, [P, I64, I64, I64, I64, F64]),
@@ -556,3 +557,23 @@ def dequantize_gguf(raw, n: int, dtype: int) -> np.ndarray:
     if rc != 0:
         raise ValueError("unsupported dtype or raw too short")
     return y[: int(n)]
+
+
+def matmul_q8_0(a, raw, sa, m: int, n: int, k: int, bias=None) -> np.ndarray:
+    """Q8_0 weights (raw blocks, n rows of k / 32) on int8 activation codes
+    a [m, k] with scale sa (one value: per tensor; m values: per token).
+    Extension with no reference counterpart: acc = fmaf chain over the groups
+    of (float)dot_g * d, y = fl32(fl64(acc) * sa + b)."""
+    A = np.ascontiguousarray(a, dtype=np.int32).reshape(-1)
+    r = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    s = np.ascontiguousarray(np.atleast_1d(sa), dtype=np.float32)
+    if s.size not in (1, m):
+        raise ValueError("sa: one value or one per row")
+    stride = 0 if s.size == 1 else 1
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    y = np.zeros((max(int(m), 1), max(int(n), 1)), np.float32)
+    rc = lib().tkvo_matmul_q8_0(_p(A), _p(r), r.size, _p(s), stride, None if b is None else _p(b),
+                                0 if b is None else b.size, _p(y), int(m), int(n), int(k))
+    if rc != 0:
+        raise ValueError("k % 32 != 0 or raw too short")
+    return y[: int(m), : int(n)]

@@ -289,6 +289,19 @@ static void check_int4_gguf(void) {
     float out[32];
     CHECK(tkvo_dequantize_gguf(blk, 34, 32, 8, out) == 0, "gguf q8_0 rc");
     for (int i = 0; i < 32; i++) CHECK(out[i] == (float)i, "gguf q8_0 values");
+    /* Q8_0 linear on int8 codes: one row of ones against the block above
+     * (d = 1): sum 0..31 = 496, times sa = 0.5, plus bias 1 */
+    {
+        int32_t ones[32];
+        for (int i = 0; i < 32; i++) ones[i] = 1;
+        const float sa_q8 = 0.5f, b_q8 = 1.0f;
+        float yq;
+        CHECK(tkvo_matmul_q8_0(ones, blk, 34, &sa_q8, 0, &b_q8, 1, &yq, 1, 1, 32) == 0,
+              "q8_0 matmul rc");
+        CHECK(yq == 249.0f, "q8_0 matmul value");
+        CHECK(tkvo_matmul_q8_0(ones, blk, 33, &sa_q8, 0, NULL, 0, &yq, 1, 1, 32) != 0,
+              "q8_0 matmul short raw");
+    }
     free(y);
     free(a2);
     free(ap);

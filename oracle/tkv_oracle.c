@@ -1157,6 +1157,40 @@ int32_t tkvo_dequantize_gguf(const uint8_t* raw, int64_t nraw, int64_t n, int32_
     return 0;
 }
 
+/* Q8_0 weights on int8 activation codes: an extension with no counterpart
+ * in the reference (it decodes Q8_0 blocks to f32 with the loop above,
+ * gguf.tkv:284-290, and multiplies in float).  raw holds n rows of k / 32
+ * Q8_0 blocks (f16 d, 32 int8 q: the bytes tkvo_dequantize_gguf reads);
+ * a[m, k] are int8 activation codes with scale sa[m * sa_stride]:
+ *   dot_g = sum over block g's 32 k of a[m, k] q[n, k]        (exact integer)
+ *   acc   = 0;  acc = fmaf((float)dot_g, d[n, g], acc)   g = 0, 1, ... in order
+ *   y     = fl32(fl64(fl64(acc) * sa) + b[n])              (b = 0 without bias)
+ * k % 32 != 0 or raw too short: TKVO_ERR_ARG. */
+int32_t tkvo_matmul_q8_0(const int32_t* a, const uint8_t* raw, int64_t nraw, const float* sa,
+                         int64_t sa_stride, const float* bias, int64_t nbias, float* y,
+                         int64_t m, int64_t n, int64_t k) {
+    if (m < 0 || n < 0 || k <= 0 || k % 32 != 0 || sa_stride < 0 || sa_stride > 1) return TKVO_ERR_ARG;
+    const int64_t kb = k / 32;
+    if (nraw < n * kb * 34) return TKVO_ERR_ARG;
+    for (int64_t i = 0; i < m; i++) {
+        const double s = (double)sa[i * sa_stride];
+        for (int64_t j = 0; j < n; j++) {
+            float acc = 0.0f;
+            for (int64_t g = 0; g < kb; g++) {
+                const uint8_t* p = raw + (j * kb + g) * 34;
+                const float d = tkvo_f16_to_f32((int64_t)p[0] | (int64_t)p[1] << 8);
+                int32_t dot = 0;
+                for (int t = 0; t < 32; t++) dot += a[i * k + g * 32 + t] * (int32_t)(int8_t)p[2 + t];
+                acc = fmaf((float)dot, d, acc);
+            }
+            double v = (double)acc * s;
+            v = v + (j < nbias ? (double)bias[j] : 0.0);
+            y[i * n + j] = (float)v;
+        }
+    }
+    return 0;
+}
+
 /* ===================================================================== */
 /* tv/training/gpt2_ref.tkv:1977-1991 input generator                    */
 /* ===================================================================== */

@@ -201,6 +201,11 @@ int32_t tkvo_matmul_int4_grouped(const float* a, const int32_t* packed_w, const 
 float tkvo_f16_to_f32(int64_t h);
 int32_t tkvo_dequantize_gguf(const uint8_t* raw, int64_t nraw, int64_t n, int32_t dtype,
                              float* out);
+/* Extension (no reference counterpart): Q8_0 weights on int8 activation
+ * codes with group scales; the recipe is stated at the definition. */
+int32_t tkvo_matmul_q8_0(const int32_t* a, const uint8_t* raw, int64_t nraw, const float* sa,
+                         int64_t sa_stride, const float* bias, int64_t nbias, float* y,
+                         int64_t m, int64_t n, int64_t k);
 
 /* ---- gpt2_ref.tkv input generator ------------------------------------ */
 int64_t tkvo_lcg31(int64_t state);

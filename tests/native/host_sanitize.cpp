@@ -49,6 +49,13 @@ static void no_device_independent_checks() {
     CHECK(tkv_hip_ctx_destroy(0) == TKV_HIP_OK, "ctx_destroy(0)");
     CHECK(tkv_hip_linear_forward_static(0, nullptr, 1, 0, nullptr, nullptr) == TKV_HIP_BAD_ARG,
           "static entry with no weight");
+    float one = 1.0f;
+    CHECK(tkv_hip_dev_matmul_q8_0(0, nullptr, nullptr, nullptr, 4, 4, 128, &one, 2, nullptr,
+                                  nullptr) == TKV_HIP_BAD_ARG,
+          "q8_0 GEMM with scale stride 2");
+    CHECK(tkv_hip_dev_matmul_q8_0(0, nullptr, nullptr, nullptr, 4, 4, 128, nullptr, 0, nullptr,
+                                  nullptr) == TKV_HIP_BAD_ARG,
+          "q8_0 GEMM without scale");
 }
 
 static void no_device_checks() {
@@ -61,6 +68,9 @@ static void no_device_checks() {
     int64_t h = 0;
     CHECK(tkv_hip_ctx_create(0, &h) == TKV_HIP_NO_DEVICE, "ctx_create without a device");
     CHECK(tkv_hip_ctx_set_tuning(0, 0, 2) == TKV_HIP_NO_DEVICE, "set_tuning without a device");
+    std::vector<uint8_t> raw(34, 0);
+    CHECK(tkv_hip_weight_create_gguf_q8_0(0, raw.data(), 1, 32, nullptr, &h) == TKV_HIP_NO_DEVICE,
+          "q8_0 weight without a device");
 }
 
 static void device_checks() {
@@ -176,6 +186,59 @@ static void device_checks() {
               "fp8 linear_forward refuses per-token activations");
         CHECK(tkv_hip_ctx_synchronize(ctx) == TKV_HIP_OK, "fp8 synchronize");
         CHECK(tkv_hip_weight_free(wf) == TKV_HIP_OK, "fp8 weight_free");
+    }
+    // GGUF Q8_0 weights (raw blocks on the device): both activation modes,
+    // the raw GEMM entry on the handle's codes, and the refusals
+    {
+        const int kb = k / 32;
+        std::vector<uint8_t> blocks((size_t)n * kb * 34);
+        for (size_t i = 0; i < blocks.size(); i++) blocks[i] = (uint8_t)(i * 37 + 11);
+        for (int b = 0; b < n * kb; b++) {  // f16 scales 2^-6 .. 2^-3, both signs
+            blocks[(size_t)b * 34] = 0;
+            blocks[(size_t)b * 34 + 1] = (uint8_t)(0x24 + 4 * (b % 4)) | (uint8_t)((b & 1) << 7);
+        }
+        void* draw = nullptr;
+        CHECK(tkv_hip_malloc(ctx, blocks.size(), &draw) == TKV_HIP_OK, "malloc q8_0 blocks");
+        CHECK(tkv_hip_memcpy_h2d(ctx, draw, blocks.data(), blocks.size()) == TKV_HIP_OK,
+              "h2d q8_0 blocks");
+        int64_t wq = 0;
+        CHECK(tkv_hip_weight_create_gguf_q8_0(ctx, (const uint8_t*)draw, n, k - 16,
+                                              (const float*)db, &wq) == TKV_HIP_BAD_ARG,
+              "q8_0 weight with K % 32 != 0");
+        CHECK(tkv_hip_weight_create_gguf_q8_0(ctx, (const uint8_t*)draw, n, k, (const float*)db,
+                                              &wq) == TKV_HIP_OK,
+              "q8_0 weight_create");
+        for (int mode = 0; mode < 2; mode++)
+            CHECK(tkv_hip_linear_forward(ctx, wq, (const float*)dx, m, mode, (float*)dy) ==
+                      TKV_HIP_OK,
+                  "q8_0 linear_forward");
+        void *codes = nullptr, *dqa = nullptr, *dsa = nullptr;
+        float* gsc_dev = nullptr;
+        int64_t wn = 0, wk = 0;
+        int32_t wfmt = -1;
+        CHECK(tkv_hip_weight_info(wq, &codes, &gsc_dev, nullptr, &wn, &wk, &wfmt) == TKV_HIP_OK &&
+                  wfmt == TKV_HIP_WEIGHT_Q8_0 && wn == n && wk == k,
+              "q8_0 weight_info");
+        std::vector<int8_t> a8(m * k);
+        for (int i = 0; i < m * k; i++) a8[i] = (int8_t)((i * 13) % 255 - 127);
+        const float sa1 = 0.01f;
+        CHECK(tkv_hip_malloc(ctx, m * k, &dqa) == TKV_HIP_OK, "malloc q8_0 a");
+        CHECK(tkv_hip_malloc(ctx, 4, &dsa) == TKV_HIP_OK, "malloc q8_0 sa");
+        CHECK(tkv_hip_memcpy_h2d(ctx, dqa, a8.data(), m * k) == TKV_HIP_OK, "h2d q8_0 a");
+        CHECK(tkv_hip_memcpy_h2d(ctx, dsa, &sa1, 4) == TKV_HIP_OK, "h2d q8_0 sa");
+        CHECK(tkv_hip_dev_matmul_q8_0(ctx, (const int8_t*)dqa, (const int8_t*)codes, gsc_dev, m, n,
+                                      k, (const float*)dsa, 0, nullptr, (float*)dy) == TKV_HIP_OK,
+              "q8_0 GEMM");
+        CHECK(tkv_hip_dev_matmul_q8_0(ctx, (const int8_t*)dqa, (const int8_t*)codes, gsc_dev, m, n,
+                                      k - 32, (const float*)dsa, 0, nullptr, (float*)dy) ==
+                  TKV_HIP_UNSUPPORTED,
+              "q8_0 GEMM with K % 128 != 0");
+        CHECK(tkv_hip_linear_forward_static(wq, (const float*)dx, m, 0, (float*)dy, nullptr) ==
+                  TKV_HIP_UNSUPPORTED,
+              "static entry refuses Q8_0 weights");
+        CHECK(tkv_hip_ctx_synchronize(ctx) == TKV_HIP_OK, "q8_0 synchronize");
+        CHECK(tkv_hip_weight_free(wq) == TKV_HIP_OK, "q8_0 weight_free");
+        for (void* p : {draw, dqa, dsa}) CHECK(tkv_hip_free(ctx, p) == TKV_HIP_OK, "free q8_0");
     }
     // tuning overrides: every configuration of the tiled GEMM on one product
     for (int cfg = 0; cfg <= 11; cfg++) {

@@ -790,3 +790,123 @@ def test_gguf_block_known_answers():
     assert np.array_equal(y, (q.astype(np.float64) * 2.0 ** -24).astype(np.float32))
     with pytest.raises(ValueError):
         O.dequantize_gguf(raw[:40], 64, O.GGUF_Q8_0)
+
+
+# ---------------------------------------------------------------------------
+# Q8_0 weights on int8 activation codes (an extension: the reference decodes
+# Q8_0 blocks to f32, gguf.tkv:284-290, and has no quantized GEMM for them)
+# ---------------------------------------------------------------------------
+
+def q8_0_blocks(rows, kb, d_codes, q):
+    """Raw Q8_0 bytes of rows x kb blocks: f16 scale codes d_codes [rows, kb]
+    and int8 codes q [rows, kb * 32]."""
+    raw = np.zeros((rows, kb, 34), np.uint8)
+    raw[:, :, 0] = d_codes & 255
+    raw[:, :, 1] = (d_codes >> 8) & 255
+    raw[:, :, 2:] = np.asarray(q, np.int8).reshape(rows, kb, 32).view(np.uint8)
+    return raw.reshape(-1)
+
+
+def _round_f32(x: Fraction) -> Fraction:
+    """x rounded to the nearest f32 (ties to even), finite range."""
+    if x == 0:
+        return Fraction(0)
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** (max(e, -126) - 23)
+    q = a / ulp
+    whole = q.numerator // q.denominator
+    rest = q - whole
+    if rest > Fraction(1, 2) or (rest == Fraction(1, 2) and whole % 2 == 1):
+        whole += 1
+    assert whole * ulp < Fraction(2) ** 128
+    return (whole * ulp) if x > 0 else -(whole * ulp)
+
+
+def test_q8_0_matmul_exact_on_dyadic_inputs():
+    """Power-of-two group scales and small codes keep every step of the fma
+    chain exact, so y is the exact product of the reference decoder's weights
+    (dequantize_gguf, gguf.tkv:284-290) with the activation codes, scaled and
+    biased once in f64: pins the block layout, the row / column roles, the
+    per-tensor and per-token scale and the bias against numpy f64 matmul."""
+    m, n, k = 7, 9, 256
+    kb = k // 32
+    e = RNG.integers(-4, 1, (n, kb))
+    d_codes = (RNG.integers(0, 2, (n, kb)) << 15) | ((e + 15) << 10)    # +-2^e
+    q = RNG.integers(-8, 9, (n, k)).astype(np.int8)
+    raw = q8_0_blocks(n, kb, d_codes, q)
+    a = RNG.integers(-8, 9, (m, k)).astype(np.int32)
+    w = O.dequantize_gguf(raw, n * k, O.GGUF_Q8_0).reshape(n, k).astype(np.float64)
+    exact = a.astype(np.float64) @ w.T       # multiples of 2^-4 below 2^14: exact
+    bias = RNG.standard_normal(n).astype(np.float32)
+    for sa in (np.float32(0.0123), (RNG.random(m) + 0.01).astype(np.float32)):
+        s = np.asarray(sa, np.float64).reshape(-1, 1)
+        for b in (bias, None):
+            want = (exact * s + (0.0 if b is None else b.astype(np.float64))).astype(np.float32)
+            got = O.matmul_q8_0(a, raw, sa, m, n, k, b)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(ValueError):
+        O.matmul_q8_0(a[:, :200], raw, 1.0, m, n, 200)                 # k % 32 != 0
+    with pytest.raises(ValueError):
+        O.matmul_q8_0(a, raw[:-1], 1.0, m, n, k)                       # raw too short
+
+
+def test_q8_0_matmul_rounds_once_per_group():
+    """General scales and full-range codes: the oracle equals an exact-rational
+    emulation of the stated chain (each group's fma rounded once to f32, in
+    group order), and on these inputs a chain that rounds the product before
+    the add differs from it, so the check tells the two apart."""
+    m, n, k = 3, 5, 384
+    kb = k // 32
+    d_codes = RNG.integers(0x0400, 0x7C00, (n, kb)) | (RNG.integers(0, 2, (n, kb)) << 15)
+    q = RNG.integers(-128, 128, (n, k)).astype(np.int8)
+    a = RNG.integers(-127, 128, (m, k)).astype(np.int64)
+    raw = q8_0_blocks(n, kb, d_codes, q)
+    d = d_codes.astype(np.uint16).view(np.float16).astype(np.float64)
+    sa = np.float32(0.037)
+    got = O.matmul_q8_0(a, raw, sa, m, n, k)
+    differs = 0
+    for i in range(m):
+        for j in range(n):
+            fused, split = Fraction(0), Fraction(0)
+            for g in range(kb):
+                dot = int(a[i, 32 * g:32 * g + 32] @ q[j, 32 * g:32 * g + 32].astype(np.int64))
+                dg = Fraction(float(d[j, g]))
+                fused = _round_f32(fused + dot * dg)
+                split = _round_f32(split + _round_f32(dot * dg))
+            differs += fused != split
+            want = np.float32(float(fused) * float(sa) + 0.0)
+            assert got[i, j].view(np.uint32) == want.view(np.uint32), (i, j)
+    assert differs > 0
+
+
+def test_q8_0_matmul_within_stated_bound_of_float_product():
+    """Against the reference's own semantics -- decode the blocks to f32, then
+    multiply the float activation -- the per-token int8 codes of x
+    (quantize_dynamic_int8_rowwise, engine.tkv:266-285) cost at most
+    (sa / 2) sum_k |w[n, k]| per output (plus 128 2^-24 sa sum_k |w|: the
+    codes come from the unrounded f64 scale, sa is its f32 rounding), and the
+    f32 chain one rounding per group:
+    |y - x w^T| <= (sa / 2 + 2^-17 sa) sum_k |w| + kb 2^-24 sum_g |d dot_g| sa + 2^-24 |y|."""
+    m, n, k = 6, 11, 512
+    kb = k // 32
+    d_codes = RNG.integers(0x1C00, 0x2800, (n, kb))                   # 2^-8 .. 2^-5
+    q = RNG.integers(-128, 128, (n, k)).astype(np.int8)
+    raw = q8_0_blocks(n, kb, d_codes, q)
+    x = RNG.standard_normal((m, k)).astype(np.float32)
+    codes, sa = O.quantize_dynamic_int8_rowwise(x.reshape(-1), m, k)
+    codes = np.asarray(codes, np.int64).reshape(m, k)
+    sa = np.asarray(sa, np.float32)
+    y = O.matmul_q8_0(codes, raw, sa, m, n, k).astype(np.float64)
+    w = O.dequantize_gguf(raw, n * k, O.GGUF_Q8_0).reshape(n, k).astype(np.float64)
+    ref = x.astype(np.float64) @ w.T
+    d = d_codes.astype(np.uint16).view(np.float16).astype(np.float64)
+    dots = np.einsum("mgk,ngk->mng", codes.reshape(m, kb, 32), q.astype(np.int64).reshape(n, kb, 32))
+    chain = kb * 2.0 ** -24 * np.abs(dots * d[None]).sum(axis=2) * sa[:, None]
+    bound = (sa[:, None] / 2 + 2.0 ** -17 * sa[:, None]) * np.abs(w).sum(axis=1)[None] + chain \
+        + 2.0 ** -24 * np.abs(y)
+    assert np.all(np.abs(y - ref) <= bound)
+    # the activation term dominates: the bound is not vacuous
+    assert np.abs(y - ref).max() > 0.01 * bound.max()

@@ -773,6 +773,24 @@ int32_t tkv_hip_dev_matmul_fp8_e4m3_fast(int64_t ctx, const uint8_t* a, const ui
     return launch_gemm_f8(c, a, w, m, n, k, scale_a, scale_a_stride, scales_w, bias, y, true);
 }
 
+int32_t tkv_hip_dev_matmul_q8_0(int64_t ctx, const int8_t* a, const int8_t* codes,
+                                const float* group_scales, int64_t m, int64_t n, int64_t k,
+                                const float* scale_a, int64_t scale_a_stride, const float* bias,
+                                float* y) {
+    if (m < 0 || n < 0 || k < 0 || (scale_a_stride != 0 && scale_a_stride != 1) || !scale_a)
+        return set_error(TKV_HIP_BAD_ARG, "matmul_q8_0: bad arguments");
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (m == 0 || n == 0) return TKV_HIP_OK;
+    if (!a || !codes || !group_scales || !y)
+        return set_error(TKV_HIP_BAD_ARG, "matmul_q8_0: NULL operand");
+    const int rc = launch_gemm_q8(c, a, codes, group_scales, m, n, k, scale_a, scale_a_stride,
+                                  bias, y);
+    return rc == TKV_HIP_UNSUPPORTED
+               ? set_error(rc, "matmul_q8_0: K must be a positive multiple of 128, operands 16-byte aligned")
+               : rc;
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

@@ -987,7 +987,7 @@ static int64_t tiles_of(int64_t m, int64_t n) {
 // context's TKV_HIP_TUNE_GEMM_CFG override (0..11; 2.. are the warp-
 // specialised configurations, 10 the skinny kernel for INT8 with M <= 32, 11
 // the fused-role kernel) forces one.
-static int pick_cfg(Ctx* c, int64_t m, int64_t n) {
+static inline int pick_cfg(Ctx* c, int64_t m, int64_t n) {
     const int64_t f = tuned(c, TKV_HIP_TUNE_GEMM_CFG);
     if (f >= 0) return (int)f;
     // Warp-specialised 128x192 tiles (cfg 2) measured best over the four

@@ -24,6 +24,7 @@ struct Weight {
     void* codes = nullptr;   // [n, ldk] int8 or e4m3 bytes, zero-padded
     void* codes16 = nullptr; // WEIGHT_FP8: [n, ldk] halves, the codes' reference decode
     float* scales = nullptr; // [n] per-channel scales
+    float* gscales = nullptr;// WEIGHT_Q8_0: [n, ldk / 32] group scales (the blocks' d)
     float* bias = nullptr;   // [n] or null
 };
 
@@ -81,6 +82,7 @@ static void weight_release(Weight* wt) {
     (void)hipDeviceSynchronize();
     if (wt->codes) (void)hipFree(wt->codes);
     if (wt->codes16) (void)hipFree(wt->codes16);
+    if (wt->gscales) (void)hipFree(wt->gscales);
     if (wt->scales) (void)hipFree(wt->scales);
     if (wt->bias) (void)hipFree(wt->bias);
     delete wt;
@@ -105,6 +107,28 @@ static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t
     void* qa;
     TKV_RC_TRY(ctx_workspace(c, 0, (size_t)(m * k), &qa));
     tkv_hip_qparams_dev* ap = c->params + 1;
+    if (wt->format == TKV_HIP_WEIGHT_Q8_0) {
+        // the INT8 path's activation quantizers, then the group-scaled GEMM
+        const float* sa = &ap->scale;
+        int64_t stride = 0;
+        if (act_mode == TKV_HIP_ACT_PER_TENSOR) {
+            TKV_RC_TRY(launch_quant_i8_dynamic(c, x, m * k, TKV_HIP_RECIPE_PRIMARY, ap, qa, false));
+        } else if (act_mode == TKV_HIP_ACT_PER_TOKEN) {
+            void* ws;
+            TKV_RC_TRY(ctx_workspace(c, 1, (size_t)m * 4, &ws));
+            TKV_RC_TRY(launch_quant_rows(c, x, m, k, RM_DYNAMIC, nullptr, qa, false,
+                                         static_cast<float*>(ws), nullptr, 1));
+            sa = static_cast<const float*>(ws);
+            stride = 1;
+        } else {
+            return set_error(TKV_HIP_BAD_ARG, "linear_forward: unknown act_mode");
+        }
+        const int rc = launch_gemm_q8(c, static_cast<int8_t*>(qa), static_cast<int8_t*>(wt->codes),
+                                      wt->gscales, m, wt->n, k, sa, stride, wt->bias, y);
+        return rc == TKV_HIP_UNSUPPORTED
+                   ? set_error(rc, "linear_forward: Q8_0 GEMM sizes out of range")
+                   : rc;
+    }
     if (wt->format == TKV_HIP_WEIGHT_INT8) {
         I8Epilogue ep;
         ep.mode = EPI_PER_CHANNEL;
@@ -294,6 +318,40 @@ int32_t tkv_hip_weight_create_int8(int64_t ctx, const int8_t* codes, const float
     return TKV_HIP_OK;
 }
 
+int32_t tkv_hip_weight_create_gguf_q8_0(int64_t ctx, const uint8_t* raw, int64_t n, int64_t k,
+                                        const float* bias, int64_t* handle_out) {
+    Ctx* c;
+    TKV_RC_TRY(ctx_get(ctx, &c));
+    if (!raw || !handle_out || n <= 0 || k <= 0 || k % 32 != 0 || n >= (1ll << 28))
+        return set_error(TKV_HIP_BAD_ARG, "weight_create_gguf_q8_0: bad arguments (K % 32 != 0?)");
+    if (c->capturing)
+        return set_error(TKV_HIP_BAD_ARG, "weight_create_gguf_q8_0: allocates and synchronizes, not inside a stream capture");
+    Weight* wt = new (std::nothrow) Weight();
+    if (!wt) return set_error(TKV_HIP_OOM, "weight_create_gguf_q8_0: host allocation failed");
+    int rc = weight_alloc(c, wt, n, k, TKV_HIP_WEIGHT_Q8_0, bias);
+    if (rc == TKV_HIP_OK) {
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&wt->gscales),
+                                 (size_t)(n * (wt->ldk / 32)) * 4);
+        if (e != hipSuccess)
+            rc = fail_hip(e, "hipMalloc", __FILE__, __LINE__);
+        else
+            rc = launch_q8_0_unpack(c, raw, n, k, wt->ldk, static_cast<uint8_t*>(wt->codes),
+                                    wt->gscales);
+        if (rc == TKV_HIP_UNSUPPORTED)
+            rc = set_error(TKV_HIP_BAD_ARG, "weight_create_gguf_q8_0: layout not supported");
+    }
+    if (rc == TKV_HIP_OK) {
+        hipError_t e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) rc = fail_hip(e, "hipStreamSynchronize", __FILE__, __LINE__);
+    }
+    if (rc != TKV_HIP_OK) {
+        weight_release(wt);
+        return rc;
+    }
+    *handle_out = reinterpret_cast<int64_t>(wt);
+    return TKV_HIP_OK;
+}
+
 int32_t tkv_hip_weight_free(int64_t handle) {
     weight_release(reinterpret_cast<Weight*>(handle));
     return TKV_HIP_OK;
@@ -304,7 +362,7 @@ int32_t tkv_hip_weight_info(int64_t handle, void** codes, float** scales, float*
     Weight* wt = reinterpret_cast<Weight*>(handle);
     if (!wt) return set_error(TKV_HIP_BAD_ARG, "NULL weight handle");
     if (codes) *codes = wt->codes;
-    if (scales) *scales = wt->scales;
+    if (scales) *scales = wt->format == TKV_HIP_WEIGHT_Q8_0 ? wt->gscales : wt->scales;
     if (bias) *bias = wt->bias;
     if (n) *n = wt->n;
     if (k) *k = wt->ldk;

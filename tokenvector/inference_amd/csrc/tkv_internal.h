@@ -245,6 +245,19 @@ int64_t gguf_block_bytes(int dtype);
 // INT8 GEMM against W [n, ldk], y = fl32(fl64(fl64(acc * sa[m]) * sw[n]) + b[n]).
 int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t ldk,
                      int64_t n, const float* scales_w, const float* bias, float* y);
+// gemm_q8.hip: GGUF Q8_0 weights on the INT8 MFMA (extension).
+// Unpack n rows of k / 32 raw blocks (34 bytes) into codes [n, ldk] (16-byte
+// aligned, padding left as it is) and group scales gs [n, ldk / 32] (padding
+// groups 0).  k % 32 != 0, ldk % 128 != 0: UNSUPPORTED.
+int launch_q8_0_unpack(Ctx* c, const uint8_t* raw, int64_t n, int64_t k, int64_t ldk,
+                       uint8_t* codes, float* gs);
+// y[m, n] = fl32(fl64(fl64(acc) * sa) + b[n]), acc the fma chain over the
+// groups of fl32(dot_g) * gs[n, g]; a [m, ldk], w [n, ldk] int8 codes,
+// sa = scale_a[m * scale_a_stride] (stride 0 or 1).  ldk % 128 != 0 or
+// unaligned operands: UNSUPPORTED, nothing launched.
+int launch_gemm_q8(Ctx* c, const int8_t* a, const int8_t* w, const float* gs, int64_t m,
+                   int64_t n, int64_t ldk, const float* scale_a, int64_t scale_a_stride,
+                   const float* bias, float* y);
 // K granularity of the GEMM main loop: operands whose row stride is a
 // multiple of it (and 16-byte aligned) run without repacking.
 int64_t gemm_k_align();

@@ -20,6 +20,7 @@ ACT_PER_TOKEN = 1
 WEIGHT_INT8 = 0
 WEIGHT_FP8 = 1
 WEIGHT_FP8_FAST = 2
+WEIGHT_Q8_0 = 3      # GGUF Q8_0 blocks on the INT8 GEMM with group scales (extension)
 
 
 def _vp(x) -> C.c_void_p:
@@ -286,6 +287,16 @@ def matmul_int8(ctx, a, w, m, n, k, scale_a, scale_a_stride, scale_w, scales_w, 
                                                   _vp(y), int(recipe)))
 
 
+def matmul_q8_0(ctx, a, codes, group_scales, m, n, k, scale_a, scale_a_stride, bias, y) -> None:
+    """Q8_0 weights on int8 activation codes (extension; no reference
+    counterpart): a [m,k], codes [n,k] int8, group_scales f32 [n, k/32];
+    acc = fma chain over the groups of float(dot_g) * d, y = acc * sa + bias."""
+    _lib.check(_lib.lib().tkv_hip_dev_matmul_q8_0(ctx.handle, _vp(a), _vp(codes),
+                                                  _vp(group_scales), int(m), int(n), int(k),
+                                                  _vp(scale_a), int(scale_a_stride), _vp(bias),
+                                                  _vp(y)))
+
+
 def qlinear_matmul(ctx, a, sa, zpa, w, sw, zpw, sy, zpy, y, m, n, k, recipe: int = 0) -> None:
     """QLinearMatMul on int8 codes: a [m,k], w [n,k] (B transposed), y int8 [m,n]."""
     _lib.check(_lib.lib().tkv_hip_dev_qlinear_matmul(
@@ -367,6 +378,16 @@ class QuantizedLinear:
         h = C.c_int64()
         _lib.check(_lib.lib().tkv_hip_weight_create_int8(ctx.handle, _vp(codes), _vp(scales), int(n),
                                                          int(k), _vp(bias), C.byref(h)))
+        return cls(ctx, h.value)
+
+    @classmethod
+    def from_gguf_q8_0(cls, ctx: Context, raw, n: int, k: int, bias=None) -> "QuantizedLinear":
+        """A weight [n, k] from raw GGUF Q8_0 blocks on the device (n rows of
+        k / 32 blocks of 34 bytes); `scales` is then the group scales [n, k/32]
+        with k the padded row stride."""
+        h = C.c_int64()
+        _lib.check(_lib.lib().tkv_hip_weight_create_gguf_q8_0(ctx.handle, _vp(raw), int(n), int(k),
+                                                              _vp(bias), C.byref(h)))
         return cls(ctx, h.value)
 
     def forward(self, x, m: int, y, act_mode: int = ACT_PER_TENSOR) -> None:
