@@ -95,6 +95,14 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     const int lr = lane & 15, kg = lane >> 4;
     const int ks0 = wave * kKsw;
 
+    // The weight loads are unconditional, from a clamped k-step (fragments
+    // past nks are never used: the MFMA loop skips them): under the
+    // wave-uniform branch they had, the compiler left a register copy where
+    // the branches join and waited there (vmcnt(0)) for the load, a memory
+    // round trip in the middle of issuing the loads.  The activation loads
+    // stay lane-masked (clamped, every thread past nchunks would load), with
+    // no value for the masked lanes, which nothing reads: a zero there made
+    // the same join copy and wait.
     // weight fragments (B operand): column n0 + 16 c + lr, bytes [64 ks + 16 kg, +16)
     v4i wf[NCB][kKsw];
 #pragma unroll
@@ -103,10 +111,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
         const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + kg * 16;
 #pragma unroll
         for (int s = 0; s < kKsw; s++) {
-            const int ks = ks0 + s;
-            wf[c][s] = ks < nks
-                           ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64))
-                           : v4i{0, 0, 0, 0};
+            const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
+            wf[c][s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64));
         }
     }
     // activation chunks of the valid rows
@@ -120,9 +126,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
         ck16[j] = c / rows;
         const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)(r0 + crow[j]) * K +
                                                            (int64_t)ck16[j] * 16);
+        if (c < nchunks) {
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            xv[j][q] = c < nchunks ? xp[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int q = 0; q < 4; q++) xv[j][q] = xp[q];
+        }
     }
     if (threadIdx.x < 16) s_am[threadIdx.x] = 0u;
     for (int i = threadIdx.x; i < 256 * NCB; i += nthreads) s_acc[i] = 0;
