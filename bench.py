@@ -303,9 +303,19 @@ def bench_q8_0(ctx, D, m=M, reps=20):
             for buf in t:
                 buf.close()
         sa.close()
+        # decode batches through tkv_hip_linear_forward (per-token activations,
+        # the one-kernel Q8_0 decode path), warm weights, back to back
+        for dm in (1, 4, 32):
+            x = D.DeviceBuffer.from_host(ctx, rng.standard_normal(dm * k).astype(np.float32))
+            y = D.DeviceBuffer.empty(ctx, (dm, n), np.float32)
+            dus = _time_us(ctx, D, lambda i: wt.forward(x, dm, y, D.ACT_PER_TOKEN), 50)
+            out[f"{name}_decode_m{dm}"] = {"us": round(dus, 2)}
+            x.close()
+            y.close()
         wt.close()
     out["note"] = ("k_gemm_q8: group-scaled INT8 MFMA, bound by the per-group f32 conversion + fma "
-                   "(1258 TOPS), not by the MFMA peak")
+                   "(1258 TOPS), not by the MFMA peak; *_decode_m*: k_decode_q8 per call (per-token "
+                   "quantize, one MFMA per group, the group chain in LDS), warm weights")
     return out
 
 

@@ -521,7 +521,9 @@ int32_t tkv_hip_dev_dequantize_gguf(int64_t ctx, const uint8_t* raw, int64_t n, 
 #define TKV_HIP_WEIGHT_Q8_0 3
 /* Weight handle from raw Q8_0 blocks (device bytes, row-major) for
  * tkv_hip_linear_forward: either act_mode, the activation quantized as for
- * INT8 weights (K % 128 == 0 there).  K % 32 != 0: BAD_ARG.
+ * INT8 weights (K % 128 == 0 there; per-token decode batches, M <= 32, run
+ * one kernel with K % 64 == 0, K <= 3072, same results).  K % 32 != 0:
+ * BAD_ARG.
  * tkv_hip_weight_info returns the group scales [N, k / 32] as `scales`
  * (k = the codes' padded row stride). */
 int32_t tkv_hip_weight_create_gguf_q8_0(int64_t ctx, const uint8_t* raw, int64_t n, int64_t k,

@@ -8,7 +8,9 @@ the reference's f16 decode; the GEMM bit-exact against the oracle (its group
 chain is fixed: one fma per group, in group order), on ragged shapes, per
 tensor and per token, with and without bias, through the raw GEMM entry and
 through tkv_hip_linear_forward; against the reference's decode-then-multiply
-of the float activation, within the bound the header states.
+of the float activation, within the bound the header states; decode batches
+(M <= 32, per-token) through their one-kernel path, bit-exact against the
+oracle and against the tile GEMM on the same codes.
 """
 import ctypes as C
 import sys
@@ -249,5 +251,68 @@ def test_q8_0_errors(ctx, hip):
     with pytest.raises(ValueError):
         D.matmul_q8_0(ctx, da, wt.codes, wt.scales, 2, 4, 128, ds, 2, None, dy)   # stride 2
     for buf in (dr, dx, dy, ds, da):
+        buf.close()
+    wt.close()
+
+
+Q8_DECODE = [(1, 2304, 768), (4, 768, 3072), (5, 100, 192), (16, 3072, 768), (17, 768, 3072),
+             (32, 2304, 768), (32, 768, 3072)]
+
+
+@pytest.mark.parametrize("m,n,k", Q8_DECODE)
+def test_q8_0_decode(ctx, m, n, k):
+    """Decode batches (M <= 32, per-token activations) take the one-kernel
+    Q8_0 decode path (in-kernel per-token quantize, one MFMA per group, the
+    group chain in LDS): bit-exact against the oracle's rowwise quantizer +
+    tkvo_matmul_q8_0, and the same bits as the tile GEMM on those codes."""
+    say(f"q8_0 decode m={m} n={n} k={k}")
+    raw, q, _ = _blocks(n, k, 900 + m + n)
+    x = O.gi_noise(m * k, 50 + m, 1.0).reshape(m, k)
+    bias = O.gi_noise(n, 51, 0.01)
+    wt, db = _weight(ctx, raw, n, k, bias)
+    dx = D.DeviceBuffer.from_host(ctx, x)
+    dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+    wt.forward(dx, m, dy, D.ACT_PER_TOKEN)
+    got = dy.download()
+    c, s = O.quantize_dynamic_int8_rowwise(x.reshape(-1), m, k)
+    codes = np.asarray(c, np.int32).reshape(m, k)
+    sa = np.asarray(s, np.float32)
+    assert _bits_equal(got, O.matmul_q8_0(codes, raw, sa, m, n, k, bias))
+    if k % 128 == 0:
+        da = D.DeviceBuffer.from_host(ctx, codes.astype(np.int8))
+        ds = D.DeviceBuffer.from_host(ctx, sa)
+        dy2 = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+        D.matmul_q8_0(ctx, da, wt.codes, wt.scales, m, n, k, ds, 1, db, dy2)
+        assert _bits_equal(dy2.download(), got)
+        for buf in (da, ds, dy2):
+            buf.close()
+    for buf in (dx, dy, db):
+        buf.close()
+    wt.close()
+
+
+@pytest.mark.parametrize("group", [1, 3, 16])
+def test_q8_0_decode_forced_groups(ctx, group):
+    """Forced tokens per workgroup (the context's decode-group override): one
+    token, a group that leaves a ragged last group, and 16 (the largest LDS
+    footprint, capped by the device's LDS per workgroup) stay bit-exact."""
+    m, n, k = 32, 768, 3072
+    say(f"q8_0 decode forced group={group}")
+    raw, q, _ = _blocks(n, k, 1234)
+    x = O.gi_noise(m * k, 77, 1.0).reshape(m, k)
+    wt, _ = _weight(ctx, raw, n, k)
+    dx = D.DeviceBuffer.from_host(ctx, x)
+    dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+    ctx.set_tuning(D.TUNE_DECODE_GROUP, group)
+    try:
+        wt.forward(dx, m, dy, D.ACT_PER_TOKEN)
+        got = dy.download()
+    finally:
+        ctx.set_tuning(D.TUNE_DECODE_GROUP, -1)
+    c, s = O.quantize_dynamic_int8_rowwise(x.reshape(-1), m, k)
+    want = O.matmul_q8_0(np.asarray(c, np.int32).reshape(m, k), raw, np.asarray(s, np.float32),
+                         m, n, k)
+    assert _bits_equal(got, want)
+    for buf in (dx, dy):
         buf.close()
     wt.close()

@@ -217,6 +217,192 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     }
 }
 
+// Row stride (in groups) of the Q8_0 decode's dots and scales: nkb (even)
+// rounded up to twice an odd number, so 16 rows of it start 16 distinct
+// even banks apart and float2 reads of the 16 columns do not conflict.
+__host__ __device__ constexpr int q8_decode_stride(int nkb) { return (nkb / 2) % 2 ? nkb : nkb + 2; }
+__host__ __device__ constexpr int64_t q8_decode_lds(int64_t k, int64_t rg) {
+    return rg * k + (rg * 64 + 64) * q8_decode_stride((int)(k / 32));
+}
+
+// GGUF Q8_0 weights (extension; the reference decodes them to f32,
+// gguf.tkv:284-290) for decode batches: the per-token quantize of
+// k_decode_i8, then for 16 columns and a row group
+//   dot_g = sum over block g's 32 k of a[m, k] q[n, k]   (exact INT32)
+//   acc   = 0;  acc = fma(float(dot_g), d[n, g], acc)  for g = 0, 1, ... in order
+//   y     = fl32(fl64(fl64(acc) * sa[m]) + b[n])
+// -- the recipe of the Q8_0 tile GEMM, so results are the same bits.  Each
+// wave multiplies its 6 groups (3 64-deep k-steps) with one
+// v_mfma_i32_16x16x32_i8 each into a zero accumulator and keeps every
+// group's dots in LDS; after a barrier one thread per output runs the fma
+// chain over all groups in order (the order fixes the rounding, so the
+// groups cannot be summed per wave) and the epilogue.
+// x f32 [M, K] (16-byte aligned rows, K % 64 == 0), W int8 [N, ldk], gs f32
+// [N, ldk / 32], bias f32 [N] or null, y f32 [M, N]; RG <= 16 tokens per
+// group.  Dynamic LDS (q8_decode_lds): RG K code bytes (16-byte chunks of
+// 16 k, the group's rows interleaved per chunk); the dots [RG][16][nkp] and
+// scales [16][nkp], output-major so that a chain reads two groups per LDS
+// load, nkp = K / 32 rounded up to twice an odd number so that the 16
+// columns' rows start in distinct banks.  Dots are kept as f32 (exact, |dot|
+// < 2^24), converted by the waves that form them.
+__global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
+    const float* __restrict__ x, const uint8_t* __restrict__ W, const float* __restrict__ gs,
+    int M, int N, int K, int ldk, int RG, int ncb, int ngr, const float* __restrict__ bias,
+    float* __restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    const int nks = K / 64, nkb = K / 32, nkp = q8_decode_stride(nkb);
+    uint8_t* s_a = s_dyn;                                                   // [K / 16][RG][16]
+    float* s_p = reinterpret_cast<float*>(s_dyn + RG * K);                  // [RG][16][nkp]
+    float* s_d = reinterpret_cast<float*>(s_dyn + RG * K + RG * 64 * nkp);  // [16][nkp]
+    __shared__ uint32_t s_am[16];
+    __shared__ double s_inv[16];
+    __shared__ float s_sa[16];
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int nthreads = (int)blockDim.x;
+    const int t = xcd_tile((int)blockIdx.x, ncb * ngr);
+    const int cb = t / ngr, rg = t % ngr;
+    const int n0 = cb * 16, r0 = rg * RG;
+    const int rows = M - r0 < RG ? M - r0 : RG;
+    const int lr = lane & 15, kg = lane >> 4;
+    const int ks0 = wave * kKsw;
+    const int gstride = ldk / 32;
+
+    // Loads as in k_decode_i8 (unconditional weights from a clamped k-step,
+    // lane-masked activation chunks with no default): the B operand of group
+    // g = 2 ks + h is column n0 + lr, bytes [32 g + 8 kg, +8); each thread
+    // also takes up to two of the 16 columns' group scales (16 * K / 32 <=
+    // 1.5 threads' worth), stored to LDS once the loads are all issued.
+    const int wcol = n0 + lr < N ? n0 + lr : N - 1;
+    const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + 8 * kg;
+    int64_t wf[kKsw][2];
+#pragma unroll
+    for (int s = 0; s < kKsw; s++) {
+        const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            wf[s][h] = __builtin_nontemporal_load(
+                reinterpret_cast<const int64_t*>(wp + (2 * ks + h) * 32));
+    }
+    float dv[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        int i = (int)threadIdx.x + q * nthreads;
+        i = i < 16 * nkb ? i : 16 * nkb - 1;
+        const int c = i & 15, g = i >> 4;
+        const int col = n0 + c < N ? n0 + c : N - 1;
+        dv[q] = gs[(int64_t)col * gstride + g];
+    }
+    const int nchunks = nks * 4 * rows;
+    float4 xv[kChunks][4];
+    int crow[kChunks], ck16[kChunks];
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int c = (int)threadIdx.x + j * nthreads;
+        crow[j] = c % rows;
+        ck16[j] = c / rows;
+        const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)(r0 + crow[j]) * K +
+                                                           (int64_t)ck16[j] * 16);
+        if (c < nchunks) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) xv[j][q] = xp[q];
+        }
+    }
+    if (threadIdx.x < 16) s_am[threadIdx.x] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int c = (int)threadIdx.x + j * nthreads;
+        if (c < nchunks) {
+            float am = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) am = amax4(am, xv[j][q]);
+            atomicMax(&s_am[crow[j]], __float_as_uint(am));
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int i = (int)threadIdx.x + q * nthreads;
+        if (i < 16 * nkb) s_d[(i & 15) * nkp + (i >> 4)] = dv[q];
+    }
+    __syncthreads();
+    if (threadIdx.x < rows) {
+        double dam = (double)__uint_as_float(s_am[threadIdx.x]);
+        if (dam < 0.00000001) dam = 0.00000001;
+        const double sc = dam / 127.0;  // engine.tkv:277-279
+        s_inv[threadIdx.x] = 1.0 / sc;
+        s_sa[threadIdx.x] = (float)sc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int c = (int)threadIdx.x + j * nthreads;
+        if (c < nchunks) {
+            const double inv = s_inv[crow[j]];
+            const v4i q = {quant4(xv[j][0], inv), quant4(xv[j][1], inv), quant4(xv[j][2], inv),
+                           quant4(xv[j][3], inv)};
+            *reinterpret_cast<v4i*>(s_a + ((ck16[j] * RG + crow[j]) << 4)) = q;
+        }
+    }
+    __syncthreads();
+    // Group dots: the A operand of group g is row lr's codes [32 g + 8 kg,
+    // +8), the first or second half of 16-byte chunk 2 g + kg / 2; rows past
+    // the group read 0.  The result holds column lr, rows 4 kg + i.
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < kKsw; s++) {
+        const int ks = ks0 + s;
+        if (ks < nks) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int g = 2 * ks + h;
+                const int64_t af =
+                    lr < rows ? *reinterpret_cast<const int64_t*>(
+                                    s_a + (((2 * g + (kg >> 1)) * RG + lr) << 4) + 8 * (kg & 1))
+                              : 0;
+                const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, wf[s][h], zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (4 * kg + i < rows) s_p[((4 * kg + i) * 16 + lr) * nkp + g] = (float)p[i];
+            }
+        }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < rows * 16) {
+        const int r = (int)threadIdx.x >> 4, c = (int)threadIdx.x & 15;
+        // the chain's LDS reads are issued 8 groups at a time (float2 loads),
+        // so one LDS latency covers 8 dependent fmas instead of each
+        const float2* pp = reinterpret_cast<const float2*>(s_p + (r * 16 + c) * nkp);
+        const float2* dp = reinterpret_cast<const float2*>(s_d + c * nkp);
+        constexpr int U = 4;  // float2 pairs per batch
+        float acc = 0.0f;
+        int h = 0;
+        for (; h + U <= nkb / 2; h += U) {
+            float2 pv[U], dw[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                pv[u] = pp[h + u];
+                dw[u] = dp[h + u];
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                acc = __builtin_fmaf(pv[u].x, dw[u].x, acc);
+                acc = __builtin_fmaf(pv[u].y, dw[u].y, acc);
+            }
+        }
+        for (; h < nkb / 2; h++) {
+            const float2 pv = pp[h], dw = dp[h];
+            acc = __builtin_fmaf(pv.x, dw.x, acc);
+            acc = __builtin_fmaf(pv.y, dw.y, acc);
+        }
+        const int col = n0 + c;
+        if (col < N) {
+            double v = (double)acc * (double)s_sa[r];
+            v = v + (bias ? (double)bias[col] : 0.0);
+            __builtin_nontemporal_store((float)v, y + (int64_t)(r0 + r) * N + col);
+        }
+    }
+}
+
 }  // namespace
 
 // Tokens per row group: all of them up to 4; 4 up to 16 tokens, which keeps
@@ -269,6 +455,28 @@ int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
         hipLaunchKernelGGL(k_decode_i8<1>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
                            (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
                            rg, (int)ncb, (int)ngr, scales_w, bias, y);
+    TKV_LAUNCH_CHECK();
+    return TKV_HIP_OK;
+}
+
+int launch_decode_q8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w,
+                     const float* gs, int64_t ldk, int64_t n, const float* bias, float* y) {
+    if (m < 1 || m > kDecodeMaxM || k % 64 != 0 || k / 64 > (int64_t)kMaxWaves * kKsw ||
+        ldk % 128 != 0 || ldk < k || !aligned(x, 16) || !aligned(w, 16) || n < 1 ||
+        n >= (1ll << 28))
+        return TKV_HIP_UNSUPPORTED;
+    const int64_t ncb = ceil_div(n, (int64_t)16);
+    int rg = decode_rows_per_group(c, m, ncb, c->num_cus);
+    // the group's codes, dots and scales must fit the workgroup's LDS (1 KB
+    // kept for the kernel's static arrays): fewer tokens per group otherwise
+    while (rg > 1 && q8_decode_lds(k, rg) + 1024 > (int64_t)c->max_lds) rg--;
+    if (q8_decode_lds(k, rg) + 1024 > (int64_t)c->max_lds) return TKV_HIP_UNSUPPORTED;
+    const int64_t ngr = ceil_div(m, (int64_t)rg);
+    const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
+    const size_t lds = (size_t)q8_decode_lds(k, rg);
+    hipLaunchKernelGGL(k_decode_q8, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
+                       (unsigned)lds, c->stream, x, w, gs, (int)m, (int)n, (int)k, (int)ldk, rg,
+                       (int)ncb, (int)ngr, bias, y);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -102,6 +102,11 @@ static int linear_forward(Ctx* c, Weight* wt, const float* x, int64_t m, int32_t
                                         wt->ldk, wt->n, wt->scales, wt->bias, y);
         if (rc != TKV_HIP_UNSUPPORTED) return rc;
     }
+    if (wt->format == TKV_HIP_WEIGHT_Q8_0 && act_mode == TKV_HIP_ACT_PER_TOKEN) {
+        const int rc = launch_decode_q8(c, x, m, k, static_cast<const uint8_t*>(wt->codes),
+                                        wt->gscales, wt->ldk, wt->n, wt->bias, y);
+        if (rc != TKV_HIP_UNSUPPORTED) return rc;
+    }
     if (wt->ldk != k)
         return set_error(TKV_HIP_UNSUPPORTED, "linear_forward: K must be a multiple of the GEMM K step (128)");
     void* qa;

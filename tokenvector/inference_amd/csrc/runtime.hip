@@ -40,7 +40,7 @@ bool hip_path_enabled() {
     return enabled;
 }
 
-static int check_device(int device, int* num_cus) {
+static int check_device(int device, int* num_cus, size_t* max_lds = nullptr) {
     int count = 0;
     hipError_t e = hipGetDeviceCount(&count);
     if (e != hipSuccess || count == 0)
@@ -53,16 +53,19 @@ static int check_device(int device, int* num_cus) {
         return set_error(TKV_HIP_NO_DEVICE,
                          std::string("libtkv_hip is built for gfx950, device is ") + prop.gcnArchName);
     *num_cus = prop.multiProcessorCount;
+    if (max_lds) *max_lds = prop.sharedMemPerBlock;
     return TKV_HIP_OK;
 }
 
 int ctx_create(int device, Ctx** out) {
     int cus = 0;
-    TKV_RC_TRY(check_device(device, &cus));
+    size_t lds = 0;
+    TKV_RC_TRY(check_device(device, &cus, &lds));
     TKV_HIP_TRY(hipSetDevice(device));
     Ctx* c = new Ctx();
     c->device = device;
     c->num_cus = cus;
+    if (lds) c->max_lds = lds;
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete c;

@@ -61,6 +61,7 @@ struct Ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     int num_cus = 256;
+    size_t max_lds = 65536;  // LDS bytes a workgroup may use (static + dynamic)
     // reduction scratch: kMaxReduceBlocks per-block partials (written by the
     // partials kernel, read by the finalize kernel; no clearing needed)
     RedPartial* partials = nullptr;
@@ -245,6 +246,12 @@ int64_t gguf_block_bytes(int dtype);
 // INT8 GEMM against W [n, ldk], y = fl32(fl64(fl64(acc * sa[m]) * sw[n]) + b[n]).
 int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t ldk,
                      int64_t n, const float* scales_w, const float* bias, float* y);
+// The same for GGUF Q8_0 weights (extension): codes w [n, ldk], group
+// scales gs [n, ldk / 32], the Q8_0 GEMM's recipe (one fma per 32-element
+// group, in order); ldk % 128 == 0.  UNSUPPORTED as above, with nothing
+// launched.
+int launch_decode_q8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w,
+                     const float* gs, int64_t ldk, int64_t n, const float* bias, float* y);
 // gemm_q8.hip: GGUF Q8_0 weights on the INT8 MFMA (extension).
 // Unpack n rows of k / 32 raw blocks (34 bytes) into codes [n, ldk] (16-byte
 // aligned, padding left as it is) and group scales gs [n, ldk / 32] (padding
