@@ -212,6 +212,9 @@ static void device_checks() {
             CHECK(tkv_hip_linear_forward(ctx, wq, (const float*)dx, m, mode, (float*)dy) ==
                       TKV_HIP_OK,
                   "q8_0 linear_forward");
+        CHECK(tkv_hip_linear_forward(ctx, wq, (const float*)dx, 5, TKV_HIP_ACT_PER_TOKEN,
+                                     (float*)dy) == TKV_HIP_OK,
+              "q8_0 linear_forward, decode batch");
         void *codes = nullptr, *dqa = nullptr, *dsa = nullptr;
         float* gsc_dev = nullptr;
         int64_t wn = 0, wk = 0;
