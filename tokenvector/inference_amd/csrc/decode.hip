@@ -268,27 +268,29 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
     const int gstride = ldk / 32;
 
     // Loads as in k_decode_i8 (unconditional weights from a clamped k-step,
-    // lane-masked activation chunks with no default): the B operand of group
-    // g = 2 ks + h is column n0 + lr, bytes [32 g + 8 kg, +8); each thread
-    // also takes up to two of the 16 columns' group scales (16 * K / 32 <=
-    // 1.5 threads' worth), stored to LDS once the loads are all issued.
+    // lane-masked activation chunks with no default): lane (lr, kg) loads
+    // bytes [64 ks + 16 kg, +16) of column n0 + lr per 64-deep k-step, one
+    // 16-byte load for two groups (8-byte loads per group, twice the load
+    // instructions, measured 1.6-1.9x this kernel's INT8 counterpart at
+    // K = 3072, M = 1).  Each thread also takes up to two of the 16 columns'
+    // group scales (16 * K / 32 <= 1.5 threads' worth), stored to LDS once
+    // the loads are all issued.
     const int wcol = n0 + lr < N ? n0 + lr : N - 1;
-    const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + 8 * kg;
-    int64_t wf[kKsw][2];
+    const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + 16 * kg;
+    v4i wq[kKsw];
 #pragma unroll
     for (int s = 0; s < kKsw; s++) {
         const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-            wf[s][h] = __builtin_nontemporal_load(
-                reinterpret_cast<const int64_t*>(wp + (2 * ks + h) * 32));
+        wq[s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64));
     }
+    // scale i is group i % nkb of column i / nkb: consecutive threads read
+    // consecutive groups of one column (coalesced)
     float dv[2];
 #pragma unroll
     for (int q = 0; q < 2; q++) {
         int i = (int)threadIdx.x + q * nthreads;
         i = i < 16 * nkb ? i : 16 * nkb - 1;
-        const int c = i & 15, g = i >> 4;
+        const int c = i / nkb, g = i - c * nkb;
         const int col = n0 + c < N ? n0 + c : N - 1;
         dv[q] = gs[(int64_t)col * gstride + g];
     }
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
 #pragma unroll
     for (int q = 0; q < 2; q++) {
         const int i = (int)threadIdx.x + q * nthreads;
-        if (i < 16 * nkb) s_d[(i & 15) * nkp + (i >> 4)] = dv[q];
+        if (i < 16 * nkb) s_d[(i / nkb) * nkp + i % nkb] = dv[q];
     }
     __syncthreads();
     if (threadIdx.x < rows) {
@@ -344,10 +346,35 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
         }
     }
     __syncthreads();
-    // Group dots: the A operand of group g is row lr's codes [32 g + 8 kg,
-    // +8), the first or second half of 16-byte chunk 2 g + kg / 2; rows past
-    // the group read 0.  The result holds column lr, rows 4 kg + i.
+    // Group dots.  Lane kg < 2 holds 16 bytes of group 2 ks, lane kg >= 2 of
+    // group 2 ks + 1; lanes l and l ^ 32 swap one 8-byte half, after which
+    // every lane holds one 8-byte piece of each group: kg 0..3 hold bytes
+    // [8 j, +8) of both groups with j = 0, 2, 1, 3 (low half: group 2 ks,
+    // high half: group 2 ks + 1).  A dot product only needs A and B in the
+    // same k order, so the A operand of group g is row lr's codes at that same
+    // offset, 32 g + 8 j: the first or second half (kg / 2) of 16-byte chunk
+    // 2 g + (kg & 1).  Rows past the group read 0.  The result holds column
+    // lr, rows 4 kg + i.
+    // (the swaps run for every k-step, including clamped ones past nks,
+    // before any MFMA: outside the k-step branch they are issued together)
     const v4i zero = {0, 0, 0, 0};
+    const bool lo_half = kg < 2;
+    int64_t wf[kKsw][2];
+#pragma unroll
+    for (int s = 0; s < kKsw; s++) {
+        v4i w = wq[s];
+        const int r0 = __shfl_xor(lo_half ? w.z : w.x, 32);
+        const int r1 = __shfl_xor(lo_half ? w.w : w.y, 32);
+        if (lo_half) {
+            w.z = r0;
+            w.w = r1;
+        } else {
+            w.x = r0;
+            w.y = r1;
+        }
+        wf[s][0] = (int64_t)(uint32_t)w.x | ((int64_t)w.y << 32);
+        wf[s][1] = (int64_t)(uint32_t)w.z | ((int64_t)w.w << 32);
+    }
 #pragma unroll
     for (int s = 0; s < kKsw; s++) {
         const int ks = ks0 + s;
@@ -357,7 +384,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
                 const int g = 2 * ks + h;
                 const int64_t af =
                     lr < rows ? *reinterpret_cast<const int64_t*>(
-                                    s_a + (((2 * g + (kg >> 1)) * RG + lr) << 4) + 8 * (kg & 1))
+                                    s_a + (((2 * g + (kg & 1)) * RG + lr) << 4) + 8 * (kg >> 1))
                               : 0;
                 const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, wf[s][h], zero, 0, 0, 0);
 #pragma unroll
