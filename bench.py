@@ -734,7 +734,7 @@ def main():
                      "per_shape": gemm["per_shape"]},
     }
     for key, sec in (("quantize", "quant"), ("fp8", "fp8"), ("decode", "decode"),
-                     ("qlinear", "qlinear"), ("int4", "int4")):
+                     ("qlinear", "qlinear"), ("q8_0", "q8_0"), ("int4", "int4")):
         if sec in r:
             line[key] = r[sec]
     if not args.no_cpu_baseline:
