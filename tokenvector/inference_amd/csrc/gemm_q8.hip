@@ -15,9 +15,12 @@
 //
 // Kernel: 64 x 128 tiles, 4 waves of 32 x 64 (1 x 2 blocks of 32 x 32), three
 // workgroups per CU, persistent over tiles in XCD order.  A 2-slot ring of
-// 128-deep K slices is filled by LDS DMA (issue_slice), each slice with a
-// 2 KB slab of the tile's group scales (128 columns x 4 groups, 16 bytes per
-// column, copied by waves 0 and 1); one barrier per slice.  A 32-deep k-step
+// 128-deep K slices is filled by LDS DMA (issue_slice); each lane loads its
+// own columns' 4 group scales of the next slice (one 16-byte load per
+// column block) into registers with that slice's DMA; one barrier per slice.
+// (A scale slab filled by DMA beside the operands made the compiler wait
+// vmcnt(0) for every slice's DMAs before reading the current slice's scales:
+// it could not tell the slab being filled from the one being read.)  A 32-deep k-step
 // is one group: one v_mfma_i32_32x32x32_i8 per block into a zero
 // accumulator, then per lane 16 conversions and 16 fmas into the f32
 // accumulators.  Those two VALU operations per output and group take four
@@ -41,20 +44,20 @@ namespace {
 typedef Cfg<64, 128, 2, 2, 128, 2> CfgQ8;  // 48 KB ring + 4 KB of scale slabs
 constexpr int kQ8PerCU = 3;                  // resident workgroups per CU
 constexpr int kGroupsPerSlice = CfgQ8::BK / 32;
-constexpr int kSlabBytes = CfgQ8::BN * kGroupsPerSlice * 4;
-static_assert(CfgQ8::BN == 128 && CfgQ8::WAVES >= 2, "waves 0 and 1 copy 64 columns' scales each");
-static_assert(kQ8PerCU * (CfgQ8::LDS_BYTES + CfgQ8::STAGES * kSlabBytes) <= 163840,
-              "LDS of the resident workgroups");
+static_assert(kGroupsPerSlice == 4, "one float4 of group scales per column and slice");
+static_assert(kQ8PerCU * CfgQ8::LDS_BYTES <= 163840, "LDS of the resident workgroups");
 
-// Group scales of slice kt for tile columns [n0, n0 + 128): lane l of wave w
-// (w < 2) copies column n0 + 64 w + l's 16 bytes (4 groups) to slab byte
-// (64 w + l) * 16.  Columns past N read column N - 1 (never stored).
-__device__ __forceinline__ void issue_scales(const float* __restrict__ gs, int gstride, int N,
-                                             int n0, int kt, uint8_t* slab, int wave, int lane) {
-    if (wave < CfgQ8::BN / 64) {
-        const int col = n0 + wave * 64 + lane;
-        const float* g = gs + (int64_t)(col < N ? col : N - 1) * gstride + kt * kGroupsPerSlice;
-        __builtin_amdgcn_global_load_lds((const void*)g, (lds_ptr)(slab + wave * 1024), 16, 0, 0);
+// The 4 group scales of slice kt for the lane's column of each block j
+// (tile column w_row[j]); columns past N read column N - 1 (never stored).
+template <int TN>
+__device__ __forceinline__ void load_scales(const float* __restrict__ gs, int gstride, int N,
+                                            int n0, int kt, const int (&w_row)[TN],
+                                            float4 (&d4)[TN]) {
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int col = n0 + w_row[j] < N ? n0 + w_row[j] : N - 1;
+        d4[j] = *reinterpret_cast<const float4*>(gs + (int64_t)col * gstride +
+                                                 kt * kGroupsPerSlice);
     }
 }
 
@@ -68,7 +71,6 @@ __global__ __launch_bounds__(CfgQ8::THREADS, kQ8PerCU) void k_gemm_q8(
     float* __restrict__ Y) {
     typedef CfgQ8 C;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t slab[C::STAGES][kSlabBytes];
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int wm = wave / C::WN, wn = wave % C::WN, khalf = lane >> 5;
     const int tiles_n = (N + C::BN - 1) / C::BN;
@@ -86,7 +88,8 @@ __global__ __launch_bounds__(CfgQ8::THREADS, kQ8PerCU) void k_gemm_q8(
     int m0 = (t / tiles_n) * C::BM, n0 = (t % tiles_n) * C::BN;
     int slot = 0;
     issue_slice<C>(A, W, M, N, ldk, m0, n0, 0, smem, wave, lane);
-    issue_scales(gs, gstride, N, n0, 0, slab[0], wave, lane);
+    float4 d4[C::TN];
+    load_scales(gs, gstride, N, n0, 0, w_row, d4);
     for (;;) {
         float acc[C::TM][C::TN][16];
 #pragma unroll
@@ -111,21 +114,17 @@ __global__ __launch_bounds__(CfgQ8::THREADS, kQ8PerCU) void k_gemm_q8(
             wait_vmcnt<0>();
             barrier();
             const int nslot = slot ^ 1;
+            uint8_t* const nbase = smem + nslot * C::STAGE_BYTES;
+            float4 dn[C::TN] = {};
             if (kt + 1 < nk) {
-                issue_slice<C>(A, W, M, N, ldk, m0, n0, (kt + 1) * C::BK,
-                               smem + nslot * C::STAGE_BYTES, wave, lane);
-                issue_scales(gs, gstride, N, n0, kt + 1, slab[nslot], wave, lane);
+                issue_slice<C>(A, W, M, N, ldk, m0, n0, (kt + 1) * C::BK, nbase, wave, lane);
+                load_scales(gs, gstride, N, n0, kt + 1, w_row, dn);
             } else if (more) {
-                issue_slice<C>(A, W, M, N, ldk, m0n, n0n, 0, smem + nslot * C::STAGE_BYTES, wave,
-                               lane);
-                issue_scales(gs, gstride, N, n0n, 0, slab[nslot], wave, lane);
+                issue_slice<C>(A, W, M, N, ldk, m0n, n0n, 0, nbase, wave, lane);
+                load_scales(gs, gstride, N, n0n, 0, w_row, dn);
             }
             const uint8_t* sa = smem + slot * C::STAGE_BYTES;
             const uint8_t* sw = sa + C::A_BYTES;
-            float4 d4[C::TN];
-#pragma unroll
-            for (int j = 0; j < C::TN; j++)
-                d4[j] = *reinterpret_cast<const float4*>(slab[slot] + w_row[j] * 16);
 #pragma unroll
             for (int g = 0; g < kGroupsPerSlice; g++) {
                 v4i af[C::TM], bf[C::TN];
@@ -149,6 +148,8 @@ __global__ __launch_bounds__(CfgQ8::THREADS, kQ8PerCU) void k_gemm_q8(
                     }
             }
             slot = nslot;
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) d4[j] = dn[j];
         }
         const EpiOperands<C, ROWS> o = eo.pinned();
         write_tile<C, 0, C::TM * 16>(reinterpret_cast<uint32_t*>(Y), m0, n0, M, N,
