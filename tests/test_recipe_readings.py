@@ -19,7 +19,7 @@ BASELINE config's seeded inputs, how many results differ between them:
         |y_p - y_a| <= 2^-21 * (|acc * sa * sw| + |b|)
     everywhere (the f32 chain rounds three times, the f64 chain once);
   * QL: requantized int8 outputs that differ (by exactly 1 where they do).
-Run with -s to print the table that DESIGN.md quotes.
+Run with -s to print the table of counts.
 
 The exact INT32 accumulators come from a float64 matrix product of the
 codes: every product is an integer below 2^14 and every partial sum an
