@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __re
             zi = s_zi[w] < zi ? s_zi[w] : zi;
         }
         if constexpr (FIN) {
-            store_partial_sc1(partials + blockIdx.x, mn, mx, zi);
+            store_partial_sc1<TRACK_ZERO>(partials + blockIdx.x, mn, mx, zi);
         } else {
             RedPartial p;
             p.mn = mn;
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kRedBlock) void k_minmax_partials(const float* __re
     if constexpr (FIN) {
         if (!arrive_last(arrivals, gridDim.x)) return;
         double dmn, dmx;
-        reduce_partials<true>(x, (int)gridDim.x, TRACK_ZERO, partials, dmn, dmx);
+        reduce_partials_sc1<TRACK_ZERO>(x, (int)gridDim.x, partials, dmn, dmx);
         if (threadIdx.x == 0) {
             if (x0 != x0) dmn = dmx = (double)x0;  // nan_first
             finalize_minmax(dmn, dmx, mode, recipe, out);

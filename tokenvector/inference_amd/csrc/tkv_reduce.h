@@ -120,14 +120,16 @@ __device__ __forceinline__ void arrive_clear(unsigned* counter) {
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One partial as two agent-scope 8-byte stores / loads ({mn, mx}, zidx).
+// One partial as two agent-scope 8-byte stores / loads ({mn, mx}, zidx; the
+// zero index only when it is tracked, TZ).
+template <bool TZ = true>
 __device__ __forceinline__ void store_partial_sc1(RedPartial* p, float mn, float mx,
                                                   unsigned long long zi) {
     const unsigned long long w = (unsigned long long)__float_as_uint(mn) |
                                  ((unsigned long long)__float_as_uint(mx) << 32);
     __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), w, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&p->zidx, zi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (TZ) __hip_atomic_store(&p->zidx, zi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool SC1>
@@ -189,6 +191,67 @@ __device__ inline void reduce_partials(const float* __restrict__ x, int nparts, 
         const double z = x[zi];
         if (mn == 0.0f) dmn = z;
         if (mx == 0.0f) dmx = z;
+    }
+}
+
+// reduce_partials for the last workgroup of a kernel whose workgroups stored
+// their partials with store_partial_sc1<TZ>: every thread issues all of its
+// agent-scope loads before reducing them, one round trip for up to
+// kMaxReduceBlocks partials (indices past nparts reload the last partial,
+// which min / max / first-index ignore; with a loop the compiler waited for
+// each trip's loads in turn), and the zero index is loaded and reduced only
+// when TZ.
+template <bool TZ>
+__device__ inline void reduce_partials_sc1(const float* __restrict__ x, int nparts,
+                                           const RedPartial* __restrict__ partials, double& dmn,
+                                           double& dmx) {
+    constexpr int kPer = kMaxReduceBlocks / kBlock;
+    unsigned long long w[kPer], z[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        int b = (int)threadIdx.x + i * kBlock;
+        b = b < nparts ? b : nparts - 1;
+        w[i] = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(partials + b),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (TZ)
+            z[i] = __hip_atomic_load(&partials[b].zidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float mn = __builtin_inff(), mx = -__builtin_inff();
+    unsigned long long zi = ~0ull;
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        mn = fminf(mn, __uint_as_float((uint32_t)w[i]));
+        mx = fmaxf(mx, __uint_as_float((uint32_t)(w[i] >> 32)));
+        if constexpr (TZ) zi = z[i] < zi ? z[i] : zi;
+    }
+    __shared__ float s_mn[kBlock / 64], s_mx[kBlock / 64];
+    __shared__ unsigned long long s_zi[kBlock / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    if constexpr (TZ) zi = wave_min_u64(zi);
+    if (lane == 0) {
+        s_mn[wave] = mn;
+        s_mx[wave] = mx;
+        if constexpr (TZ) s_zi[wave] = zi;
+    }
+    __syncthreads();
+    mn = s_mn[0];
+    mx = s_mx[0];
+    if constexpr (TZ) zi = s_zi[0];
+    for (int v = 1; v < kBlock / 64; v++) {
+        mn = fminf(mn, s_mn[v]);
+        mx = fmaxf(mx, s_mx[v]);
+        if constexpr (TZ) zi = s_zi[v] < zi ? s_zi[v] : zi;
+    }
+    dmn = mn;
+    dmx = mx;
+    if constexpr (TZ) {
+        if (zi != ~0ull) {
+            const double zv = x[zi];
+            if (mn == 0.0f) dmn = zv;
+            if (mx == 0.0f) dmx = zv;
+        }
     }
 }
 
