@@ -41,7 +41,7 @@ namespace tkv {
 namespace gemm {
 namespace {
 
-typedef Cfg<64, 128, 2, 2, 128, 2> CfgQ8;  // 48 KB ring + 4 KB of scale slabs
+typedef Cfg<64, 128, 2, 2, 128, 2> CfgQ8;  // 48 KB ring (2 slots of 64 + 128 rows x 128 B)
 constexpr int kQ8PerCU = 3;                  // resident workgroups per CU
 constexpr int kGroupsPerSlice = CfgQ8::BK / 32;
 static_assert(kGroupsPerSlice == 4, "one float4 of group scales per column and slice");
@@ -202,6 +202,7 @@ int launch_q8_0_unpack(Ctx* c, const uint8_t* raw, int64_t n, int64_t k, int64_t
         !gs || !aligned(codes, 16))
         return TKV_HIP_UNSUPPORTED;
     const int64_t gstride = ldk / 32, total = n * gstride;
+    if (total >= (1ll << 31)) return TKV_HIP_UNSUPPORTED;  // one work-item each, < 2^32 in all
     hipLaunchKernelGGL(gemm::k_q8_0_unpack, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
                        c->stream, raw, n, (int)(k / 32), (int)gstride, codes, ldk, gs);
     TKV_LAUNCH_CHECK();
