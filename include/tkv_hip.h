@@ -103,7 +103,10 @@ int32_t tkv_hip_ctx_synchronize(int64_t ctx);
  *   INT4_GEMV_WAVE  0..1   1: INT4 decode batches take the per-column kernel
  *   GRID_SPIN       0..2^20  polls a workgroup of the single-pass calibrate
  *                          + quantize makes at its grid barrier before it
- *                          scans the whole tensor itself (0: at once) */
+ *                          scans the whole tensor itself (0: at once)
+ *   DECODE_DMA      0..1   the per-token decode linear's weight path: 0 each
+ *                          lane's B operand loaded into registers, 1 whole
+ *                          128-byte lines copied into LDS */
 enum {
     TKV_HIP_TUNE_GEMM_CFG = 0,
     TKV_HIP_TUNE_GEMM_STAGGER = 1,
@@ -111,7 +114,8 @@ enum {
     TKV_HIP_TUNE_QUANT_TWO_PASS = 3,
     TKV_HIP_TUNE_INT4_GEMV_WAVE = 4,
     TKV_HIP_TUNE_GRID_SPIN = 5,
-    TKV_HIP_TUNE_COUNT = 6
+    TKV_HIP_TUNE_DECODE_DMA = 6,
+    TKV_HIP_TUNE_COUNT = 7
 };
 int32_t tkv_hip_ctx_set_tuning(int64_t ctx, int32_t knob, int64_t value);
 /* Device memory and copies for callers without their own allocator (tests,

@@ -155,12 +155,13 @@ def test_set_tuning_ranges(hip):
     ctx = D.Context(0)
     ranges = {D.TUNE_GEMM_CFG: (0, 11), D.TUNE_GEMM_STAGGER: (0, 8),
               D.TUNE_DECODE_GROUP: (1, 16), D.TUNE_QUANT_TWO_PASS: (0, 1),
-              D.TUNE_INT4_GEMV_WAVE: (0, 1), D.TUNE_GRID_SPIN: (0, 1 << 20)}
+              D.TUNE_INT4_GEMV_WAVE: (0, 1), D.TUNE_GRID_SPIN: (0, 1 << 20),
+              D.TUNE_DECODE_DMA: (0, 1)}
     for knob, (lo, hi) in ranges.items():
         for v in (lo, hi, -1):
             assert L.tkv_hip_ctx_set_tuning(ctx.handle, knob, v) == _lib.OK, (knob, v)
         for v in (lo - 1 if lo - 1 != -1 else -2, hi + 1):
             assert L.tkv_hip_ctx_set_tuning(ctx.handle, knob, v) == _lib.BAD_ARG, (knob, v)
-    assert L.tkv_hip_ctx_set_tuning(ctx.handle, 6, 0) == _lib.BAD_ARG
+    assert L.tkv_hip_ctx_set_tuning(ctx.handle, 7, 0) == _lib.BAD_ARG
     assert L.tkv_hip_ctx_set_tuning(ctx.handle, -1, 0) == _lib.BAD_ARG
     ctx.close()

@@ -995,23 +995,29 @@ def _per_token_want(x, w, b, m, n, k):
 
 
 DECODE_EDGE = [(1, 100, 64), (3, 17, 128), (5, 33, 192), (17, 200, 1024), (31, 2304, 768),
-               (32, 768, 3072), (2, 768, 3072), (8, 3072, 768), (20, 100, 64), (24, 130, 128)]
+               (32, 768, 3072), (2, 768, 3072), (8, 3072, 768), (20, 100, 64), (24, 130, 128),
+               (9, 300, 448)]
 
 
-@pytest.mark.parametrize("rg", [None, 1, 3, 16])
-def test_decode_linear_edge_cases(ctx, rg):
+@pytest.mark.parametrize("rg,dma", [(None, None), (1, None), (3, None), (16, None),
+                                    (None, 0), (None, 1), (3, 1)])
+def test_decode_linear_edge_cases(ctx, rg, dma):
     """The one-kernel decode linear (per-token quantize + INT8 GEMM +
     epilogue, M <= 32): ragged row groups and column blocks, one to sixteen
     waves, workgroups of several column blocks above 16 tokens (with fewer
     waves than blocks at K = 64 and 128), a zero row (scale floor), a row
     holding NaN (skipped by the absmax, coded 0), an outlier row; forced
-    row-group sizes; and a misaligned x, which takes the two-kernel path.
-    Bit-exact."""
+    row-group sizes; both weight paths forced on every shape (registers, and
+    whole lines through LDS, whose DMA count per wave is 4 at K = 192 and
+    shares lines between waves); and a misaligned x, which takes the
+    two-kernel path.  Bit-exact."""
     ctx.set_tuning(D.TUNE_DECODE_GROUP, -1 if rg is None else rg)
+    ctx.set_tuning(D.TUNE_DECODE_DMA, -1 if dma is None else dma)
     try:
         _decode_edge_cases(ctx, rg)
     finally:
         ctx.set_tuning(D.TUNE_DECODE_GROUP, -1)
+        ctx.set_tuning(D.TUNE_DECODE_DMA, -1)
 
 
 def _decode_edge_cases(ctx, rg):

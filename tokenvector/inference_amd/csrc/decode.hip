@@ -12,10 +12,12 @@
 // is the row's absmax over all of K) and its columns' full weight rows, so
 // it reads both itself and nothing crosses workgroups: no atomics, no
 // barrier, no scratch memory, and the result does not depend on scheduling.
-//   * Every load is issued at the start: the weight fragments (16 B per lane
-//     per 64-deep k-step, the B operand of v_mfma_i32_16x16x64_i8) and the
-//     activation fragments (16 f32 per lane per k-step, the A operand's
-//     elements before quantization); one memory latency covers both.
+//   * Every load is issued at the start: the activation fragments (16 f32
+//     per lane per k-step, the A operand's elements before quantization),
+//     then the workgroup's weight rows, copied straight into LDS (direct DMA,
+//     whole 128-byte lines of 8 rows per instruction); the row scales are
+//     formed while the weight lines land, and the B operands of
+//     v_mfma_i32_16x16x64_i8 are read from LDS.
 //   * Wave w takes the contiguous k-steps [KSW w, KSW w + KSW); the row
 //     absmax is reduced over the 4 lanes sharing a row (shuffles) and then
 //     over the waves (LDS), then each wave quantizes its fragments in
@@ -38,6 +40,7 @@ namespace {
 
 using gemm::v4i;
 using gemm::wave_id;
+using gemm::barrier;
 using gemm::xcd_tile;
 
 constexpr int kKsw = 3;         // 64-deep k-steps per wave
@@ -59,9 +62,26 @@ __device__ __forceinline__ float amax4(float m, const float4 v) {
     return fmaxf(fmaxf(m, fabsf(v.x)), fmaxf(fmaxf(fabsf(v.y), fabsf(v.z)), fabsf(v.w)));
 }
 
-// x f32 [M, K] (16-byte aligned rows, K % 64 == 0), W int8 [N, ldk]
-// (K-major, ldk % 16 == 0), sw f32 [N], bias f32 [N] or null, y f32 [M, N].
-// ncb = ceil(N / 16) column blocks, ngr = ceil(M / RG) row groups.
+// x f32 [M, K] (16-byte aligned rows, K % 64 == 0, K <= KMAX), W int8 [N,
+// ldk] (K-major, ldk % 128 == 0: rows are read in whole 128-byte lines, the
+// padding past K included), sw f32 [N], bias f32 [N] or null, y f32 [M, N].
+// ncb = ceil(N / (16 NCB)) column groups, ngr = ceil(M / RG) row groups.
+//
+// Weight rows in LDS (dynamic, NCB 16 nl 128 bytes, nl = ceil(K / 128)):
+// the workgroup's 16 NCB rows of W arrive by direct DMA, one 1 KB
+// instruction per 128-byte line of 8 rows.  Instruction d = (c nl + p) 2 + h
+// holds line p of rows 16 c + 8 h + r, r = 0 .. 7, lane 8 r + q taking the
+// line's 16-byte chunk q ^ w_swz(8 h + r).  Whole lines per instruction: the
+// 64-byte halves that a B-operand load per lane reads (16 rows per
+// instruction) measured 1.1-1.3x slower per call at M = 16 and 32 (kernel
+// trace, one box).  The swizzle makes a 16-lane read of one chunk of the 16
+// rows hit 16 distinct 16-byte bank groups (and any 8 consecutive lanes of
+// it 8 distinct ones).  Each wave issues DPW instructions per column block,
+// the last ones clamped to the final instruction (repeats write the same
+// bytes).  With little weight per workgroup and at most one workgroup per
+// CU (qkv and mlp_up at M <= 4: 12 KB) the LDS hop costs more than the whole
+// lines save (4.1-4.5 against 4.4-4.8 us cold), so those launches load each
+// lane's B operand straight into registers (DPW = 0, no weight LDS).
 //
 // The activation is quantized only for the group's valid rows: chunk
 // c < nks * 4 * rows is 16 consecutive elements of row c % rows at k =
@@ -75,12 +95,18 @@ __device__ __forceinline__ float amax4(float m, const float4 v) {
 // up to M = 16 in a kernel trace of both on one box.)
 constexpr int kChunks = 3;  // 16 rows * 3072 / (16 elements * 1024 threads) = 3
 
-template <int NCB>
+__device__ __forceinline__ int w_swz(int row) { return (row & 7) ^ (row >> 3); }
+
+template <int NCB, int KMAX, int DPW>
 __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     const float* __restrict__ x, const uint8_t* __restrict__ W, int M, int N, int K, int ldk,
     int RG, int ncb, int ngr, const float* __restrict__ sw, const float* __restrict__ bias,
     float* __restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t s_a[];  // 16 K bytes
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_w[];
+    // The activation codes are an array of their own: the compiler then
+    // knows that their stores and loads cannot touch the weight DMA's bytes
+    // and does not wait for it there.
+    __shared__ __attribute__((aligned(16))) uint8_t s_a[16 * KMAX];
     __shared__ uint32_t s_am[16];
     __shared__ double s_inv[16];
     __shared__ float s_sa[16];
@@ -91,28 +117,30 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
     const int cb = t / ngr, rg = t % ngr;
     const int n0 = cb * 16 * NCB, r0 = rg * RG;
     const int rows = M - r0 < RG ? M - r0 : RG;  // valid rows of this group (1 .. 16)
-    const int nks = K / 64;
+    const int nks = K / 64, nl = (K + 127) / 128;
     const int lr = lane & 15, kg = lane >> 4;
     const int ks0 = wave * kKsw;
 
-    // The weight loads are unconditional, from a clamped k-step (fragments
-    // past nks are never used: the MFMA loop skips them): under the
-    // wave-uniform branch they had, the compiler left a register copy where
-    // the branches join and waited there (vmcnt(0)) for the load, a memory
-    // round trip in the middle of issuing the loads.  The activation loads
-    // stay lane-masked (clamped, every thread past nchunks would load), with
-    // no value for the masked lanes, which nothing reads: a zero there made
-    // the same join copy and wait.
+    // Register form (DPW == 0): the weight loads are unconditional, from a
+    // clamped k-step (fragments past nks are never used: the MFMA loop skips
+    // them): under the wave-uniform branch they had, the compiler left a
+    // register copy where the branches join and waited there (vmcnt(0)) for
+    // the load, a memory round trip in the middle of issuing the loads.  The
+    // activation loads stay lane-masked (clamped, every thread past nchunks
+    // would load), with no value for the masked lanes, which nothing reads: a
+    // zero there made the same join copy and wait.
     // weight fragments (B operand): column n0 + 16 c + lr, bytes [64 ks + 16 kg, +16)
     v4i wf[NCB][kKsw];
+    if constexpr (DPW == 0) {
 #pragma unroll
-    for (int c = 0; c < NCB; c++) {
-        const int wcol = n0 + 16 * c + lr < N ? n0 + 16 * c + lr : N - 1;
-        const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + kg * 16;
+        for (int c = 0; c < NCB; c++) {
+            const int wcol = n0 + 16 * c + lr < N ? n0 + 16 * c + lr : N - 1;
+            const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + kg * 16;
 #pragma unroll
-        for (int s = 0; s < kKsw; s++) {
-            const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
-            wf[c][s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64));
+            for (int s = 0; s < kKsw; s++) {
+                const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
+                wf[c][s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64));
+            }
         }
     }
     // activation chunks of the valid rows
@@ -131,9 +159,32 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
             for (int q = 0; q < 4; q++) xv[j][q] = xp[q];
         }
     }
+    // DMA form: the weight lines, unconditional DMAs from clamped rows and
+    // instruction indices (no branch, and nothing lands in registers).  Lines
+    // past K are the rows' zero padding; the MFMA loop never reads them.
+    if constexpr (DPW > 0) {
+        const int r = lane >> 3, q = lane & 7;
+#pragma unroll
+        for (int c = 0; c < NCB; c++) {
+#pragma unroll
+            for (int i = 0; i < DPW; i++) {
+                const int d0 = wave * DPW + i;
+                const int d = d0 < 2 * nl ? d0 : 2 * nl - 1;
+                const int row = 8 * (d & 1) + r;
+                const int col = n0 + 16 * c + row < N ? n0 + 16 * c + row : N - 1;
+                const uint8_t* g =
+                    W + (int64_t)col * ldk + (d >> 1) * 128 + ((q ^ w_swz(row)) << 4);
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)g, (gemm::lds_ptr)(s_w + ((c * nl) * 2 + d) * 1024), 16, 0, 0);
+            }
+        }
+    }
     if (threadIdx.x < 16) s_am[threadIdx.x] = 0u;
     for (int i = threadIdx.x; i < 256 * NCB; i += nthreads) s_acc[i] = 0;
-    __syncthreads();
+    // Raw barriers (gemm::barrier: lgkmcnt(0), then s_barrier) until the
+    // MFMAs: __syncthreads() is a release fence, which would wait for the
+    // weight DMA (an outstanding LDS write) at the first barrier.
+    barrier();
     // row absmax from 0 (engine.tkv:272-276: NaN never compares greater;
     // fmaxf skips it, so the bits compared below are those of a finite or
     // infinite non-negative value, ordered as unsigned integers)
@@ -147,7 +198,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
             atomicMax(&s_am[crow[j]], __float_as_uint(am));
         }
     }
-    __syncthreads();
+    barrier();
     if (threadIdx.x < rows) {
         double dam = (double)__uint_as_float(s_am[threadIdx.x]);
         if (dam < 0.00000001) dam = 0.00000001;
@@ -155,7 +206,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
         s_inv[threadIdx.x] = 1.0 / sc;
         s_sa[threadIdx.x] = (float)sc;
     }
-    __syncthreads();
+    barrier();
 #pragma unroll
     for (int j = 0; j < kChunks; j++) {
         const int c = (int)threadIdx.x + j * nthreads;
@@ -167,11 +218,18 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
             *reinterpret_cast<v4i*>(s_a + ((ck16[j] * 16 + crow[j]) << 4)) = q;
         }
     }
-    __syncthreads();
+    // every wave's weight DMAs have landed (vmcnt counts them) before any
+    // wave reads the lines, some of which other waves copied
+    if constexpr (DPW > 0) gemm::wait_vmcnt<0>();
+    barrier();
 
     v4i acc[NCB];
 #pragma unroll
     for (int c = 0; c < NCB; c++) acc[c] = v4i{0, 0, 0, 0};
+    // B operand of k-step ks, column block c: chunk 4 (ks & 1) + kg of line
+    // ks >> 1 of row lr
+    const int wrow = ((lr >> 3) << 10) + ((lr & 7) << 7);
+    const int wsw = w_swz(lr);
 #pragma unroll
     for (int s = 0; s < kKsw; s++) {
         const int ks = ks0 + s;
@@ -179,9 +237,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_i8(
             const v4i af = lr < rows
                                ? *reinterpret_cast<const v4i*>(s_a + (((ks * 4 + kg) * 16 + lr) << 4))
                                : v4i{0, 0, 0, 0};
+            const int woff = ((ks >> 1) << 11) + wrow + (((4 * (ks & 1) + kg) ^ wsw) << 4);
 #pragma unroll
-            for (int c = 0; c < NCB; c++)
-                acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, wf[c][s], acc[c], 0, 0, 0);
+            for (int c = 0; c < NCB; c++) {
+                v4i b;
+                if constexpr (DPW > 0)
+                    b = *reinterpret_cast<const v4i*>(s_w + ((c * nl) << 11) + woff);
+                else
+                    b = wf[c][s];
+                acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, b, acc[c], 0, 0, 0);
+            }
         }
     }
     // 16 x 16 result per column block: lane holds column lane & 15, rows
@@ -456,32 +521,66 @@ static int decode_rows_per_group(const Ctx* c, int64_t m, int64_t ncb, int num_c
 int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t ldk,
                      int64_t n, const float* scales_w, const float* bias, float* y) {
     if (m < 1 || m > kDecodeMaxM || k % 64 != 0 || k / 64 > (int64_t)kMaxWaves * kKsw ||
-        ldk % 16 != 0 || ldk < k || !aligned(x, 16) || !aligned(w, 16) || n < 1 ||
+        ldk % 128 != 0 || ldk < k || !aligned(x, 16) || !aligned(w, 16) || n < 1 ||
         n >= (1ll << 28))
         return TKV_HIP_UNSUPPORTED;
     // 16-column blocks per workgroup.  Above 16 tokens a workgroup's row
-    // group is quantized once for several column blocks: 64 columns while
-    // their weight rows stay within 64 KB (K <= 1024), else 32 (cold calls at
-    // M = 32, interleaved rounds on one box: qkv 6.95 -> 6.76 us, mlp_up
-    // 7.08 -> 6.50, mlp_down 8.85 -> 8.44 with 32 columns and 11.0 with 64;
-    // at M = 16 two blocks measured 0.1-0.4 us slower than one).
-    const int ncols = m <= 16 ? 1 : (k <= 1024 ? 4 : 2);
+    // group is quantized once for several column blocks: 64 columns for K <=
+    // 1024, else 32 (cold calls at M = 32, interleaved rounds on one box:
+    // qkv 6.95 -> 6.76 us, mlp_up 7.08 -> 6.50, mlp_down 8.85 -> 8.44 with 32
+    // columns and 11.0 with 64; at M = 16 two blocks measured 0.1-0.4 us
+    // slower than one).
+    int ncols = m <= 16 ? 1 : (k <= 1024 ? 4 : 2);
+    const int64_t nl = ceil_div(k, (int64_t)128);
+    const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
+    const int kmax = k <= 1024 ? 1024 : 3072;
+    // LDS: the weight lines (dynamic), the activation codes and the partial
+    // tiles; fewer column blocks per workgroup if the device's share is less
+    auto lds_of = [&](int nc) { return nc * 16 * nl * 128 + 16 * kmax + 1024 * nc + 512; };
+    while (ncols > 1 && lds_of(ncols) > (int64_t)c->max_lds) ncols /= 2;
+    if (lds_of(ncols) > (int64_t)c->max_lds) return TKV_HIP_UNSUPPORTED;
     const int64_t ncb = ceil_div(n, (int64_t)16 * ncols);
     const int rg = decode_rows_per_group(c, m, ncb, c->num_cus);
     const int64_t ngr = ceil_div(m, (int64_t)rg);
-    const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
-    if (ncols == 4)
-        hipLaunchKernelGGL(k_decode_i8<4>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
-                           (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
-                           rg, (int)ncb, (int)ngr, scales_w, bias, y);
-    else if (ncols == 2)
-        hipLaunchKernelGGL(k_decode_i8<2>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
-                           (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
-                           rg, (int)ncb, (int)ngr, scales_w, bias, y);
-    else
-        hipLaunchKernelGGL(k_decode_i8<1>, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
-                           (unsigned)(16 * k), c->stream, x, w, (int)m, (int)n, (int)k, (int)ldk,
-                           rg, (int)ncb, (int)ngr, scales_w, bias, y);
+    // DMA instructions per wave and column block: 2 nl in all over nw waves
+    // (3 for K = 768 and 3072; at most 4 for any K here).  The register form
+    // (dpw 0) where a workgroup's weight rows are under 32 KB and the grid
+    // fits the CUs in one pass (cold calls, same box, two alternating rounds:
+    // mlp_down M = 32 8.18 -> 7.05 us and M = 1 4.98 -> 4.68 with the DMA;
+    // qkv M = 16 5.94 -> 5.63, M = 32 6.72 -> 6.07; qkv and mlp_up at M <= 4
+    // 4.1-4.5 us in registers against 4.4-4.8 through LDS).
+    int dpw = 2 * nl > 3 * nw ? 4 : 3;
+    if (dpw * nw < 2 * nl) return TKV_HIP_UNSUPPORTED;
+    if (tuned(c, TKV_HIP_TUNE_DECODE_DMA) == 0 ||
+        (tuned(c, TKV_HIP_TUNE_DECODE_DMA) < 0 && ncols * 16 * nl * 128 < (32 << 10) &&
+         ncb * ngr <= c->num_cus))
+        dpw = 0;
+    const dim3 grid((unsigned)(ncb * ngr)), block((unsigned)(nw * 64));
+    const unsigned dyn = dpw ? (unsigned)(ncols * 16 * nl * 128) : 0u;
+#define TKV_DEC(NC, KM)                                                                        \
+    do {                                                                                       \
+        if (dpw == 4)                                                                          \
+            hipLaunchKernelGGL((k_decode_i8<NC, KM, 4>), grid, block, dyn, c->stream, x, w,   \
+                               (int)m, (int)n, (int)k, (int)ldk, rg, (int)ncb, (int)ngr,      \
+                               scales_w, bias, y);                                             \
+        else if (dpw == 3)                                                                     \
+            hipLaunchKernelGGL((k_decode_i8<NC, KM, 3>), grid, block, dyn, c->stream, x, w,   \
+                               (int)m, (int)n, (int)k, (int)ldk, rg, (int)ncb, (int)ngr,      \
+                               scales_w, bias, y);                                             \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_decode_i8<NC, KM, 0>), grid, block, dyn, c->stream, x, w,   \
+                               (int)m, (int)n, (int)k, (int)ldk, rg, (int)ncb, (int)ngr,      \
+                               scales_w, bias, y);                                             \
+    } while (0)
+    if (kmax == 1024) {
+        if (ncols == 4) TKV_DEC(4, 1024);
+        else if (ncols == 2) TKV_DEC(2, 1024);
+        else TKV_DEC(1, 1024);
+    } else {
+        if (ncols == 2) TKV_DEC(2, 3072);
+        else TKV_DEC(1, 3072);
+    }
+#undef TKV_DEC
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }

@@ -207,9 +207,10 @@ constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static uint8_t* g_scratch_ptr[kMaxDevices];
 static int g_scratch_cus[kMaxDevices];
+static size_t g_scratch_lds[kMaxDevices];
 
 // The calling thread's current device must be `dev`.
-static int static_scratch(int dev, uint8_t** out, int* cus) {
+static int static_scratch(int dev, uint8_t** out, int* cus, size_t* lds) {
     if (dev < 0 || dev >= kMaxDevices) return set_error(TKV_HIP_NO_DEVICE, "device index out of range");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
@@ -218,10 +219,14 @@ static int static_scratch(int dev, uint8_t** out, int* cus) {
         int n = 0;
         TKV_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
         g_scratch_cus[dev] = n;
+        int l = 0;
+        TKV_HIP_TRY(hipDeviceGetAttribute(&l, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+        g_scratch_lds[dev] = (size_t)l;
         g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
     }
     *out = g_scratch_ptr[dev];
     *cus = g_scratch_cus[dev];
+    *lds = g_scratch_lds[dev];
     return TKV_HIP_OK;
 }
 
@@ -418,10 +423,12 @@ static int linear_forward_static_on(Weight* wt, const float* x, int64_t m, int32
                                     float* y, void* stream) {
     uint8_t* base;
     int cus;
-    TKV_RC_TRY(static_scratch(wt->device, &base, &cus));
+    size_t lds;
+    TKV_RC_TRY(static_scratch(wt->device, &base, &cus, &lds));
     Ctx c;
     c.device = wt->device;
     c.num_cus = cus;
+    if (lds) c.max_lds = lds;
     c.stream = static_cast<hipStream_t>(stream);
     c.own_stream = nullptr;
     c.no_alloc = true;

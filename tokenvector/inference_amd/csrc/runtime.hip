@@ -303,8 +303,8 @@ int32_t tkv_hip_ctx_get_stream(int64_t ctx, void** stream_out) {
 int32_t tkv_hip_ctx_set_tuning(int64_t ctx, int32_t knob, int64_t value) {
     Ctx* c;
     TKV_RC_TRY(ctx_get(ctx, &c));
-    static const int64_t hi[TKV_HIP_TUNE_COUNT] = {11, 8, 16, 1, 1, 1 << 20};
-    static const int64_t lo[TKV_HIP_TUNE_COUNT] = {0, 0, 1, 0, 0, 0};
+    static const int64_t hi[TKV_HIP_TUNE_COUNT] = {11, 8, 16, 1, 1, 1 << 20, 1};
+    static const int64_t lo[TKV_HIP_TUNE_COUNT] = {0, 0, 1, 0, 0, 0, 0};
     if (knob < 0 || knob >= TKV_HIP_TUNE_COUNT)
         return set_error(TKV_HIP_BAD_ARG, "set_tuning: unknown knob " + std::to_string(knob));
     if (value != -1 && (value < lo[knob] || value > hi[knob]))

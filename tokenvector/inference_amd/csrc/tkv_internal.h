@@ -99,7 +99,7 @@ struct Ctx {
     // its workspaces never grow; a call that would need more fails.
     bool no_alloc = false;
     // Tuning overrides (TKV_HIP_TUNE_*), -1 = automatic.
-    int64_t tune[TKV_HIP_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1};
+    int64_t tune[TKV_HIP_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1};
 };
 
 // The override of `knob` on context c, or -1 (automatic).

@@ -38,6 +38,7 @@ TUNE_DECODE_GROUP = 2
 TUNE_QUANT_TWO_PASS = 3
 TUNE_INT4_GEMV_WAVE = 4
 TUNE_GRID_SPIN = 5
+TUNE_DECODE_DMA = 6
 
 
 class Context:
