@@ -259,20 +259,27 @@ Q8_DECODE = [(1, 2304, 768), (4, 768, 3072), (5, 100, 192), (16, 3072, 768), (17
              (32, 2304, 768), (32, 768, 3072)]
 
 
+@pytest.mark.parametrize("dma", [None, 0, 1])
 @pytest.mark.parametrize("m,n,k", Q8_DECODE)
-def test_q8_0_decode(ctx, m, n, k):
+def test_q8_0_decode(ctx, m, n, k, dma):
     """Decode batches (M <= 32, per-token activations) take the one-kernel
     Q8_0 decode path (in-kernel per-token quantize, one MFMA per group, the
-    group chain in LDS): bit-exact against the oracle's rowwise quantizer +
-    tkvo_matmul_q8_0, and the same bits as the tile GEMM on those codes."""
-    say(f"q8_0 decode m={m} n={n} k={k}")
+    group chain in LDS), with the weight path automatic or forced (registers,
+    or whole lines through LDS; 4 DMAs per wave at K = 192): bit-exact
+    against the oracle's rowwise quantizer + tkvo_matmul_q8_0, and the same
+    bits as the tile GEMM on those codes."""
+    say(f"q8_0 decode m={m} n={n} k={k} dma={dma}")
     raw, q, _ = _blocks(n, k, 900 + m + n)
     x = O.gi_noise(m * k, 50 + m, 1.0).reshape(m, k)
     bias = O.gi_noise(n, 51, 0.01)
     wt, db = _weight(ctx, raw, n, k, bias)
     dx = D.DeviceBuffer.from_host(ctx, x)
     dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
-    wt.forward(dx, m, dy, D.ACT_PER_TOKEN)
+    ctx.set_tuning(D.TUNE_DECODE_DMA, -1 if dma is None else dma)
+    try:
+        wt.forward(dx, m, dy, D.ACT_PER_TOKEN)
+    finally:
+        ctx.set_tuning(D.TUNE_DECODE_DMA, -1)
     got = dy.download()
     c, s = O.quantize_dynamic_int8_rowwise(x.reshape(-1), m, k)
     codes = np.asarray(c, np.int32).reshape(m, k)

@@ -310,15 +310,19 @@ __host__ __device__ constexpr int64_t q8_decode_lds(int64_t k, int64_t rg) {
 // load, nkp = K / 32 rounded up to twice an odd number so that the 16
 // columns' rows start in distinct banks.  Dots are kept as f32 (exact, |dot|
 // < 2^24), converted by the waves that form them.
+template <int DPW>
 __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
     const float* __restrict__ x, const uint8_t* __restrict__ W, const float* __restrict__ gs,
     int M, int N, int K, int ldk, int RG, int ncb, int ngr, const float* __restrict__ bias,
     float* __restrict__ y) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
-    const int nks = K / 64, nkb = K / 32, nkp = q8_decode_stride(nkb);
-    uint8_t* s_a = s_dyn;                                                   // [K / 16][RG][16]
-    float* s_p = reinterpret_cast<float*>(s_dyn + RG * K);                  // [RG][16][nkp]
-    float* s_d = reinterpret_cast<float*>(s_dyn + RG * K + RG * 64 * nkp);  // [16][nkp]
+    const int nks = K / 64, nkb = K / 32, nkp = q8_decode_stride(nkb), nl = (K + 127) / 128;
+    // lines form (DPW > 0): the 16 weight rows first, laid out as in k_decode_i8
+    const int wb = DPW > 0 ? 16 * nl * 128 : 0;
+    uint8_t* s_w = s_dyn;
+    uint8_t* s_a = s_dyn + wb;                                                   // [K / 16][RG][16]
+    float* s_p = reinterpret_cast<float*>(s_dyn + wb + RG * K);                  // [RG][16][nkp]
+    float* s_d = reinterpret_cast<float*>(s_dyn + wb + RG * K + RG * 64 * nkp);  // [16][nkp]
     __shared__ uint32_t s_am[16];
     __shared__ double s_inv[16];
     __shared__ float s_sa[16];
@@ -333,20 +337,24 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
     const int gstride = ldk / 32;
 
     // Loads as in k_decode_i8 (unconditional weights from a clamped k-step,
-    // lane-masked activation chunks with no default): lane (lr, kg) loads
-    // bytes [64 ks + 16 kg, +16) of column n0 + lr per 64-deep k-step, one
-    // 16-byte load for two groups (8-byte loads per group, twice the load
-    // instructions, measured 1.6-1.9x this kernel's INT8 counterpart at
-    // K = 3072, M = 1).  Each thread also takes up to two of the 16 columns'
+    // lane-masked activation chunks with no default).  Register form: lane
+    // (lr, kg) loads bytes [64 ks + 16 kg, +16) of column n0 + lr per 64-deep
+    // k-step, one 16-byte load for two groups (8-byte loads per group, twice
+    // the load instructions, measured 1.6-1.9x this kernel's INT8
+    // counterpart at K = 3072, M = 1).  Lines form: the weight rows are
+    // copied into LDS after the activation loads, whole 128-byte lines of 8
+    // rows per DMA.  Each thread also takes up to two of the 16 columns'
     // group scales (16 * K / 32 <= 1.5 threads' worth), stored to LDS once
     // the loads are all issued.
-    const int wcol = n0 + lr < N ? n0 + lr : N - 1;
-    const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + 16 * kg;
     v4i wq[kKsw];
+    if constexpr (DPW == 0) {
+        const int wcol = n0 + lr < N ? n0 + lr : N - 1;
+        const uint8_t* __restrict__ wp = W + (int64_t)wcol * ldk + 16 * kg;
 #pragma unroll
-    for (int s = 0; s < kKsw; s++) {
-        const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
-        wq[s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64));
+        for (int s = 0; s < kKsw; s++) {
+            const int ks = ks0 + s < nks ? ks0 + s : nks - 1;
+            wq[s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + ks * 64));
+        }
     }
     // scale i is group i % nkb of column i / nkb: consecutive threads read
     // consecutive groups of one column (coalesced)
@@ -374,8 +382,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
             for (int q = 0; q < 4; q++) xv[j][q] = xp[q];
         }
     }
+    if constexpr (DPW > 0) {
+        const int r = lane >> 3, q = lane & 7;
+#pragma unroll
+        for (int i = 0; i < DPW; i++) {
+            const int d0 = wave * DPW + i;
+            const int d = d0 < 2 * nl ? d0 : 2 * nl - 1;
+            const int row = 8 * (d & 1) + r;
+            const int col = n0 + row < N ? n0 + row : N - 1;
+            const uint8_t* g = W + (int64_t)col * ldk + (d >> 1) * 128 + ((q ^ w_swz(row)) << 4);
+            __builtin_amdgcn_global_load_lds((const void*)g, (gemm::lds_ptr)(s_w + d * 1024), 16,
+                                             0, 0);
+        }
+    }
     if (threadIdx.x < 16) s_am[threadIdx.x] = 0u;
-    __syncthreads();
+    // raw barriers up to the MFMAs: __syncthreads() would wait for the
+    // weight DMA (an outstanding LDS write) at each one
+    barrier();
 #pragma unroll
     for (int j = 0; j < kChunks; j++) {
         const int c = (int)threadIdx.x + j * nthreads;
@@ -391,7 +414,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
         const int i = (int)threadIdx.x + q * nthreads;
         if (i < 16 * nkb) s_d[(i / nkb) * nkp + i % nkb] = dv[q];
     }
-    __syncthreads();
+    barrier();
     if (threadIdx.x < rows) {
         double dam = (double)__uint_as_float(s_am[threadIdx.x]);
         if (dam < 0.00000001) dam = 0.00000001;
@@ -399,7 +422,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
         s_inv[threadIdx.x] = 1.0 / sc;
         s_sa[threadIdx.x] = (float)sc;
     }
-    __syncthreads();
+    barrier();
 #pragma unroll
     for (int j = 0; j < kChunks; j++) {
         const int c = (int)threadIdx.x + j * nthreads;
@@ -410,7 +433,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
             *reinterpret_cast<v4i*>(s_a + ((ck16[j] * RG + crow[j]) << 4)) = q;
         }
     }
-    __syncthreads();
+    if constexpr (DPW > 0) gemm::wait_vmcnt<0>();  // every wave's weight lines have landed
+    barrier();
     // Group dots.  Lane kg < 2 holds 16 bytes of group 2 ks, lane kg >= 2 of
     // group 2 ks + 1; lanes l and l ^ 32 swap one 8-byte half, after which
     // every lane holds one 8-byte piece of each group: kg 0..3 hold bytes
@@ -422,11 +446,14 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
     // lr, rows 4 kg + i.
     // (the swaps run for every k-step, including clamped ones past nks,
     // before any MFMA: outside the k-step branch they are issued together)
+    // Lines form: the B operand of group g is row lr's bytes [32 g + 8 kg,
+    // +8) (16-byte chunk 2 (g & 3) + kg / 2 of line g / 4, half kg & 1), the
+    // k order unpermuted, so A reads the same offset of its row's codes.
     const v4i zero = {0, 0, 0, 0};
     const bool lo_half = kg < 2;
     int64_t wf[kKsw][2];
 #pragma unroll
-    for (int s = 0; s < kKsw; s++) {
+    for (int s = 0; s < kKsw && DPW == 0; s++) {
         v4i w = wq[s];
         const int r0 = __shfl_xor(lo_half ? w.z : w.x, 32);
         const int r1 = __shfl_xor(lo_half ? w.w : w.y, 32);
@@ -447,11 +474,22 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_decode_q8(
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int g = 2 * ks + h;
-                const int64_t af =
-                    lr < rows ? *reinterpret_cast<const int64_t*>(
-                                    s_a + (((2 * g + (kg & 1)) * RG + lr) << 4) + 8 * (kg >> 1))
-                              : 0;
-                const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, wf[s][h], zero, 0, 0, 0);
+                int64_t af, bw;
+                if constexpr (DPW > 0) {
+                    af = lr < rows ? *reinterpret_cast<const int64_t*>(
+                                         s_a + (((2 * g + (kg >> 1)) * RG + lr) << 4) + 8 * (kg & 1))
+                                   : 0;
+                    const int ch = 2 * (g & 3) + (kg >> 1);
+                    bw = *reinterpret_cast<const int64_t*>(
+                        s_w + ((((g >> 2) << 1) + (lr >> 3)) << 10) +
+                        ((((lr & 7) << 3) + (ch ^ w_swz(lr))) << 4) + 8 * (kg & 1));
+                } else {
+                    af = lr < rows ? *reinterpret_cast<const int64_t*>(
+                                         s_a + (((2 * g + (kg & 1)) * RG + lr) << 4) + 8 * (kg >> 1))
+                                   : 0;
+                    bw = wf[s][h];
+                }
+                const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bw, zero, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     if (4 * kg + i < rows) s_p[((4 * kg + i) * 16 + lr) * nkp + g] = (float)p[i];
@@ -593,16 +631,37 @@ int launch_decode_q8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
         return TKV_HIP_UNSUPPORTED;
     const int64_t ncb = ceil_div(n, (int64_t)16);
     int rg = decode_rows_per_group(c, m, ncb, c->num_cus);
-    // the group's codes, dots and scales must fit the workgroup's LDS (1 KB
-    // kept for the kernel's static arrays): fewer tokens per group otherwise
-    while (rg > 1 && q8_decode_lds(k, rg) + 1024 > (int64_t)c->max_lds) rg--;
-    if (q8_decode_lds(k, rg) + 1024 > (int64_t)c->max_lds) return TKV_HIP_UNSUPPORTED;
-    const int64_t ngr = ceil_div(m, (int64_t)rg);
+    const int64_t nl = ceil_div(k, (int64_t)128);
     const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
-    const size_t lds = (size_t)q8_decode_lds(k, rg);
-    hipLaunchKernelGGL(k_decode_q8, dim3((unsigned)(ncb * ngr)), dim3((unsigned)(nw * 64)),
-                       (unsigned)lds, c->stream, x, w, gs, (int)m, (int)n, (int)k, (int)ldk, rg,
-                       (int)ncb, (int)ngr, bias, y);
+    const int64_t max_lds = (int64_t)c->max_lds;
+    // Lines form (the weight rows through LDS in whole lines, as in
+    // k_decode_i8) by the same rule: 32 KB of weight rows per workgroup or
+    // more workgroups than CUs, if it fits; the context knob forces either.
+    const int dpw = 2 * nl > 3 * nw ? 4 : 3;
+    if (dpw * nw < 2 * nl) return TKV_HIP_UNSUPPORTED;
+    const int64_t wbytes = 16 * nl * 128;
+    const int64_t knob = tuned(c, TKV_HIP_TUNE_DECODE_DMA);
+    bool lines = knob >= 0 ? knob == 1
+                           : (wbytes >= (32 << 10) || ncb * ceil_div(m, (int64_t)rg) > c->num_cus);
+    // the group's codes, dots and scales (and the lines) must fit the
+    // workgroup's LDS (1 KB kept for the kernel's static arrays): fewer
+    // tokens per group otherwise
+    auto lds_of = [&](int r) { return q8_decode_lds(k, r) + (lines ? wbytes : 0) + 1024; };
+    if (lines && lds_of(1) > max_lds) lines = false;
+    while (rg > 1 && lds_of(rg) > max_lds) rg--;
+    if (lds_of(rg) > max_lds) return TKV_HIP_UNSUPPORTED;
+    const int64_t ngr = ceil_div(m, (int64_t)rg);
+    const dim3 grid((unsigned)(ncb * ngr)), block((unsigned)(nw * 64));
+    const unsigned lds = (unsigned)(lds_of(rg) - 1024);
+    if (!lines)
+        hipLaunchKernelGGL(k_decode_q8<0>, grid, block, lds, c->stream, x, w, gs, (int)m, (int)n,
+                           (int)k, (int)ldk, rg, (int)ncb, (int)ngr, bias, y);
+    else if (dpw == 4)
+        hipLaunchKernelGGL(k_decode_q8<4>, grid, block, lds, c->stream, x, w, gs, (int)m, (int)n,
+                           (int)k, (int)ldk, rg, (int)ncb, (int)ngr, bias, y);
+    else
+        hipLaunchKernelGGL(k_decode_q8<3>, grid, block, lds, c->stream, x, w, gs, (int)m, (int)n,
+                           (int)k, (int)ldk, rg, (int)ncb, (int)ngr, bias, y);
     TKV_LAUNCH_CHECK();
     return TKV_HIP_OK;
 }
