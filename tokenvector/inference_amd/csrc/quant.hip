@@ -755,7 +755,7 @@ __device__ __forceinline__ void quant_row(const float4 (&v)[C4], int64_t r, int6
     for (int c = 0; c < C4; c++)
         al = fmaxf(fmaxf(al, fabsf(v[c].x)),
                    fmaxf(fabsf(v[c].y), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
-    double am = (double)wave_max(al);
+    double am = (double)wave_max_nonneg(al);
     if (am < 0.00000001) am = 0.00000001;
     const double sc = am / 127.0;
     if (lane == 0) scales_out[r] = (float)sc;

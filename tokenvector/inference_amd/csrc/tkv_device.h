@@ -154,6 +154,26 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
+// Max over the wave of a non-negative, non-NaN value, returned to every
+// lane: DPP row shifts and row broadcasts (VALU only) leave it in lane 63,
+// then one readlane.  Lanes without a DPP source read 0, which such a max
+// ignores.  wave_max's shuffles are ds_bpermute, one dependent LDS round trip
+// per step.  The whole wave must be active.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    int b = __float_as_int(v);
+#define TKV_DPP_MAX(CTRL, ROWS)                                                       \
+    b = __float_as_int(fmaxf(__int_as_float(b),                                        \
+                             __int_as_float(__builtin_amdgcn_update_dpp(0, b, CTRL, ROWS, \
+                                                                       0xf, false))))
+    TKV_DPP_MAX(0x111, 0xf);  // row_shr:1
+    TKV_DPP_MAX(0x112, 0xf);  // row_shr:2
+    TKV_DPP_MAX(0x114, 0xf);  // row_shr:4
+    TKV_DPP_MAX(0x118, 0xf);  // row_shr:8: lane 15 of each row holds its row's max
+    TKV_DPP_MAX(0x142, 0xa);  // row_bcast:15 into rows 1 and 3
+    TKV_DPP_MAX(0x143, 0xc);  // row_bcast:31 into rows 2 and 3: lane 63 holds the max
+#undef TKV_DPP_MAX
+    return __int_as_float(__builtin_amdgcn_readlane(b, 63));
+}
 __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
