@@ -572,11 +572,14 @@ int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
     const int64_t nl = ceil_div(k, (int64_t)128);
     const int64_t nw = ceil_div(k / 64, (int64_t)kKsw);
     const int kmax = k <= 1024 ? 1024 : 3072;
-    // LDS: the weight lines (dynamic), the activation codes and the partial
-    // tiles; fewer column blocks per workgroup if the device's share is less
-    auto lds_of = [&](int nc) { return nc * 16 * nl * 128 + 16 * kmax + 1024 * nc + 512; };
-    while (ncols > 1 && lds_of(ncols) > (int64_t)c->max_lds) ncols /= 2;
-    if (lds_of(ncols) > (int64_t)c->max_lds) return TKV_HIP_UNSUPPORTED;
+    // LDS: the activation codes and the partial tiles (fewer column blocks
+    // per workgroup if the device's share is less), plus the weight lines
+    // (dynamic) in the DMA form, which is taken only where they fit
+    const int64_t max_lds = (int64_t)c->max_lds;
+    auto lds_reg = [&](int nc) { return (int64_t)16 * kmax + 1024 * nc + 512; };
+    auto lds_dma = [&](int nc) { return nc * 16 * nl * 128 + lds_reg(nc); };
+    while (ncols > 1 && lds_reg(ncols) > max_lds) ncols /= 2;
+    if (lds_reg(ncols) > max_lds) return TKV_HIP_UNSUPPORTED;
     const int64_t ncb = ceil_div(n, (int64_t)16 * ncols);
     const int rg = decode_rows_per_group(c, m, ncb, c->num_cus);
     const int64_t ngr = ceil_div(m, (int64_t)rg);
@@ -588,10 +591,10 @@ int launch_decode_i8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
     // qkv M = 16 5.94 -> 5.63, M = 32 6.72 -> 6.07; qkv and mlp_up at M <= 4
     // 4.1-4.5 us in registers against 4.4-4.8 through LDS).
     int dpw = 2 * nl > 3 * nw ? 4 : 3;
-    if (dpw * nw < 2 * nl) return TKV_HIP_UNSUPPORTED;
     if (tuned(c, TKV_HIP_TUNE_DECODE_DMA) == 0 ||
         (tuned(c, TKV_HIP_TUNE_DECODE_DMA) < 0 && ncols * 16 * nl * 128 < (32 << 10) &&
-         ncb * ngr <= c->num_cus))
+         ncb * ngr <= c->num_cus) ||
+        dpw * nw < 2 * nl || lds_dma(ncols) > max_lds)
         dpw = 0;
     const dim3 grid((unsigned)(ncb * ngr)), block((unsigned)(nw * 64));
     const unsigned dyn = dpw ? (unsigned)(ncols * 16 * nl * 128) : 0u;
@@ -638,11 +641,11 @@ int launch_decode_q8(Ctx* c, const float* x, int64_t m, int64_t k, const uint8_t
     // k_decode_i8) by the same rule: 32 KB of weight rows per workgroup or
     // more workgroups than CUs, if it fits; the context knob forces either.
     const int dpw = 2 * nl > 3 * nw ? 4 : 3;
-    if (dpw * nw < 2 * nl) return TKV_HIP_UNSUPPORTED;
     const int64_t wbytes = 16 * nl * 128;
     const int64_t knob = tuned(c, TKV_HIP_TUNE_DECODE_DMA);
     bool lines = knob >= 0 ? knob == 1
                            : (wbytes >= (32 << 10) || ncb * ceil_div(m, (int64_t)rg) > c->num_cus);
+    if (dpw * nw < 2 * nl) lines = false;
     // the group's codes, dots and scales (and the lines) must fit the
     // workgroup's LDS (1 KB kept for the kernel's static arrays): fewer
     // tokens per group otherwise
