@@ -914,6 +914,56 @@ def test_gemm_every_config_int8(ctx, gemm_cfg, cfg):
         assert _same_f32(dy.download(), want), (cfg, "per-tensor", m, n, k)
 
 
+SKINNY_SHAPES = [(1, 1, 128), (1, 768, 3072), (32, 2304, 768), (17, 100, 200), (5, 300, 384),
+                 (32, 768, 768), (4, 8320, 256), (9, 64, 4096)]
+
+
+@pytest.mark.parametrize("dma", [0, 1])
+def test_skinny_weight_paths(ctx, gemm_cfg, dma):
+    """The skinny kernel (M <= 32) with its weight operand loaded per lane
+    into registers (0) or copied into LDS as whole 128-byte lines (1): K
+    split over workgroups (N = 768) and unsplit (one to sixteen waves), ragged
+    N and K (K padded to the 128-byte step), a K range of 32 lines; INT32
+    accumulators exact, the per-token and per-tensor epilogues and
+    QLinearMatMul bit-exact."""
+    gemm_cfg(10)
+    ctx.set_tuning(D.TUNE_DECODE_DMA, dma)
+    try:
+        for m, n, k in SKINNY_SHAPES:
+            say(f"skinny dma={dma} {m}x{n}x{k}")
+            a = RNG.integers(-127, 128, (m, k)).astype(np.int8)
+            w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
+            da, dw = D.DeviceBuffer.from_host(ctx, a), D.DeviceBuffer.from_host(ctx, w)
+            dacc = D.DeviceBuffer.empty(ctx, (m, n), np.int32)
+            D.matmul_int8_accum(ctx, da, dw, m, n, k, dacc)
+            acc = a.astype(np.float64) @ w.astype(np.float64).T
+            assert np.array_equal(dacc.download().astype(np.float64), acc), (dma, m, n, k)
+            sa = RNG.uniform(0.005, 0.05, m).astype(np.float32)
+            sw = RNG.uniform(1e-4, 3e-4, n).astype(np.float32)
+            b = RNG.normal(0, 0.01, n).astype(np.float32)
+            dsa, dsw, db = (D.DeviceBuffer.from_host(ctx, v) for v in (sa, sw, b))
+            dy = D.DeviceBuffer.empty(ctx, (m, n), np.float32)
+            for stride in (1, 0):
+                D.matmul_int8(ctx, da, dw, m, n, k, dsa, stride, 0.0, dsw, db, dy)
+                s_a = sa.astype(np.float64)[:, None] if stride else np.float64(sa[0])
+                want = ((acc * s_a) * sw.astype(np.float64)[None, :]
+                        + b.astype(np.float64)[None, :]).astype(np.float32)
+                assert _same_f32(dy.download(), want), (dma, stride, m, n, k)
+            qsa, qsw = np.float32(0.02), np.float32(0.003)
+            qsy = np.float32(np.sqrt(k) * 128 * 128 * qsa * qsw / 90.0)
+            dq = D.DeviceBuffer.empty(ctx, (m, n), np.int8)
+            _lib_check(D, "tkv_hip_dev_qlinear_matmul", ctx.handle, da.ptr, float(qsa), -3, dw.ptr,
+                       float(qsw), 5, float(qsy), 7, dq.ptr, m, n, k, 0)
+            bq = np.ascontiguousarray(w.reshape(n, k).T).reshape(-1).astype(np.int32)
+            wantq = O.qlinear_matmul(a.reshape(-1).astype(np.int32), qsa, -3, bq, qsw, 5, qsy, 7,
+                                     m * n, m, n, k)
+            assert np.array_equal(dq.download().astype(np.int32).reshape(-1), wantq), (dma, m, n, k)
+            for buf in (da, dw, dacc, dsa, dsw, db, dy, dq):
+                buf.close()
+    finally:
+        ctx.set_tuning(D.TUNE_DECODE_DMA, -1)
+
+
 @pytest.mark.parametrize("cfg", GEMM_CFGS)
 def test_gemm_every_config_fp8(ctx, gemm_cfg, cfg):
     """Both FP8 policies under every tile configuration, to their stated

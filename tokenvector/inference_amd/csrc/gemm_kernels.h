@@ -851,12 +851,20 @@ __global__ __launch_bounds__(C::THREADS, 2) void k_gemm_f(const uint8_t* __restr
 // and are never stored), the partial INT32 tiles are summed exactly with LDS
 // atomics, and wave 0 runs the same epilogue as the tiled kernels on the
 // 32 x 32 tile.
+__device__ __forceinline__ int lines_swz(int row) { return (row & 7) ^ (row >> 3); }
+
 struct CfgGemv {
     static constexpr int BM = 32, BN = 32, WM = 1, WN = 1, WTM = 32, WTN = 32, TM = 1, TN = 1;
 };
 constexpr int kGemvMaxM = 32;
 constexpr int kGemvUnroll = 8;
 
+// LINES: the workgroup's 32 weight rows over its K range go into LDS first
+// by direct DMA, whole 128-byte lines of 8 rows per 1 KB instruction (the
+// rows' 16-byte chunks XOR-swizzled so that 16 lanes reading one chunk of 16
+// rows hit distinct bank groups), and the B operands are read from there; a
+// direct B load reads 32 bytes of each of 32 rows' lines per instruction.
+// ldk % 128 == 0; dynamic LDS: 4 KB per 128-byte line of the K range.
 // SPLIT: workgroup b takes column block b % ncb and the K steps of split
 // b / ncb (of `splits`), so narrow N still spreads over the CUs.  Its INT32
 // partial sums go into part[block][1024] with device-scope atomic adds (exact
@@ -866,7 +874,7 @@ constexpr int kGemvUnroll = 8;
 // clears the count, and runs the epilogue: no workgroup ever waits for
 // another, and part / arrivals are zero again when the kernel ends (zeroed at
 // context creation).
-template <int KW, bool SPLIT, class E>
+template <int KW, bool SPLIT, class E, bool LINES = false>
 __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__ A,
                                                      const uint8_t* __restrict__ W, int M, int N,
                                                      int ldk, E ep, void* __restrict__ Y,
@@ -889,14 +897,44 @@ __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__
     v16i acc;
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[i] = 0;
+    // LINES: lines [p_lo, p_hi) of the K range; instruction d = 4 (p - p_lo)
+    // + h holds rows 8 h .. 8 h + 7, lane 8 rr + q taking chunk q ^
+    // lines_swz(8 h + rr)
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_wl[];
+    const int p_lo = k_lo >> 2;
+    auto wfrag = [&](int ks) -> v4i {
+        if constexpr (LINES) {
+            const int ch = 2 * (ks & 3) + kh;
+            return *reinterpret_cast<const v4i*>(
+                s_wl + ((4 * ((ks >> 2) - p_lo) + (r >> 3)) << 10) +
+                ((((r & 7) << 3) + (ch ^ lines_swz(r & 15))) << 4));
+        } else {
+            return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + ks * 32));
+        }
+    };
+    if constexpr (LINES) {
+        const int nd = 4 * (((k_hi + 3) >> 2) - p_lo);
+        const int rr = lane >> 3, q = lane & 7;
+        for (int d = wave; d < nd; d += KW) {
+            const int row = 8 * (d & 3) + rr;
+            const int col = n0 + row < N ? n0 + row : N - 1;
+            const uint8_t* g = W + (int64_t)col * ldk + (int64_t)(p_lo + (d >> 2)) * 128 +
+                               ((q ^ lines_swz(row & 15)) << 4);
+            __builtin_amdgcn_global_load_lds((const void*)g, (lds_ptr)(s_wl + d * 1024), 16, 0,
+                                             0);
+        }
+        // each wave's DMAs have landed, then a raw barrier publishes them
+        // all (__syncthreads() would also wait, being a release fence)
+        wait_vmcnt<0>();
+        barrier();
+    }
     int ks = k_lo + wave;
     for (; ks + (kGemvUnroll - 1) * KW < k_hi; ks += kGemvUnroll * KW) {
         v4i af[kGemvUnroll], wf[kGemvUnroll];
 #pragma unroll
         for (int u = 0; u < kGemvUnroll; u++) {
             af[u] = *reinterpret_cast<const v4i*>(arow + (ks + u * KW) * 32);
-            wf[u] = __builtin_nontemporal_load(
-                reinterpret_cast<const v4i*>(wrow + (ks + u * KW) * 32));
+            wf[u] = wfrag(ks + u * KW);
         }
 #pragma unroll
         for (int u = 0; u < kGemvUnroll; u++)
@@ -904,8 +942,7 @@ __global__ __launch_bounds__(KW * 64) void k_gemv_i8(const uint8_t* __restrict__
     }
     for (; ks < k_hi; ks += KW) {
         const v4i af = *reinterpret_cast<const v4i*>(arow + ks * 32);
-        const v4i wf = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + ks * 32));
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wf, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, wfrag(ks), acc, 0, 0, 0);
     }
     __syncthreads();  // red[] zeroed
     typename PolicyI8::Acc sum[1][1];
@@ -1085,22 +1122,46 @@ static int launch_gemv(Ctx* c, const uint8_t* a, const uint8_t* w, int64_t m, in
                        int64_t ldk, const E& ep, void* y) {
     const int64_t wgs = ceil_div(n, (int64_t)32);
     const int64_t nks = ldk / 32;
+    // Weight path: whole lines through LDS wherever they fit (ldk % 128 == 0,
+    // the K range's lines at 4 KB each within 128 KB), unless the context's
+    // decode weight-path knob forces registers.  Cold weights, one box, two
+    // rounds: unsplit launches (qkv / mlp_up shapes, 16 waves) 4.94 / 5.03 ->
+    // 4.19 / 4.25 us at M = 1 and 5.48 / 5.72 -> 4.76 / 4.81 at M = 32; split
+    // launches (mlp_down, 264 workgroups of 12 KB) within +-0.1 us.
+    const bool want_lines = tuned(c, TKV_HIP_TUNE_DECODE_DMA) != 0 && ldk % 128 == 0;
+    auto lines_lds = [&](int64_t span) { return 4096 * ((span + 3) / 4 + 1); };
     if (wgs * 4 <= c->num_cus && wgs <= kGemvSplitBlocks) {
         int64_t splits = ceil_div((int64_t)c->num_cus, wgs);
         if (splits > nks / 8) splits = nks / 8;
         if (splits >= 2) {
-            hipLaunchKernelGGL((k_gemv_i8<4, true, E>), dim3((unsigned)(wgs * splits)),
-                               dim3(4 * 64), 0, c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y,
-                               (int)splits, c->gemv_part, c->gemv_arrivals);
+            const int64_t lds = lines_lds(ceil_div(nks, splits));
+            if (want_lines && lds <= (128 << 10))
+                hipLaunchKernelGGL((k_gemv_i8<4, true, E, true>), dim3((unsigned)(wgs * splits)),
+                                   dim3(4 * 64), (unsigned)lds, c->stream, a, w, (int)m, (int)n,
+                                   (int)ldk, ep, y, (int)splits, c->gemv_part, c->gemv_arrivals);
+            else
+                hipLaunchKernelGGL((k_gemv_i8<4, true, E>), dim3((unsigned)(wgs * splits)),
+                                   dim3(4 * 64), 0, c->stream, a, w, (int)m, (int)n, (int)ldk, ep,
+                                   y, (int)splits, c->gemv_part, c->gemv_arrivals);
             TKV_LAUNCH_CHECK();
             return TKV_HIP_OK;
         }
     }
     int64_t kw = ceil_div((int64_t)c->num_cus * 8, wgs);
     if (kw > nks) kw = nks;
-#define TKV_GEMV(KW)                                                                          \
-    hipLaunchKernelGGL((k_gemv_i8<KW, false, E>), dim3((unsigned)wgs), dim3(KW * 64), 0,     \
-                       c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, 1, nullptr, nullptr)
+    const int64_t lds = lines_lds(nks);
+    const bool lines = want_lines && lds <= (128 << 10);
+#define TKV_GEMV(KW)                                                                           \
+    do {                                                                                       \
+        if (lines)                                                                             \
+            hipLaunchKernelGGL((k_gemv_i8<KW, false, E, true>), dim3((unsigned)wgs),          \
+                               dim3(KW * 64), (unsigned)lds, c->stream, a, w, (int)m, (int)n, \
+                               (int)ldk, ep, y, 1, nullptr, nullptr);                          \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_gemv_i8<KW, false, E>), dim3((unsigned)wgs), dim3(KW * 64), \
+                               0, c->stream, a, w, (int)m, (int)n, (int)ldk, ep, y, 1, nullptr, \
+                               nullptr);                                                       \
+    } while (0)
     if (kw >= 16)
         TKV_GEMV(16);
     else if (kw >= 8)
