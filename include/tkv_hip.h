@@ -106,9 +106,9 @@ int32_t tkv_hip_ctx_synchronize(int64_t ctx);
  *                          scans the whole tensor itself (0: at once)
  *   DECODE_DMA      0..1   the weight path of the M <= 32 kernels (the
  *                          per-token decode linear with INT8 or GGUF Q8_0
- *                          weights, the skinny INT8 GEMM): 0 each lane's B
- *                          operand loaded into registers, 1 whole 128-byte
- *                          lines copied into LDS */
+ *                          weights, the skinny INT8 GEMM, the INT4 decode
+ *                          kernel): 0 each lane's B operand loaded into
+ *                          registers, 1 whole 128-byte lines copied into LDS */
 enum {
     TKV_HIP_TUNE_GEMM_CFG = 0,
     TKV_HIP_TUNE_GEMM_STAGGER = 1,

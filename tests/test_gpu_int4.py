@@ -258,8 +258,10 @@ def test_int4_matmul_dyadic_exact_and_errors(hip):
                                       ("mlp_up", 3072, 768), ("mlp_down", 768, 3072)])
 def test_int4_decode_gpt2_shapes(ctx, name, n, k, m):
     """Decode batches on the four GPT-2 shapes (group size 128), device
-    buffers: every output within the reordering bound of the oracle, and a
-    second launch bit-identical (the split-K reduction has a fixed order)."""
+    buffers: every output within the reordering bound of the oracle, a
+    second launch bit-identical (the split-K reduction has a fixed order),
+    and the register weight path (the context's decode weight-path knob)
+    bit-identical to the default path through LDS."""
     gs = 128
     say(f"int4 decode {name} m={m}")
     a = O.gi_noise(m * k, 31 + m, 1.0)
@@ -278,6 +280,12 @@ def test_int4_decode_gpt2_shapes(ctx, name, n, k, m):
     for _ in range(2):
         D.matmul_int4_grouped(ctx, da, dw, ds, db, None, dy, m, n, k, gs)
         assert np.array_equal(dy.download(), y)
+    ctx.set_tuning(D.TUNE_DECODE_DMA, 0)
+    try:
+        D.matmul_int4_grouped(ctx, da, dw, ds, db, None, dy, m, n, k, gs)
+    finally:
+        ctx.set_tuning(D.TUNE_DECODE_DMA, -1)
+    assert np.array_equal(dy.download(), y)
 
 
 def test_graph_replays_int4(ctx):

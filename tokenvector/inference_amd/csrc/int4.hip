@@ -641,7 +641,16 @@ __global__ __launch_bounds__(256) void k_gemv_int4_row(
 // 16 were slower (qkv M = 32 9.5 us).
 constexpr int kDecWaves = 8;
 
-template <int MB>
+// LINES: the workgroup's 16 packed weight rows over its k range are copied
+// into LDS first by direct DMA, whole 128-byte lines of 8 rows per 1 KB
+// instruction (16-byte chunks XOR-swizzled per row, so the 64 lanes' 4-byte
+// reads of one k block hit 64 distinct banks); the loop then loads only the
+// activations.  The register form reads 16 bytes of each of 16 rows' lines
+// per instruction, one k block ahead.  Needs K % 256 == 0 (rows of whole
+// lines); dynamic LDS 2 KB per line of the k range.
+__device__ __forceinline__ int int4_swz(int row) { return (row & 7) ^ (row >> 3); }
+
+template <int MB, bool LINES = false>
 __global__ __launch_bounds__(kDecWaves * 64) void k_gemv_int4_mfma(
     const float* __restrict__ A, const uint8_t* __restrict__ Wp, const float* __restrict__ scales,
     const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int gs,
@@ -669,6 +678,31 @@ __global__ __launch_bounds__(kDecWaves * 64) void k_gemv_int4_mfma(
     f64x4 acc[MB];
 #pragma unroll
     for (int i = 0; i < MB; i++) acc[i] = f64x4{0.0, 0.0, 0.0, 0.0};
+    // LINES: lines [p_lo, p_hi) of the k range (8 k blocks each); DMA d = 2
+    // (p - p_lo) + h holds rows 8 h .. 8 h + 7, lane 8 rr + q taking chunk
+    // q ^ int4_swz(8 h + rr); k block kb of row l16 is chunk kb & 7 of line
+    // kb / 8, its dword g the lane's 8 codes
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_wl[];
+    const int p_lo = lo >> 3;
+    if constexpr (LINES) {
+        const int nd = 2 * (((hi + 7) >> 3) - p_lo);
+        const int rr = lane >> 3, q = lane & 7;
+        for (int d = wave; d < nd; d += kDecWaves) {
+            const int row = 8 * (d & 1) + rr;
+            const int c = n0 + row < N ? n0 + row : N - 1;
+            const uint8_t* src = Wp + (int64_t)c * half + (int64_t)(p_lo + (d >> 1)) * 128 +
+                                 ((q ^ int4_swz(row)) << 4);
+            __builtin_amdgcn_global_load_lds((const void*)src,
+                                             (__attribute__((address_space(3))) void*)(s_wl + d * 1024),
+                                             16, 0, 0);
+        }
+        // every wave's DMAs have landed (vmcnt), then a raw barrier publishes
+        // them (__syncthreads() would also wait, being a release fence)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    const int wl_row = ((l16 >> 3) << 10) + ((l16 & 7) << 7) + 4 * g;
+    const int wl_swz = int4_swz(l16);
     // each k block's operands are loaded one block ahead, so their latency
     // overlaps the previous block's MFMAs
     float4 an[MB][2];
@@ -681,7 +715,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void k_gemv_int4_mfma(
             an[i][0] = p[0];
             an[i][1] = p[1];
         }
-        wn = *reinterpret_cast<const uint32_t*>(wrow + 16 * kb);
+        if constexpr (LINES)
+            wn = *reinterpret_cast<const uint32_t*>(s_wl + (((kb >> 3) - p_lo) << 11) + wl_row +
+                                                    (((kb & 7) ^ wl_swz) << 4));
+        else
+            wn = *reinterpret_cast<const uint32_t*>(wrow + 16 * kb);
         sn = srow[(32 * kb + 8 * g) / gs];
     };
     if (wlo < whi) fetch(wlo);
@@ -951,14 +989,27 @@ int launch_matmul_int4(Ctx* c, const float* a, const uint8_t* wp, const float* s
         if (splits > 1)
             TKV_RC_TRY(ctx_workspace(c, 12, (size_t)(ncb * splits) * mb * 256 * sizeof(double), &part));
         const unsigned grid = (unsigned)(ncb * splits);
-        if (mb == 1)
-            hipLaunchKernelGGL((k_gemv_int4_mfma<1>), dim3(grid), dim3(kDecWaves * 64), 0, c->stream, a,
-                               wp, scales, bias, y, (int)m, (int)n, (int)k, (int)gs, (int)splits,
-                               static_cast<double*>(part), c->gemv_arrivals);
-        else
-            hipLaunchKernelGGL((k_gemv_int4_mfma<2>), dim3(grid), dim3(kDecWaves * 64), 0, c->stream, a,
-                               wp, scales, bias, y, (int)m, (int)n, (int)k, (int)gs, (int)splits,
-                               static_cast<double*>(part), c->gemv_arrivals);
+        // Weight path (K % 256 == 0, 16-byte aligned codes; the context's
+        // decode weight-path knob forces either): lines through LDS for two
+        // row blocks without a K split, or K >= 2048.  Cold weights, one box,
+        // two rounds, registers -> lines: qkv / mlp_up M = 32 9.25 / 9.10 ->
+        // 8.76 / 8.64 us, mlp_down M = 16 / 32 9.50 / 11.10 -> 9.26 / 10.76;
+        // attn_out (split) and the one-block launches at K = 768 within
+        // +-0.1 us, mostly slower through LDS.
+        const int64_t knob = tuned(c, TKV_HIP_TUNE_DECODE_DMA);
+        const bool lines = k % 256 == 0 && aligned(wp, 16) &&
+                           (knob == 1 || (knob < 0 && ((mb == 2 && splits == 1) || k >= 2048)));
+        const unsigned lds = lines ? (unsigned)(2048 * (ceil_div(nkb, splits) / 8 + 2)) : 0u;
+#define TKV_I4DEC(MBV, L)                                                                          \
+    hipLaunchKernelGGL((k_gemv_int4_mfma<MBV, L>), dim3(grid), dim3(kDecWaves * 64), lds,           \
+                       c->stream, a, wp, scales, bias, y, (int)m, (int)n, (int)k, (int)gs,          \
+                       (int)splits, static_cast<double*>(part), c->gemv_arrivals)
+        if (mb == 1) {
+            if (lines) TKV_I4DEC(1, true); else TKV_I4DEC(1, false);
+        } else {
+            if (lines) TKV_I4DEC(2, true); else TKV_I4DEC(2, false);
+        }
+#undef TKV_I4DEC
         TKV_LAUNCH_CHECK();
         return TKV_HIP_OK;
     }
