@@ -1029,8 +1029,12 @@ static inline int pick_cfg(Ctx* c, int64_t m, int64_t n) {
     if (f >= 0) return (int)f;
     // Warp-specialised 128x192 tiles (cfg 2) measured best over the four
     // GPT-2 shapes at M = 8192 (warmed-up, interleaved medians); 64x128 tiles
-    // keep every CU busy when M is small.
-    return tiles_of<Cfg2>(m, n) >= c->num_cus ? 2 : 0;
+    // keep every CU busy when M is small.  The switch is at three quarters of
+    // the CUs: at M = 2048, qkv's 192 tiles ran 10.2 us with cfg 2 against
+    // 11.4 (FP8) / 12.5 (INT8) with cfg 0, while attn_out and mlp_down (64
+    // tiles) ran 6.2 / 13.8 us with cfg 0 against 8.9 / 19.1 (one box, two
+    // rounds, HIP events).
+    return tiles_of<Cfg2>(m, n) * 4 >= (int64_t)c->num_cus * 3 ? 2 : 0;
 }
 
 template <class C, class P, class E>
