@@ -401,8 +401,24 @@ def bench_decode(ctx, D, G, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
             cold = _time_us(ctx, D, lambda i: lins[i % nsets].forward(dx, m, dy, D.ACT_PER_TOKEN),
                             nsets)
             warm = _time_us(ctx, D, lambda i: base.forward(dx, m, dy, D.ACT_PER_TOKEN), 200)
+            # the same cold calls captured once into a HIP graph and replayed:
+            # per call without the host's launch path (a few us per Python
+            # call, more than the kernel on some hosts)
+            with D.Graph(ctx) as g:
+                for i in range(nsets):
+                    lins[i].forward(dx, m, dy, D.ACT_PER_TOKEN)
+            g.launch()
+            e0, e1 = D.Event(), D.Event()
+            ctx.synchronize()
+            e0.record(ctx)
+            g.launch()
+            e1.record(ctx)
+            ctx.synchronize()
+            graph = e0.elapsed_ms(e1) * 1e3 / nsets
+            g.close()
             nbytes = n * k + 8 * n + 4 * m * k + 4 * m * n
             out[f"{name}_m{m}"] = {"cold_us": round(cold, 2), "warm_us": round(warm, 2),
+                                   "graph_cold_us": round(graph, 2),
                                    "cold_GBps": round(nbytes / (cold * 1e-6) / 1e9, 1),
                                    "cold_frac_of_hbm": round(nbytes / (cold * 1e-6) / 1e9
                                                              / PEAK_HBM_GBPS, 3)}
@@ -413,6 +429,7 @@ def bench_decode(ctx, D, G, ms=(1, 4, 16, 32), cold_bytes=640 << 20):
         b.close()
     out["note"] = ("per call: per-token int8 quantize + INT8 GEMM + dequant/bias in one kernel; "
                    "us = HIP-event time per call over back-to-back calls (launch gaps included); "
+                   "graph_cold_us: the cold calls replayed from one captured HIP graph; "
                    "bytes = N*K int8 weights + 8N scales/bias + 4MK f32 x + 4MN f32 y; cold rotates "
                    f"{cold_bytes >> 20} MiB of distinct weight sets")
     return out
